@@ -1,0 +1,734 @@
+// C ABI of the gfx950 restricted head (include/marketforge_hip.h).
+//
+// Host-side validation mirrors the reference operators check for check and in
+// the same order (src/cuda/greedy.cu:237-414, src/cuda/rms_norm.cu:104-182,
+// src/cuda/linear.cu:40-81, src/cuda/device_buffer.cu:15-103), then launches.
+// Nothing here allocates device memory except mf_device_alloc itself, and
+// nothing synchronizes except mf_stream_synchronize.
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <initializer_list>
+#include <limits>
+
+#include <hip/hip_runtime.h>
+
+#include "marketforge_hip.h"
+#include "mf_device.hpp"
+#include "mf_launch.hpp"
+
+namespace {
+
+using mf::HeadArgs;
+using mf::ScoreSource;
+
+constexpr uint64_t kU64Max = std::numeric_limits<uint64_t>::max();
+constexpr uint64_t kU32Max = std::numeric_limits<uint32_t>::max();
+constexpr uint64_t kIntMax = static_cast<uint64_t>(std::numeric_limits<int>::max());
+
+mf_status status(int32_t code, uint32_t detail = 0) { return mf_status{code, detail}; }
+mf_status ok() { return status(MF_OK); }
+
+// src/cuda/cuda_internal.hpp:21-35
+mf_status runtime_status(hipError_t e) {
+  return e == hipSuccess ? ok() : status(MF_DEVICE_RUNTIME_FAILURE, static_cast<uint32_t>(e));
+}
+mf_status launch_status(hipError_t e) {
+  return e == hipSuccess ? ok() : status(MF_DEVICE_BACKEND_FAILURE, static_cast<uint32_t>(e));
+}
+
+hipStream_t native(uintptr_t stream) { return reinterpret_cast<hipStream_t>(stream); }
+
+template <typename T>
+T* ptr(uintptr_t address) {
+  return reinterpret_cast<T*>(address);
+}
+
+bool checked_mul(uint64_t a, uint64_t b, uint64_t& out) {
+  if (a != 0 && b > kU64Max / a) return false;
+  out = a * b;
+  return true;
+}
+
+// Every address valid (non-zero) and pairwise distinct (greedy.cu:214-233).
+bool distinct_valid(std::initializer_list<uintptr_t> addresses) {
+  for (auto i = addresses.begin(); i != addresses.end(); ++i) {
+    if (*i == 0) return false;
+    for (auto j = i + 1; j != addresses.end(); ++j) {
+      if (*i == *j) return false;
+    }
+  }
+  return true;
+}
+
+uint64_t align256(uint64_t v) { return (v + 255u) & ~uint64_t{255u}; }
+
+// gamma_n = n u / (1 - n u) (Higham): bound on the relative error of an
+// n-term floating-point dot product in any evaluation order.
+double gamma(double n, double u) { return n * u / (1.0 - n * u); }
+
+// Fast FP32 dot vs reference order, both within gamma_H * sum|y e| of the
+// exact value; the computed sum|y e| is at most (1 - gamma_H) low.  Factor 2
+// of safety plus 16 u so the window test's own roundings stay inside.
+float dot_bound_coef(uint64_t H) {
+  const double g = gamma(static_cast<double>(H), std::ldexp(1.0, -24));
+  return static_cast<float>(4.0 * g / (1.0 - g) + std::ldexp(1.0, -20));
+}
+
+// MFMA score (hi + lo split of y, exact FP16 products, 2H FP32 additions with
+// up to one ulp each) vs reference order, bounded through ||y|| ||e||:
+//   |g - r| <= (gamma_H + 1.001 gamma'_2H + 2^-22) ||y|| ||e||
+//              + 2^-25 sqrt(H) ||e||        (FP16 residual of small y)
+// doubled for safety.
+void mfma_bound_coefs(uint64_t H, float& coef, float& coef2) {
+  const double h = static_cast<double>(H);
+  const double c = gamma(h, std::ldexp(1.0, -24)) + 1.001 * gamma(2.0 * h, std::ldexp(1.0, -23)) +
+                   std::ldexp(1.0, -22);
+  coef = static_cast<float>(2.0 * c + std::ldexp(1.0, -20));
+  coef2 = static_cast<float>(2.0 * std::ldexp(1.0, -25) * std::sqrt(h));
+}
+
+// Absolute term for underflow: each of up to 2H operations may lose 2^-126.
+float underflow_slack(uint64_t H) {
+  return static_cast<float>(4.0 * static_cast<double>(H) * std::ldexp(1.0, -126));
+}
+
+uint32_t head_chunk(uint64_t H, uint64_t max_count) {
+  uint32_t c = H == 576 ? 128u : 64u;
+  while (c < mf::kHeadChunkMax &&
+         (max_count + c - 1) / c > mf::kHeadMaxRecords) {
+    c *= 2;
+  }
+  return c;
+}
+
+}  // namespace
+
+extern "C" {
+
+uint32_t mf_abi_version(void) { return MF_ABI_VERSION; }
+
+mf_status mf_device_count(int32_t* count) {
+  if (count == nullptr) return status(MF_INVALID_ARGUMENT);
+  int n = 0;
+  const hipError_t e = hipGetDeviceCount(&n);
+  *count = e == hipSuccess ? n : 0;
+  return runtime_status(e);
+}
+
+// ---------------------------------------------------------------- plumbing --
+
+mf_status mf_device_alloc(uint64_t bytes, uintptr_t* address) {
+  if (address == nullptr) return status(MF_INVALID_ARGUMENT);
+  *address = 0;
+  if (bytes == 0) return ok();
+  if (bytes > std::numeric_limits<size_t>::max()) return status(MF_ARITHMETIC_OVERFLOW);
+  void* p = nullptr;
+  const hipError_t e = hipMalloc(&p, static_cast<size_t>(bytes));
+  if (e != hipSuccess) return runtime_status(e);
+  *address = reinterpret_cast<uintptr_t>(p);
+  return ok();
+}
+
+mf_status mf_device_free(uintptr_t address) {
+  if (address == 0) return ok();
+  return runtime_status(hipFree(ptr<void>(address)));
+}
+
+// src/cuda/device_buffer.cu:15-33 (validate_copy)
+static mf_status validate_copy(const void* host, uint64_t bytes, uint64_t offset,
+                               uint64_t size, uintptr_t stream) {
+  if (stream == 0 || (bytes != 0 && host == nullptr)) return status(MF_INVALID_ARGUMENT);
+  if (offset > kU64Max - bytes) return status(MF_ARITHMETIC_OVERFLOW);
+  if (offset + bytes > size) return status(MF_INVALID_ARGUMENT);
+  if (bytes > std::numeric_limits<size_t>::max()) return status(MF_ARITHMETIC_OVERFLOW);
+  return ok();
+}
+
+mf_status mf_copy_to_device_async(mf_buffer destination, uint64_t offset, const void* source,
+                                  uint64_t bytes, uintptr_t stream) {
+  const mf_status v = validate_copy(source, bytes, offset, destination.bytes, stream);
+  if (v.code != MF_OK || bytes == 0) return v;
+  return runtime_status(hipMemcpyAsync(ptr<char>(destination.address) + offset, source,
+                                       static_cast<size_t>(bytes), hipMemcpyHostToDevice,
+                                       native(stream)));
+}
+
+mf_status mf_copy_to_host_async(void* destination, mf_buffer source, uint64_t offset,
+                                uint64_t bytes, uintptr_t stream) {
+  const mf_status v = validate_copy(destination, bytes, offset, source.bytes, stream);
+  if (v.code != MF_OK || bytes == 0) return v;
+  return runtime_status(hipMemcpyAsync(destination, ptr<const char>(source.address) + offset,
+                                       static_cast<size_t>(bytes), hipMemcpyDeviceToHost,
+                                       native(stream)));
+}
+
+mf_status mf_stream_create(uintptr_t* stream) {
+  if (stream == nullptr) return status(MF_INVALID_ARGUMENT);
+  *stream = 0;
+  hipStream_t s = nullptr;
+  const hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+  if (e != hipSuccess) return runtime_status(e);
+  *stream = reinterpret_cast<uintptr_t>(s);
+  return ok();
+}
+
+mf_status mf_stream_destroy(uintptr_t stream) {
+  if (stream == 0) return ok();
+  return runtime_status(hipStreamDestroy(native(stream)));
+}
+
+mf_status mf_stream_synchronize(uintptr_t stream) {
+  if (stream == 0) return status(MF_INVALID_ARGUMENT);
+  return runtime_status(hipStreamSynchronize(native(stream)));
+}
+
+// --------------------------------------------------------------- RMSNorm ----
+
+// src/cuda/rms_norm.cu:104-141 (FP32) and :143-182 (FP16) check order.
+static mf_status rms_norm(mf_buffer input, mf_buffer weight, mf_buffer output, uint64_t rows,
+                          uint64_t hidden, float epsilon, uintptr_t stream, bool half) {
+  if (rows == 0 || hidden == 0 || !std::isfinite(epsilon) || epsilon <= 0.0f || stream == 0) {
+    return status(MF_INVALID_ARGUMENT);
+  }
+  const uint64_t esize = half ? 2u : 4u;
+  uint64_t elements = 0, tensor_bytes = 0, weight_bytes = 0;
+  if (!checked_mul(rows, hidden, elements) || !checked_mul(elements, esize, tensor_bytes) ||
+      !checked_mul(hidden, esize, weight_bytes)) {
+    return status(MF_ARITHMETIC_OVERFLOW);
+  }
+  if (input.bytes != tensor_bytes || output.bytes != tensor_bytes ||
+      weight.bytes != weight_bytes || input.address == 0 || output.address == 0 ||
+      weight.address == 0 || weight.address == input.address ||
+      weight.address == output.address) {
+    return status(MF_INVALID_ARGUMENT);
+  }
+  if (rows > kIntMax) return status(MF_RESOURCE_LIMIT);
+  // this build stages one row in LDS: hidden <= 16384
+  if (hidden > 16384) return status(MF_RESOURCE_LIMIT);
+  return launch_status(mf::launch_rms_norm(
+      ptr<const void>(input.address), half, ptr<const void>(weight.address), half,
+      ptr<void>(output.address), half, nullptr, static_cast<uint32_t>(rows),
+      static_cast<uint32_t>(hidden), epsilon, native(stream)));
+}
+
+mf_status mf_rms_norm_f32(mf_buffer input, mf_buffer weight, mf_buffer output, uint64_t rows,
+                          uint64_t hidden_size, float epsilon, uintptr_t stream) {
+  return rms_norm(input, weight, output, rows, hidden_size, epsilon, stream, false);
+}
+
+mf_status mf_rms_norm_f16(mf_buffer input, mf_buffer weight, mf_buffer output, uint64_t rows,
+                          uint64_t hidden_size, float epsilon, uintptr_t stream) {
+  return rms_norm(input, weight, output, rows, hidden_size, epsilon, stream, true);
+}
+
+// ---------------------------------------------------------------- greedy ----
+
+// src/cuda/greedy.cu:237-279
+static mf_status greedy(mf_buffer logits, mf_buffer token_ids, uint64_t rows, uint64_t vocab,
+                        uintptr_t stream, bool half) {
+  if (rows == 0 || vocab == 0 || stream == 0) return status(MF_INVALID_ARGUMENT);
+  if (vocab > kU32Max) return status(MF_RESOURCE_LIMIT);
+  if (rows > kIntMax) return status(MF_RESOURCE_LIMIT);
+  if (rows > kU64Max / vocab) return status(MF_ARITHMETIC_OVERFLOW);
+  const uint64_t elements = rows * vocab;
+  const uint64_t esize = half ? 2u : 4u;
+  if (elements > kU64Max / esize || rows > kU64Max / 4u) return status(MF_ARITHMETIC_OVERFLOW);
+  if (logits.bytes != elements * esize || token_ids.bytes != rows * 4u || logits.address == 0 ||
+      token_ids.address == 0 || logits.address == token_ids.address) {
+    return status(MF_INVALID_ARGUMENT);
+  }
+  return launch_status(mf::launch_greedy(ptr<const void>(logits.address), half,
+                                         ptr<uint32_t>(token_ids.address),
+                                         static_cast<uint32_t>(rows),
+                                         static_cast<uint32_t>(vocab), native(stream)));
+}
+
+mf_status mf_greedy_select_f16(mf_buffer logits, mf_buffer token_ids, uint64_t rows,
+                               uint64_t vocabulary_size, uintptr_t stream) {
+  return greedy(logits, token_ids, rows, vocabulary_size, stream, true);
+}
+
+mf_status mf_greedy_select_f32(mf_buffer logits, mf_buffer token_ids, uint64_t rows,
+                               uint64_t vocabulary_size, uintptr_t stream) {
+  return greedy(logits, token_ids, rows, vocabulary_size, stream, false);
+}
+
+// src/cuda/greedy.cu:281-347
+static mf_status restricted_greedy(mf_buffer logits, mf_buffer allowed, mf_buffer counts,
+                                   mf_buffer token_ids, uint64_t rows, uint64_t vocab,
+                                   uint64_t max_allowed, uintptr_t stream, bool half) {
+  if (rows == 0 || vocab == 0 || max_allowed == 0 || stream == 0) {
+    return status(MF_INVALID_ARGUMENT);
+  }
+  if (vocab > kU32Max || max_allowed > kU32Max || rows > kIntMax) {
+    return status(MF_RESOURCE_LIMIT);
+  }
+  if (rows > kU64Max / vocab || rows > kU64Max / max_allowed) {
+    return status(MF_ARITHMETIC_OVERFLOW);
+  }
+  const uint64_t logit_elements = rows * vocab;
+  const uint64_t allowed_elements = rows * max_allowed;
+  const uint64_t esize = half ? 2u : 4u;
+  if (logit_elements > kU64Max / esize || allowed_elements > kU64Max / 4u ||
+      rows > kU64Max / 4u) {
+    return status(MF_ARITHMETIC_OVERFLOW);
+  }
+  if (logits.bytes != logit_elements * esize || allowed.bytes != allowed_elements * 4u ||
+      counts.bytes != rows * 4u || token_ids.bytes != rows * 4u ||
+      !distinct_valid({logits.address, allowed.address, counts.address, token_ids.address})) {
+    return status(MF_INVALID_ARGUMENT);
+  }
+  return launch_status(mf::launch_restricted_greedy(
+      ptr<const void>(logits.address), half, ptr<const uint32_t>(allowed.address),
+      ptr<const uint32_t>(counts.address), ptr<uint32_t>(token_ids.address),
+      static_cast<uint32_t>(rows), static_cast<uint32_t>(vocab),
+      static_cast<uint32_t>(max_allowed), native(stream)));
+}
+
+mf_status mf_restricted_greedy_select_f16(mf_buffer logits, mf_buffer allowed_token_ids,
+                                          mf_buffer allowed_token_counts, mf_buffer token_ids,
+                                          uint64_t rows, uint64_t vocabulary_size,
+                                          uint64_t maximum_allowed_tokens, uintptr_t stream) {
+  return restricted_greedy(logits, allowed_token_ids, allowed_token_counts, token_ids, rows,
+                           vocabulary_size, maximum_allowed_tokens, stream, true);
+}
+
+mf_status mf_restricted_greedy_select_f32(mf_buffer logits, mf_buffer allowed_token_ids,
+                                          mf_buffer allowed_token_counts, mf_buffer token_ids,
+                                          uint64_t rows, uint64_t vocabulary_size,
+                                          uint64_t maximum_allowed_tokens, uintptr_t stream) {
+  return restricted_greedy(logits, allowed_token_ids, allowed_token_counts, token_ids, rows,
+                           vocabulary_size, maximum_allowed_tokens, stream, false);
+}
+
+// ------------------------------------------------------- restricted head ----
+
+// src/cuda/greedy.cu:349-414
+mf_status mf_restricted_output_head_f16(mf_buffer hidden, mf_buffer embedding,
+                                        mf_buffer allowed_token_ids,
+                                        mf_buffer allowed_token_counts, mf_buffer token_ids,
+                                        uint64_t rows, uint64_t hidden_size,
+                                        uint64_t vocabulary_size,
+                                        uint64_t maximum_allowed_tokens, uintptr_t stream) {
+  if (rows == 0 || hidden_size == 0 || vocabulary_size == 0 || maximum_allowed_tokens == 0 ||
+      stream == 0) {
+    return status(MF_INVALID_ARGUMENT);
+  }
+  if (vocabulary_size > kU32Max || maximum_allowed_tokens > kU32Max || rows > kIntMax) {
+    return status(MF_RESOURCE_LIMIT);
+  }
+  if (rows > kU64Max / hidden_size || vocabulary_size > kU64Max / hidden_size ||
+      rows > kU64Max / maximum_allowed_tokens) {
+    return status(MF_ARITHMETIC_OVERFLOW);
+  }
+  const uint64_t hidden_elements = rows * hidden_size;
+  const uint64_t embedding_elements = vocabulary_size * hidden_size;
+  const uint64_t allowed_elements = rows * maximum_allowed_tokens;
+  if (hidden_elements > kU64Max / 2u || embedding_elements > kU64Max / 2u ||
+      allowed_elements > kU64Max / 4u || rows > kU64Max / 4u) {
+    return status(MF_ARITHMETIC_OVERFLOW);
+  }
+  if (hidden.bytes != hidden_elements * 2u || embedding.bytes != embedding_elements * 2u ||
+      allowed_token_ids.bytes != allowed_elements * 4u ||
+      allowed_token_counts.bytes != rows * 4u || token_ids.bytes != rows * 4u ||
+      !distinct_valid({hidden.address, embedding.address, allowed_token_ids.address,
+                       allowed_token_counts.address, token_ids.address})) {
+    return status(MF_INVALID_ARGUMENT);
+  }
+  // limits of this build: one workgroup per row stages the row in LDS and
+  // keeps at most 256 block records
+  if (hidden_size > mf::kHeadMaxHidden ||
+      maximum_allowed_tokens > static_cast<uint64_t>(mf::kHeadChunkMax) * mf::kHeadMaxRecords) {
+    return status(MF_RESOURCE_LIMIT);
+  }
+  HeadArgs a{};
+  a.hidden16 = ptr<const uint16_t>(hidden.address);
+  a.emb = ptr<const uint16_t>(embedding.address);
+  a.fixed_ids = ptr<const uint32_t>(allowed_token_ids.address);
+  a.fixed_counts = ptr<const uint32_t>(allowed_token_counts.address);
+  a.out_token = ptr<uint32_t>(token_ids.address);
+  a.rows = static_cast<uint32_t>(rows);
+  a.H = static_cast<uint32_t>(hidden_size);
+  a.V = static_cast<uint32_t>(vocabulary_size);
+  a.max_allowed = static_cast<uint32_t>(maximum_allowed_tokens);
+  a.chunk = head_chunk(hidden_size, maximum_allowed_tokens);
+  a.max_chunks = 0;  // one workgroup per row, no workspace
+  a.coef = dot_bound_coef(hidden_size);
+  a.slack = underflow_slack(hidden_size);
+  a.order = MF_ORDER_FMA_CHAIN;  // greedy.cu:171-176
+  return launch_status(mf::launch_head(ScoreSource::kDotF16Hidden, a, 0, native(stream)));
+}
+
+// ------------------------------------------------------------------ linear ---
+
+// src/cuda/linear.cu:40-81 (the handle check has no counterpart here)
+mf_status mf_linear_f16(mf_buffer input, mf_buffer weight, mf_buffer output, uint64_t rows,
+                        uint64_t input_features, uint64_t output_features, uintptr_t stream) {
+  if (stream == 0) return status(MF_INVALID_ARGUMENT);
+  auto matrix_bytes = [](uint64_t r, uint64_t c, uint64_t& bytes) -> mf_status {
+    if (r == 0 || c == 0) return status(MF_INVALID_ARGUMENT);
+    if (r > kU64Max / c) return status(MF_ARITHMETIC_OVERFLOW);
+    const uint64_t e = r * c;
+    if (e > kU64Max / 2u) return status(MF_ARITHMETIC_OVERFLOW);
+    bytes = e * 2u;
+    return ok();
+  };
+  uint64_t ib = 0, wb = 0, ob = 0;
+  mf_status s = matrix_bytes(rows, input_features, ib);
+  if (s.code != MF_OK) return s;
+  s = matrix_bytes(output_features, input_features, wb);
+  if (s.code != MF_OK) return s;
+  s = matrix_bytes(rows, output_features, ob);
+  if (s.code != MF_OK) return s;
+  if (rows > kIntMax || input_features > kIntMax || output_features > kIntMax) {
+    return status(MF_RESOURCE_LIMIT);
+  }
+  if (input.bytes != ib || weight.bytes != wb || output.bytes != ob || input.address == 0 ||
+      weight.address == 0 || output.address == 0 || input.address == weight.address ||
+      input.address == output.address || weight.address == output.address) {
+    return status(MF_INVALID_ARGUMENT);
+  }
+  const bool mfma_shape = (input_features % 16u) == 0 && (input.address % 16u) == 0 &&
+                          (weight.address % 16u) == 0 && output_features <= kU32Max &&
+                          rows <= kU32Max;
+  if (mfma_shape) {
+    mf::ProjArgs p{};
+    p.a16 = ptr<const uint16_t>(input.address);
+    p.m = static_cast<uint32_t>(rows);
+    p.rows = static_cast<uint32_t>(rows);
+    p.emb = ptr<const uint16_t>(weight.address);
+    p.H = static_cast<uint32_t>(input_features);
+    p.V = static_cast<uint32_t>(output_features);
+    p.out_f16 = ptr<uint16_t>(output.address);
+    return launch_status(mf::launch_projection(p, native(stream)));
+  }
+  return launch_status(mf::launch_linear_f16_simple(
+      ptr<const uint16_t>(input.address), ptr<const uint16_t>(weight.address),
+      ptr<uint16_t>(output.address), static_cast<uint32_t>(rows),
+      static_cast<uint32_t>(input_features), static_cast<uint32_t>(output_features),
+      native(stream)));
+}
+
+// ------------------------------------------------------------ decode tail ----
+
+namespace {
+
+struct TailLayout {
+  uint64_t y, row_norm, chunks_per_row, prefix, start_row, plan_counter, head_counters,
+      head_records, fb_counters, fb_records, scores, tok_norm, total;
+  uint32_t chunk, max_chunks, groups, tiles;
+};
+
+bool buffer_is(const mf_buffer& b, uint64_t bytes) { return b.address != 0 && b.bytes == bytes; }
+bool optional_is(const mf_buffer& b, uint64_t bytes) {
+  return b.address == 0 || b.bytes == bytes;
+}
+
+// Validation common to both decode-tail entry points; fills the layout.
+mf_status validate_tail(const mf_decode_tail_args* a, bool full, TailLayout& L) {
+  if (a == nullptr) return status(MF_INVALID_ARGUMENT);
+  if (a->rows == 0 || a->hidden == 0 || a->vocab == 0 || a->states == 0 ||
+      (a->order != MF_ORDER_FMA_CHAIN && a->order != MF_ORDER_MUL_ADD_CHAIN) ||
+      (a->norm_weight.address != 0 && (!std::isfinite(a->epsilon) || a->epsilon <= 0.0f))) {
+    return status(MF_INVALID_ARGUMENT);
+  }
+  if (a->vocab > kU32Max || a->states >= kU32Max - 1 || a->nnz > kU32Max ||
+      a->rows > kIntMax || a->unrestricted_count > a->rows) {
+    return status(MF_RESOURCE_LIMIT);
+  }
+  if (a->hidden > mf::kHeadMaxHidden || a->max_count > a->vocab ||
+      a->max_count > static_cast<uint64_t>(mf::kHeadChunkMax) * mf::kHeadMaxRecords ||
+      a->rows > 65535u) {
+    return status(MF_RESOURCE_LIMIT);
+  }
+  uint64_t xe = 0, ee = 0, te = 0;
+  if (!checked_mul(a->rows, a->hidden, xe) || !checked_mul(a->vocab, a->hidden, ee) ||
+      !checked_mul(a->states, a->vocab, te) || xe > kU64Max / 4u || ee > kU64Max / 2u ||
+      te > kU64Max / 4u) {
+    return status(MF_ARITHMETIC_OVERFLOW);
+  }
+  if (!buffer_is(a->x, xe * 4u) || !buffer_is(a->embedding, ee * 2u) ||
+      !optional_is(a->norm_weight, a->hidden * 4u) || !buffer_is(a->row_state, a->rows * 4u) ||
+      !buffer_is(a->state_offsets, (a->states + 1) * 4u) ||
+      !(a->nnz == 0 || buffer_is(a->state_tokens, a->nnz * 4u)) ||
+      !optional_is(a->state_next, a->nnz * 4u) || !optional_is(a->next_table, te * 4u) ||
+      (a->state_next.address != 0 && a->next_table.address != 0) ||
+      !buffer_is(a->out_token, a->rows * 4u) || !optional_is(a->out_score, a->rows * 4u) ||
+      !optional_is(a->out_next_state, a->rows * 4u) ||
+      (a->unrestricted_count > 0 &&
+       !buffer_is(a->unrestricted_rows, a->unrestricted_count * 4u))) {
+    return status(MF_INVALID_ARGUMENT);
+  }
+  // outputs must not alias each other or any input
+  const uintptr_t outs[3] = {a->out_token.address, a->out_score.address,
+                             a->out_next_state.address};
+  const uintptr_t ins[11] = {a->x.address, a->embedding.address, a->norm_weight.address,
+                             a->row_state.address, a->state_offsets.address,
+                             a->state_tokens.address, a->state_next.address,
+                             a->next_table.address, a->unrestricted_rows.address,
+                             a->workspace.address, 0};
+  for (int i = 0; i < 3; ++i) {
+    if (outs[i] == 0) continue;
+    for (int j = 0; j < 3; ++j) {
+      if (j != i && outs[j] == outs[i]) return status(MF_INVALID_ARGUMENT);
+    }
+    for (uintptr_t in : ins) {
+      if (in != 0 && in == outs[i]) return status(MF_INVALID_ARGUMENT);
+    }
+  }
+  if ((a->embedding.address % 16u) != 0 || (a->x.address % 16u) != 0) {
+    return status(MF_INVALID_ARGUMENT);
+  }
+  const uint64_t rows = a->rows;
+  L.chunk = head_chunk(a->hidden, a->max_count);
+  L.max_chunks = static_cast<uint32_t>(
+      a->max_count == 0 ? 1 : (a->max_count + L.chunk - 1) / L.chunk);
+  uint64_t g = rows * L.max_chunks;
+  L.groups = static_cast<uint32_t>(g < 2048 ? g : 2048);
+  L.tiles = mf::fallback_tiles(static_cast<uint32_t>(a->vocab));
+  uint64_t off = 0;
+  auto take = [&off](uint64_t bytes) {
+    const uint64_t at = off;
+    off = align256(off + bytes);
+    return at;
+  };
+  L.y = take(xe * 4u);
+  L.row_norm = take(rows * 4u);
+  L.chunks_per_row = take(rows * 4u);
+  L.prefix = take((rows + 1) * 4u);
+  L.start_row = take(static_cast<uint64_t>(L.groups) * 4u);
+  L.plan_counter = take(4u);
+  L.head_counters = take(rows * 4u);
+  if (full) {
+    // the selection over projected scores reads 4 bytes per candidate: one
+    // chunk of kHeadChunkMax ids per workgroup; unrestricted rows take V ids
+    const uint64_t longest = a->max_count > a->vocab ? a->max_count : a->vocab;
+    if (longest > static_cast<uint64_t>(mf::kHeadChunkMax) * mf::kHeadMaxRecords) {
+      return status(MF_RESOURCE_LIMIT);
+    }
+    L.chunk = mf::kHeadChunkMax;
+    L.max_chunks = static_cast<uint32_t>((longest + L.chunk - 1) / L.chunk);
+  }
+  L.head_records = take(rows * L.max_chunks * sizeof(mf::Record));
+  const uint64_t fb_rows = full ? 0 : a->unrestricted_count;
+  L.fb_counters = take(((fb_rows + 31) / 32 + 1) * 4u);
+  L.fb_records = take(fb_rows * L.tiles * sizeof(mf::Record));
+  L.scores = full ? take(rows * a->vocab * 4u) : off;
+  L.tok_norm = full ? take(a->vocab * 4u) : off;
+  L.total = off;
+  return ok();
+}
+
+mf_status check_workspace(const mf_decode_tail_args* a, const TailLayout& L) {
+  if (a->workspace.address == 0 || a->workspace.bytes < L.total ||
+      (a->workspace.address % 256u) != 0) {
+    return status(MF_INVALID_ARGUMENT);
+  }
+  return ok();
+}
+
+}  // namespace
+
+mf_status mf_decode_tail_workspace_bytes(const mf_decode_tail_args* args, uint64_t* bytes) {
+  if (bytes == nullptr) return status(MF_INVALID_ARGUMENT);
+  TailLayout L{};
+  const mf_status v = validate_tail(args, false, L);
+  if (v.code != MF_OK) return v;
+  *bytes = L.total;
+  return ok();
+}
+
+mf_status mf_decode_tail_full_workspace_bytes(const mf_decode_tail_args* args, uint64_t* bytes) {
+  if (bytes == nullptr) return status(MF_INVALID_ARGUMENT);
+  TailLayout L{};
+  const mf_status v = validate_tail(args, true, L);
+  if (v.code != MF_OK) return v;
+  *bytes = L.total;
+  return ok();
+}
+
+mf_status mf_workspace_init(mf_buffer workspace, uintptr_t stream) {
+  if (workspace.address == 0 || stream == 0 || (workspace.address % 16u) != 0) {
+    return status(MF_INVALID_ARGUMENT);
+  }
+  return launch_status(mf::launch_fill_zero(ptr<void>(workspace.address),
+                                            workspace.bytes & ~uint64_t{15u}, native(stream)));
+}
+
+static void fill_head_common(const mf_decode_tail_args* a, const TailLayout& L, char* ws,
+                             HeadArgs& h) {
+  h.y = reinterpret_cast<const float*>(ws + L.y);
+  h.emb = ptr<const uint16_t>(a->embedding.address);
+  h.row_state = ptr<const uint32_t>(a->row_state.address);
+  h.offsets = ptr<const uint32_t>(a->state_offsets.address);
+  h.tokens = ptr<const uint32_t>(a->state_tokens.address);
+  h.state_next = ptr<const uint32_t>(a->state_next.address);
+  h.next_table = ptr<const int32_t>(a->next_table.address);
+  h.out_token = ptr<uint32_t>(a->out_token.address);
+  h.out_score = ptr<float>(a->out_score.address);
+  h.out_next = ptr<uint32_t>(a->out_next_state.address);
+  h.records = reinterpret_cast<mf::Record*>(ws + L.head_records);
+  h.counters = reinterpret_cast<uint32_t*>(ws + L.head_counters);
+  h.rows = static_cast<uint32_t>(a->rows);
+  h.H = static_cast<uint32_t>(a->hidden);
+  h.V = static_cast<uint32_t>(a->vocab);
+  h.states = static_cast<uint32_t>(a->states);
+  h.nnz = static_cast<uint32_t>(a->nnz);
+  h.chunk = L.chunk;
+  h.max_chunks = L.max_chunks;
+  h.order = a->order;
+}
+
+static mf::PlanArgs plan_args(const mf_decode_tail_args* a, const TailLayout& L, char* ws) {
+  mf::PlanArgs p{};
+  p.row_state = ptr<const uint32_t>(a->row_state.address);
+  p.offsets = ptr<const uint32_t>(a->state_offsets.address);
+  p.states = static_cast<uint32_t>(a->states);
+  p.nnz = static_cast<uint32_t>(a->nnz);
+  p.max_chunks = L.max_chunks;
+  p.chunk = L.chunk;
+  p.head_groups = L.groups;
+  p.chunks_per_row = reinterpret_cast<uint32_t*>(ws + L.chunks_per_row);
+  p.prefix = reinterpret_cast<uint32_t*>(ws + L.prefix);
+  p.start_row = reinterpret_cast<uint32_t*>(ws + L.start_row);
+  p.counter = reinterpret_cast<uint32_t*>(ws + L.plan_counter);
+  p.out_token = ptr<uint32_t>(a->out_token.address);
+  p.out_score = ptr<float>(a->out_score.address);
+  p.out_next = ptr<uint32_t>(a->out_next_state.address);
+  return p;
+}
+
+enum class Stage { kPrepare, kRestricted, kUnrestricted };
+
+static mf_status decode_tail_stage(const mf_decode_tail_args* args, uintptr_t stream,
+                                   Stage stage) {
+  if (stream == 0) return status(MF_INVALID_ARGUMENT);
+  TailLayout L{};
+  mf_status v = validate_tail(args, false, L);
+  if (v.code != MF_OK) return v;
+  v = check_workspace(args, L);
+  if (v.code != MF_OK) return v;
+  const mf_decode_tail_args* a = args;
+  char* ws = ptr<char>(a->workspace.address);
+  const hipStream_t s = native(stream);
+  float* y = reinterpret_cast<float*>(ws + L.y);
+  float* row_norm = reinterpret_cast<float*>(ws + L.row_norm);
+  const mf::PlanArgs plan = plan_args(a, L, ws);
+  hipError_t e = hipSuccess;
+  switch (stage) {
+    case Stage::kPrepare:
+      // final RMSNorm + work plan
+      e = mf::launch_norm_plan(ptr<const float>(a->x.address),
+                               ptr<const float>(a->norm_weight.address), y, row_norm,
+                               static_cast<uint32_t>(a->rows), static_cast<uint32_t>(a->hidden),
+                               a->epsilon, plan, s);
+      break;
+    case Stage::kRestricted: {
+      // restricted rows: CSR gather head
+      HeadArgs h{};
+      fill_head_common(a, L, ws, h);
+      h.coef = dot_bound_coef(a->hidden);
+      h.slack = underflow_slack(a->hidden);
+      h.prefix = plan.prefix;
+      h.start_row = plan.start_row;
+      e = mf::launch_head(ScoreSource::kDotF32, h, L.groups, s);
+      break;
+    }
+    case Stage::kUnrestricted: {
+      // unrestricted rows: MFMA full-vocabulary head
+      if (a->unrestricted_count == 0) break;
+      mf::FallbackArgs f{};
+      f.y = y;
+      f.row_index = ptr<const uint32_t>(a->unrestricted_rows.address);
+      f.m = static_cast<uint32_t>(a->unrestricted_count);
+      f.rows = static_cast<uint32_t>(a->rows);
+      f.row_norm = row_norm;
+      f.emb = ptr<const uint16_t>(a->embedding.address);
+      f.H = static_cast<uint32_t>(a->hidden);
+      f.V = static_cast<uint32_t>(a->vocab);
+      f.records = reinterpret_cast<mf::Record*>(ws + L.fb_records);
+      f.counters = reinterpret_cast<uint32_t*>(ws + L.fb_counters);
+      f.out_token = ptr<uint32_t>(a->out_token.address);
+      f.out_score = ptr<float>(a->out_score.address);
+      f.out_next = ptr<uint32_t>(a->out_next_state.address);
+      mfma_bound_coefs(a->hidden, f.coef, f.coef2);
+      f.slack = underflow_slack(a->hidden);
+      f.order = a->order;
+      e = mf::launch_fallback(f, s);
+      break;
+    }
+  }
+  return launch_status(e);
+}
+
+mf_status mf_decode_tail_prepare(const mf_decode_tail_args* args, uintptr_t stream) {
+  return decode_tail_stage(args, stream, Stage::kPrepare);
+}
+
+mf_status mf_decode_tail_restricted(const mf_decode_tail_args* args, uintptr_t stream) {
+  return decode_tail_stage(args, stream, Stage::kRestricted);
+}
+
+mf_status mf_decode_tail_unrestricted(const mf_decode_tail_args* args, uintptr_t stream) {
+  return decode_tail_stage(args, stream, Stage::kUnrestricted);
+}
+
+mf_status mf_decode_tail_f16(const mf_decode_tail_args* args, uintptr_t stream) {
+  for (Stage st : {Stage::kPrepare, Stage::kRestricted, Stage::kUnrestricted}) {
+    const mf_status v = decode_tail_stage(args, stream, st);
+    if (v.code != MF_OK) return v;
+  }
+  return ok();
+}
+
+mf_status mf_decode_tail_full_f16(const mf_decode_tail_args* args, uintptr_t stream) {
+  if (stream == 0) return status(MF_INVALID_ARGUMENT);
+  TailLayout L{};
+  mf_status v = validate_tail(args, true, L);
+  if (v.code != MF_OK) return v;
+  v = check_workspace(args, L);
+  if (v.code != MF_OK) return v;
+  const mf_decode_tail_args* a = args;
+  char* ws = ptr<char>(a->workspace.address);
+  const hipStream_t s = native(stream);
+  float* y = reinterpret_cast<float*>(ws + L.y);
+  float* row_norm = reinterpret_cast<float*>(ws + L.row_norm);
+  float* scores = reinterpret_cast<float*>(ws + L.scores);
+  float* tok_norm = reinterpret_cast<float*>(ws + L.tok_norm);
+
+  // 1. final RMSNorm (the plan's outputs are unused here)
+  const mf::PlanArgs plan = plan_args(a, L, ws);
+  hipError_t e = mf::launch_norm_plan(ptr<const float>(a->x.address),
+                                      ptr<const float>(a->norm_weight.address), y, row_norm,
+                                      static_cast<uint32_t>(a->rows),
+                                      static_cast<uint32_t>(a->hidden), a->epsilon, plan, s);
+  if (e != hipSuccess) return launch_status(e);
+
+  // 2. full output projection of every row: FP32 scores [rows, V]
+  mf::ProjArgs p{};
+  p.y = y;
+  p.m = static_cast<uint32_t>(a->rows);
+  p.rows = static_cast<uint32_t>(a->rows);
+  p.emb = ptr<const uint16_t>(a->embedding.address);
+  p.H = static_cast<uint32_t>(a->hidden);
+  p.V = static_cast<uint32_t>(a->vocab);
+  p.out_f32 = scores;
+  p.tok_norm = tok_norm;
+  e = mf::launch_projection(p, s);
+  if (e != hipSuccess) return launch_status(e);
+
+  // 3. restricted selection over the scores (unrestricted rows: all ids)
+  HeadArgs h{};
+  fill_head_common(a, L, ws, h);
+  h.scores = scores;
+  h.row_norm = row_norm;
+  h.tok_norm = tok_norm;
+  mfma_bound_coefs(a->hidden, h.coef, h.coef2);
+  h.slack = underflow_slack(a->hidden);
+  h.lookup_unrestricted = 1;
+  e = mf::launch_head(ScoreSource::kLookup, h, 0, s);
+  return launch_status(e);
+}
+
+}  // extern "C"

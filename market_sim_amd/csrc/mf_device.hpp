@@ -1,0 +1,245 @@
+// Device-side building blocks shared by the gfx950 kernels.
+//
+// Exactness scheme used by every scoring kernel:
+//   1. a fast pass computes each candidate score g in a parallel order
+//      (lane-split FP32 FMA + cross-lane reduction, or MFMA) together with a
+//      rigorous bound b >= |g - r|, where r is the score in the reference's
+//      sequential order (greedy.cu:171-176 or operators.cpp:584-595);
+//   2. only candidates whose interval [g - b, g + b] reaches the best lower
+//      bound can be the reference winner; those are rescored in the
+//      reference order (canonical_dot) and compared with the reference rule.
+// The chosen token and its reported score are therefore the reference's
+// bit for bit, while the bulk of the work runs in the fast order.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mf {
+
+constexpr uint32_t kInvalidToken = 0xFFFFFFFFu;
+constexpr uint32_t kStateUnrestricted = 0xFFFFFFFEu;
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float half_to_float(uint16_t bits) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, bits));
+}
+
+__device__ __forceinline__ uint16_t float_to_half_rne(float v) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
+}
+
+// IEEE round-to-nearest square root and quotient of binary32 values.
+//
+// The hardware square root is faithful only (within one ulp), so the result
+// is corrected exactly: for a positive finite candidate c with neighbours
+// lo < c < hi, the midpoints (c + lo) / 2 and (c + hi) / 2 have at most 25
+// significant bits, so their squares (and their products with a binary32
+// divisor) are exact in binary64.  Comparing x against them decides the
+// correctly rounded result; a square root or quotient of binary32 values is
+// never exactly a midpoint, so no tie rule is needed.
+__device__ __forceinline__ float next_up(float c) {
+  return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, c) + 1u);
+}
+__device__ __forceinline__ float next_down(float c) {
+  return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, c) - 1u);
+}
+
+__device__ __forceinline__ float sqrt_rn(float x) {
+  float c = __builtin_sqrtf(x);
+  if (!(x > 0.0f) || !__builtin_isfinite(x)) return c;  // 0, -0, <0, inf, NaN
+  const double xd = x;
+  for (int it = 0; it < 3; ++it) {
+    const float lo = next_down(c);
+    const float hi = next_up(c);
+    const double mlo = (static_cast<double>(c) + lo) * 0.5;
+    const double mhi = (static_cast<double>(c) + hi) * 0.5;
+    if (xd < mlo * mlo) {
+      c = lo;
+    } else if (xd > mhi * mhi) {
+      c = hi;
+    } else {
+      break;
+    }
+  }
+  return c;
+}
+
+// a / b for positive finite a, b whose quotient is a positive normal float
+// (the RMSNorm uses: sum / H and 1 / sqrt); other inputs take the compiler's
+// IEEE division sequence.
+__device__ __forceinline__ float div_rn(float a, float b) {
+  float q = __fdiv_rn(a, b);
+  if (!(a > 0.0f) || !(b > 0.0f) || !__builtin_isfinite(a) || !__builtin_isfinite(b) ||
+      !(q >= 0x1p-126f) || !(q < 0x1p127f)) {
+    return q;
+  }
+  const double ad = a;
+  const double bd = b;
+  for (int it = 0; it < 3; ++it) {
+    const float lo = next_down(q);
+    const float hi = next_up(q);
+    const double mlo = (static_cast<double>(q) + lo) * 0.5;
+    const double mhi = (static_cast<double>(q) + hi) * 0.5;
+    if (ad < mlo * bd) {
+      q = lo;
+    } else if (ad > mhi * bd) {
+      q = hi;
+    } else {
+      break;
+    }
+  }
+  return q;
+}
+
+// One step of a reference summation order.  The file is compiled with
+// -ffp-contract=off, so the MUL_ADD form keeps its two roundings.
+template <bool kMulAdd>
+__device__ __forceinline__ float order_step(float s, float h, float e) {
+  if constexpr (kMulAdd) {
+    const float p = h * e;
+    return s + p;
+  } else {
+    return __builtin_fmaf(h, e, s);
+  }
+}
+
+// Score of one embedding row in a reference order, f = 0..H-1 ascending.
+// y: FP32 hidden (LDS or global); row: FP16 embedding row (global).  When the
+// row is 16-byte aligned and H % 8 == 0 the loads are 16-byte vectors; the
+// arithmetic order is identical either way.
+template <bool kMulAdd>
+__device__ float canonical_dot(const float* y, const uint16_t* row, uint32_t H) {
+  float s = 0.0f;
+  uint32_t f = 0;
+  if ((reinterpret_cast<uintptr_t>(row) & 15u) == 0 && (H & 7u) == 0) {
+    const uint4* v = reinterpret_cast<const uint4*>(row);
+#pragma unroll 4
+    for (uint32_t i = 0; i < H / 8; ++i) {
+      const uint4 q = v[i];
+      const uint16_t* h = reinterpret_cast<const uint16_t*>(&q);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        s = order_step<kMulAdd>(s, y[i * 8 + k], half_to_float(h[k]));
+      }
+    }
+    f = H;
+  }
+  for (; f < H; ++f) {
+    s = order_step<kMulAdd>(s, y[f], half_to_float(row[f]));
+  }
+  return s;
+}
+
+__device__ __forceinline__ float canonical_dot_order(int order, const float* y,
+                                                     const uint16_t* row,
+                                                     uint32_t H) {
+  return order == 1 ? canonical_dot<true>(y, row, H)
+                    : canonical_dot<false>(y, row, H);
+}
+
+// The reference selection order (greedy.cu:96-100): higher score wins, equal
+// scores go to the lower id, NaN never wins.  The identity element is
+// (-inf, kInvalidToken); a NaN candidate is mapped to the identity before any
+// reduction, so partial results are never NaN and the combine is a total
+// order (associative and commutative).
+struct Best {
+  float score;
+  uint32_t token;
+  uint32_t pos;
+};
+
+__device__ __forceinline__ Best best_identity() {
+  return Best{-__builtin_huge_valf(), kInvalidToken, 0u};
+}
+
+__device__ __forceinline__ bool better(float s1, uint32_t t1, float s2,
+                                       uint32_t t2) {
+  return s1 > s2 || (s1 == s2 && t1 < t2);
+}
+
+__device__ __forceinline__ Best best_of(Best a, Best b) {
+  return better(b.score, b.token, a.score, a.token) ? b : a;
+}
+
+__device__ __forceinline__ Best best_leaf(float score, uint32_t token,
+                                          uint32_t pos) {
+  return score != score ? best_identity() : Best{score, token, pos};
+}
+
+__device__ __forceinline__ Best wave_best(Best b) {
+#pragma unroll
+  for (int m = kWave / 2; m > 0; m >>= 1) {
+    Best o;
+    o.score = __shfl_xor(b.score, m);
+    o.token = __shfl_xor(b.token, m);
+    o.pos = __shfl_xor(b.pos, m);
+    b = best_of(b, o);
+  }
+  return b;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int m = kWave / 2; m > 0; m >>= 1) {
+    v = __builtin_fmaxf(v, __shfl_xor(v, m));
+  }
+  return v;
+}
+
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
+#pragma unroll
+  for (int m = kWave / 2; m > 0; m >>= 1) {
+    v += __shfl_xor(v, m);
+  }
+  return v;
+}
+
+// (token, pos) with the lowest token; used for the all-NaN fallback rule.
+__device__ __forceinline__ void wave_min_token(uint32_t& token, uint32_t& pos) {
+#pragma unroll
+  for (int m = kWave / 2; m > 0; m >>= 1) {
+    const uint32_t t = __shfl_xor(token, m);
+    const uint32_t p = __shfl_xor(pos, m);
+    if (t < token) {
+      token = t;
+      pos = p;
+    }
+  }
+}
+
+// Summary of one block of candidates, produced by one workgroup pass and
+// merged per row (in LDS when one workgroup owns the row, otherwise through
+// global memory by the last workgroup to finish the row).
+enum : uint32_t {
+  kRecFast = 1u,    // one window member: fast score value, interval [lower, upper]
+  kRecExact = 2u,   // best reference-order score of the block: value
+  kRecAllNan = 4u,  // every reference-order score was NaN
+  kRecInvalid = 8u, // an id >= vocabulary was seen: the whole row is invalid
+};
+
+struct alignas(16) Record {
+  float lower;
+  float upper;
+  float value;
+  uint32_t token;
+  uint32_t pos;
+  uint32_t kind;
+  uint32_t min_token;
+  uint32_t min_pos;
+};
+
+__device__ __forceinline__ uint32_t atomic_arrive(uint32_t* counter) {
+  return __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL,
+                                __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void acquire_agent() {
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+}
+
+__device__ __forceinline__ void release_agent() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+}
+
+} // namespace mf

@@ -1,0 +1,146 @@
+"""CPU checks of the C ABI: the library loads without a GPU, exports every
+function the header declares, and rejects invalid metadata before any device
+call (the reference's *_rejects_invalid_metadata tests, cuda_tests.cu)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from market_sim_amd import abi
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+FAKE_STREAM = 0x1000
+
+
+def declared_functions():
+    text = open(os.path.join(ROOT, "include", "marketforge_hip.h")).read()
+    return sorted(set(re.findall(r"^\s*(?:mf_status|uint32_t)\s+(mf_\w+)\(", text, re.M)))
+
+
+def test_header_declarations_match_binding():
+    assert declared_functions() == sorted(abi.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = abi.lib()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    assert lib.mf_abi_version() == 1
+
+
+def b(addr, n):
+    return abi.Buffer(addr, n)
+
+
+def test_greedy_rejects_invalid_metadata_before_launch():
+    """cuda_tests.cu:1137-1167."""
+    l = abi.lib()
+    logits, tokens = b(0x10000, 16), b(0x20000, 4)
+    assert l.mf_greedy_select_f16(logits, tokens, 0, 8, FAKE_STREAM).code == abi.MF_INVALID_ARGUMENT
+    assert l.mf_greedy_select_f16(logits, tokens, 1, 8, 0).code == abi.MF_INVALID_ARGUMENT
+    assert l.mf_greedy_select_f16(logits, tokens, 1, 7, FAKE_STREAM).code == abi.MF_INVALID_ARGUMENT
+    assert l.mf_greedy_select_f16(logits, tokens, 1, 2 ** 32, FAKE_STREAM).code == abi.MF_RESOURCE_LIMIT
+    assert l.mf_greedy_select_f16(logits, logits, 1, 8, FAKE_STREAM).code == abi.MF_INVALID_ARGUMENT
+
+
+def test_restricted_greedy_rejects_invalid_metadata():
+    """cuda_tests.cu:1256-1276."""
+    l = abi.lib()
+    logits, allowed, counts, out = b(0x10000, 16), b(0x20000, 16), b(0x30000, 4), b(0x40000, 4)
+    f = l.mf_restricted_greedy_select_f16
+    assert f(logits, allowed, counts, out, 1, 8, 0, FAKE_STREAM).code == abi.MF_INVALID_ARGUMENT
+    assert f(logits, allowed, counts, out, 1, 8, 3, FAKE_STREAM).code == abi.MF_INVALID_ARGUMENT
+    assert f(logits, allowed, counts, counts, 1, 8, 4, FAKE_STREAM).code == abi.MF_INVALID_ARGUMENT
+
+
+def test_restricted_output_head_rejects_invalid_metadata():
+    """cuda_tests.cu:1283-1339."""
+    l = abi.lib()
+    rows, hidden, vocab, mx = 1, 4, 8, 2
+    h, e = b(0x10000, rows * hidden * 2), b(0x20000, vocab * hidden * 2)
+    a, c, o = b(0x30000, rows * mx * 4), b(0x40000, rows * 4), b(0x50000, rows * 4)
+    f = l.mf_restricted_output_head_f16
+    assert f(h, e, a, c, o, 0, hidden, vocab, mx, FAKE_STREAM).code == abi.MF_INVALID_ARGUMENT
+    assert f(h, e, a, c, o, rows, hidden, vocab, 0, FAKE_STREAM).code == abi.MF_INVALID_ARGUMENT
+    assert f(h, e, a, c, o, rows, hidden, vocab, mx, 0).code == abi.MF_INVALID_ARGUMENT
+    assert f(h, e, a, c, c, rows, hidden, vocab, mx, FAKE_STREAM).code == abi.MF_INVALID_ARGUMENT
+    assert f(h, e, a, c, o, 2 ** 64 - 1, hidden, vocab, mx, FAKE_STREAM).code == abi.MF_RESOURCE_LIMIT
+
+
+def test_rms_norm_rejects_invalid_metadata_before_launch():
+    """cuda_tests.cu:914-945."""
+    l = abi.lib()
+    x, w, y = b(0x10000, 32), b(0x20000, 16), b(0x30000, 32)
+    f = l.mf_rms_norm_f32
+    assert f(x, w, y, 0, 4, 1e-5, FAKE_STREAM).code == abi.MF_INVALID_ARGUMENT
+    assert f(x, w, y, 2, 4, float("nan"), FAKE_STREAM).code == abi.MF_INVALID_ARGUMENT
+    assert f(x, w, y, 2, 4, 1e-5, 0).code == abi.MF_INVALID_ARGUMENT
+    assert f(x, w, y, 1, 4, 1e-5, FAKE_STREAM).code == abi.MF_INVALID_ARGUMENT
+    assert f(x, x, y, 2, 4, 1e-5, FAKE_STREAM).code == abi.MF_INVALID_ARGUMENT
+
+
+def test_linear_rejects_invalid_metadata():
+    l = abi.lib()
+    f = l.mf_linear_f16
+    x, w, y = b(0x10000, 12), b(0x20000, 12), b(0x30000, 8)
+    assert f(x, w, y, 2, 3, 2, 0).code == abi.MF_INVALID_ARGUMENT
+    assert f(x, w, y, 0, 3, 2, FAKE_STREAM).code == abi.MF_INVALID_ARGUMENT
+    assert f(x, w, y, 2 ** 62, 3, 2, FAKE_STREAM).code == abi.MF_ARITHMETIC_OVERFLOW
+    assert f(x, x, y, 2, 3, 2, FAKE_STREAM).code == abi.MF_INVALID_ARGUMENT
+
+
+def test_copy_validation():
+    """src/cuda/device_buffer.cu:15-33."""
+    l = abi.lib()
+    buf = b(0x10000, 16)
+    host = ctypes.create_string_buffer(32)
+    assert l.mf_copy_to_device_async(buf, 0, host, 8, 0).code == abi.MF_INVALID_ARGUMENT
+    assert l.mf_copy_to_device_async(buf, 0, None, 8, FAKE_STREAM).code == abi.MF_INVALID_ARGUMENT
+    assert l.mf_copy_to_device_async(buf, 12, host, 8, FAKE_STREAM).code == abi.MF_INVALID_ARGUMENT
+    assert l.mf_copy_to_device_async(buf, 2 ** 64 - 4, host, 8, FAKE_STREAM).code == abi.MF_ARITHMETIC_OVERFLOW
+
+
+def _tail_args(**over):
+    rows, hidden, vocab, states, nnz = 4, 576, 1000, 4, 40
+    a = abi.DecodeTailArgs()
+    a.x = b(0x100000, rows * hidden * 4)
+    a.norm_weight = b(0x200000, hidden * 4)
+    a.epsilon = 1e-5
+    a.order = 0
+    a.embedding = b(0x300000, vocab * hidden * 2)
+    a.row_state = b(0x400000, rows * 4)
+    a.state_offsets = b(0x500000, (states + 1) * 4)
+    a.state_tokens = b(0x600000, nnz * 4)
+    a.out_token = b(0x700000, rows * 4)
+    a.out_score = b(0x800000, rows * 4)
+    a.workspace = b(0x900000, 1 << 24)
+    a.rows, a.hidden, a.vocab, a.states, a.nnz, a.max_count = rows, hidden, vocab, states, nnz, 10
+    for k, v in over.items():
+        setattr(a, k, v)
+    return a
+
+
+def test_decode_tail_validation():
+    l = abi.lib()
+    n = ctypes.c_uint64()
+    a = _tail_args()
+    assert l.mf_decode_tail_workspace_bytes(ctypes.byref(a), ctypes.byref(n)).code == abi.MF_OK
+    assert n.value > 4 * 576 * 4
+    assert l.mf_decode_tail_f16(ctypes.byref(a), 0).code == abi.MF_INVALID_ARGUMENT
+    bad = _tail_args(rows=0)
+    assert l.mf_decode_tail_f16(ctypes.byref(bad), FAKE_STREAM).code == abi.MF_INVALID_ARGUMENT
+    bad = _tail_args(order=7)
+    assert l.mf_decode_tail_f16(ctypes.byref(bad), FAKE_STREAM).code == abi.MF_INVALID_ARGUMENT
+    bad = _tail_args(out_score=b(0x700000, 16))  # aliases out_token
+    assert l.mf_decode_tail_f16(ctypes.byref(bad), FAKE_STREAM).code == abi.MF_INVALID_ARGUMENT
+    bad = _tail_args(out_token=b(0x100000, 16))  # aliases x
+    assert l.mf_decode_tail_f16(ctypes.byref(bad), FAKE_STREAM).code == abi.MF_INVALID_ARGUMENT
+    bad = _tail_args(x=b(0x100000, 12))  # wrong size
+    assert l.mf_decode_tail_f16(ctypes.byref(bad), FAKE_STREAM).code == abi.MF_INVALID_ARGUMENT
+    bad = _tail_args(workspace=b(0x900000, 64))  # too small
+    assert l.mf_decode_tail_f16(ctypes.byref(bad), FAKE_STREAM).code == abi.MF_INVALID_ARGUMENT
+    bad = _tail_args(max_count=5000)  # longer than the vocabulary
+    assert l.mf_decode_tail_f16(ctypes.byref(bad), FAKE_STREAM).code == abi.MF_RESOURCE_LIMIT
+    bad = _tail_args(unrestricted_count=2)  # rows list missing
+    assert l.mf_decode_tail_f16(ctypes.byref(bad), FAKE_STREAM).code == abi.MF_INVALID_ARGUMENT
