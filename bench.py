@@ -74,7 +74,8 @@ def time_loop(tail, stages, steps, warmup, copies):
     from market_sim_amd import abi, ops
 
     fns = {"prepare": ops.decode_tail_prepare, "restricted": ops.decode_tail_restricted,
-           "unrestricted": ops.decode_tail_unrestricted, "full": ops.decode_tail_full_f16,
+           "unrestricted": ops.decode_tail_unrestricted,
+           "finalize": ops.decode_tail_finalize, "full": ops.decode_tail_full_f16,
            "tail": ops.decode_tail_f16}
     args = [tail.args(i % copies) for i in range(copies)]
     s = tail.stream
@@ -175,7 +176,7 @@ def main() -> int:
     w = workloads.config(args.config, seed=0)
     alg = algorithmic_bytes(w)
     tail = DeviceTail(w, copies=args.copies)
-    total_ms, wall_ms, st = time_loop(tail, ["prepare", "restricted", "unrestricted"],
+    total_ms, wall_ms, st = time_loop(tail, ["prepare", "restricted", "unrestricted", "finalize"],
                                       args.steps, args.warmup, args.copies)
     # correctness of what was timed: the last step's outputs vs the oracle on
     # a row sample is checked in tests; here record a token checksum
@@ -201,7 +202,7 @@ def main() -> int:
                    "unrestricted_rows": alg["B_u"], "candidates": alg["N"],
                    "distinct_ids": alg["U"], "table_copies": args.copies,
                    "order": "fma chain (greedy.cu:171-176)"},
-        "roofline": {"kernel": "head_planned_kernel (CSR gather)", "bound": "hbm",
+        "roofline": {"kernel": "gather_kernel (CSR gather)", "bound": "hbm",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "bytes_per_launch": alg["gather"], "avg_launch_us": round(gather_ms * 1e3, 2)},

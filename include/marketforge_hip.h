@@ -224,15 +224,19 @@ mf_status mf_decode_tail_f16(const mf_decode_tail_args* args, uintptr_t stream);
 
 /* Stages of mf_decode_tail_f16 for callers that schedule them separately
  * (e.g. the unrestricted stage on a second stream once prepare is done).
- * prepare:      final RMSNorm into the workspace + the gather work plan;
- *               writes the outputs of invalid rows.
- * restricted:   CSR gather head of the restricted rows (needs prepare).
- * unrestricted: MFMA full-vocabulary head of unrestricted_rows (needs
- *               prepare; runs after restricted when both share a stream). */
+ * prepare:      final RMSNorm into the workspace, per-row metadata, the FP16
+ *               split of unrestricted rows; presets invalid rows' outputs.
+ * restricted:   CSR gather of the restricted rows into tile records.
+ * unrestricted: MFMA full-vocabulary head of unrestricted_rows into tile
+ *               records.
+ * finalize:     per row, merges the records, rescores the surviving
+ *               candidates in the reference order, writes the outputs.
+ * restricted and unrestricted need prepare; finalize needs both. */
 mf_status mf_decode_tail_prepare(const mf_decode_tail_args* args, uintptr_t stream);
 mf_status mf_decode_tail_restricted(const mf_decode_tail_args* args, uintptr_t stream);
 mf_status mf_decode_tail_unrestricted(const mf_decode_tail_args* args,
                                       uintptr_t stream);
+mf_status mf_decode_tail_finalize(const mf_decode_tail_args* args, uintptr_t stream);
 
 /* The full-output-projection comparator for the same contract: an MFMA
  * projection of every row over the whole vocabulary into FP32 scores, then

@@ -88,6 +88,7 @@ SIGNATURES = {
     "mf_decode_tail_prepare": (Status, [ctypes.POINTER(DecodeTailArgs), _UP]),
     "mf_decode_tail_restricted": (Status, [ctypes.POINTER(DecodeTailArgs), _UP]),
     "mf_decode_tail_unrestricted": (Status, [ctypes.POINTER(DecodeTailArgs), _UP]),
+    "mf_decode_tail_finalize": (Status, [ctypes.POINTER(DecodeTailArgs), _UP]),
     "mf_decode_tail_full_workspace_bytes": (
         Status, [ctypes.POINTER(DecodeTailArgs), ctypes.POINTER(_U64)]),
     "mf_decode_tail_full_f16": (Status, [ctypes.POINTER(DecodeTailArgs), _UP]),

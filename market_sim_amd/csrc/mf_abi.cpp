@@ -353,11 +353,10 @@ mf_status mf_restricted_output_head_f16(mf_buffer hidden, mf_buffer embedding,
   a.V = static_cast<uint32_t>(vocabulary_size);
   a.max_allowed = static_cast<uint32_t>(maximum_allowed_tokens);
   a.chunk = head_chunk(hidden_size, maximum_allowed_tokens);
-  a.max_chunks = 0;  // one workgroup per row, no workspace
   a.coef = dot_bound_coef(hidden_size);
   a.slack = underflow_slack(hidden_size);
   a.order = MF_ORDER_FMA_CHAIN;  // greedy.cu:171-176
-  return launch_status(mf::launch_head(ScoreSource::kDotF16Hidden, a, 0, native(stream)));
+  return launch_status(mf::launch_head(a, native(stream)));
 }
 
 // ------------------------------------------------------------------ linear ---
@@ -414,16 +413,20 @@ mf_status mf_linear_f16(mf_buffer input, mf_buffer weight, mf_buffer output, uin
 
 namespace {
 
+constexpr uint32_t kFullTile = 256;  // selection over projected scores
+
 struct TailLayout {
-  uint64_t y, row_norm, chunks_per_row, prefix, start_row, plan_counter, head_counters,
-      head_records, fb_counters, fb_records, scores, tok_norm, total;
-  uint32_t chunk, max_chunks, groups, tiles;
+  uint64_t y, row_norm, row_meta, y_hi, y_lo, fb_map, records, fb_records, scores, tok_norm,
+      total;
+  uint32_t tile, max_tiles, fb_tiles;
 };
 
 bool buffer_is(const mf_buffer& b, uint64_t bytes) { return b.address != 0 && b.bytes == bytes; }
 bool optional_is(const mf_buffer& b, uint64_t bytes) {
   return b.address == 0 || b.bytes == bytes;
 }
+
+uint32_t gather_tile(uint64_t H) { return H == 2048 ? 128u : 64u; }
 
 // Validation common to both decode-tail entry points; fills the layout.
 mf_status validate_tail(const mf_decode_tail_args* a, bool full, TailLayout& L) {
@@ -437,8 +440,9 @@ mf_status validate_tail(const mf_decode_tail_args* a, bool full, TailLayout& L) 
       a->rows > kIntMax || a->unrestricted_count > a->rows) {
     return status(MF_RESOURCE_LIMIT);
   }
-  if (a->hidden > mf::kHeadMaxHidden || a->max_count > a->vocab ||
-      a->max_count > static_cast<uint64_t>(mf::kHeadChunkMax) * mf::kHeadMaxRecords ||
+  // limits of this build: the hidden row is staged in LDS (H <= 8192, and
+  // H % 16 == 0 for the MFMA K split), lists are at most the vocabulary
+  if (a->hidden > mf::kHeadMaxHidden || (a->hidden % 16u) != 0 || a->max_count > a->vocab ||
       a->rows > 65535u) {
     return status(MF_RESOURCE_LIMIT);
   }
@@ -463,11 +467,11 @@ mf_status validate_tail(const mf_decode_tail_args* a, bool full, TailLayout& L) 
   // outputs must not alias each other or any input
   const uintptr_t outs[3] = {a->out_token.address, a->out_score.address,
                              a->out_next_state.address};
-  const uintptr_t ins[11] = {a->x.address, a->embedding.address, a->norm_weight.address,
+  const uintptr_t ins[10] = {a->x.address, a->embedding.address, a->norm_weight.address,
                              a->row_state.address, a->state_offsets.address,
                              a->state_tokens.address, a->state_next.address,
                              a->next_table.address, a->unrestricted_rows.address,
-                             a->workspace.address, 0};
+                             a->workspace.address};
   for (int i = 0; i < 3; ++i) {
     if (outs[i] == 0) continue;
     for (int j = 0; j < 3; ++j) {
@@ -481,12 +485,17 @@ mf_status validate_tail(const mf_decode_tail_args* a, bool full, TailLayout& L) 
     return status(MF_INVALID_ARGUMENT);
   }
   const uint64_t rows = a->rows;
-  L.chunk = head_chunk(a->hidden, a->max_count);
-  L.max_chunks = static_cast<uint32_t>(
-      a->max_count == 0 ? 1 : (a->max_count + L.chunk - 1) / L.chunk);
-  uint64_t g = rows * L.max_chunks;
-  L.groups = static_cast<uint32_t>(g < 2048 ? g : 2048);
-  L.tiles = mf::fallback_tiles(static_cast<uint32_t>(a->vocab));
+  if (full) {
+    // unrestricted rows take the whole vocabulary as their list
+    const uint64_t longest = a->max_count > a->vocab ? a->max_count : a->vocab;
+    L.tile = kFullTile;
+    L.max_tiles = static_cast<uint32_t>((longest + L.tile - 1) / L.tile);
+  } else {
+    L.tile = gather_tile(a->hidden);
+    L.max_tiles = static_cast<uint32_t>(a->max_count == 0 ? 1 : (a->max_count + L.tile - 1) / L.tile);
+  }
+  L.fb_tiles = mf::fallback_tiles(static_cast<uint32_t>(a->vocab));
+  const uint64_t fb_rows = full ? 0 : a->unrestricted_count;
   uint64_t off = 0;
   auto take = [&off](uint64_t bytes) {
     const uint64_t at = off;
@@ -495,27 +504,14 @@ mf_status validate_tail(const mf_decode_tail_args* a, bool full, TailLayout& L) 
   };
   L.y = take(xe * 4u);
   L.row_norm = take(rows * 4u);
-  L.chunks_per_row = take(rows * 4u);
-  L.prefix = take((rows + 1) * 4u);
-  L.start_row = take(static_cast<uint64_t>(L.groups) * 4u);
-  L.plan_counter = take(4u);
-  L.head_counters = take(rows * 4u);
-  if (full) {
-    // the selection over projected scores reads 4 bytes per candidate: one
-    // chunk of kHeadChunkMax ids per workgroup; unrestricted rows take V ids
-    const uint64_t longest = a->max_count > a->vocab ? a->max_count : a->vocab;
-    if (longest > static_cast<uint64_t>(mf::kHeadChunkMax) * mf::kHeadMaxRecords) {
-      return status(MF_RESOURCE_LIMIT);
-    }
-    L.chunk = mf::kHeadChunkMax;
-    L.max_chunks = static_cast<uint32_t>((longest + L.chunk - 1) / L.chunk);
-  }
-  L.head_records = take(rows * L.max_chunks * sizeof(mf::Record));
-  const uint64_t fb_rows = full ? 0 : a->unrestricted_count;
-  L.fb_counters = take(((fb_rows + 31) / 32 + 1) * 4u);
-  L.fb_records = take(fb_rows * L.tiles * sizeof(mf::Record));
-  L.scores = full ? take(rows * a->vocab * 4u) : off;
-  L.tok_norm = full ? take(a->vocab * 4u) : off;
+  L.row_meta = take(rows * sizeof(mf::RowMeta));
+  L.y_hi = take(fb_rows > 0 ? xe * 2u : 0u);
+  L.y_lo = take(fb_rows > 0 ? xe * 2u : 0u);
+  L.fb_map = take(rows * 4u);
+  L.records = take(rows * L.max_tiles * sizeof(mf::TileRecord));
+  L.fb_records = take(fb_rows * L.fb_tiles * sizeof(mf::TileRecord));
+  L.scores = take(full ? rows * a->vocab * 4u : 0u);
+  L.tok_norm = take(full ? a->vocab * 4u : 0u);
   L.total = off;
   return ok();
 }
@@ -526,6 +522,125 @@ mf_status check_workspace(const mf_decode_tail_args* a, const TailLayout& L) {
     return status(MF_INVALID_ARGUMENT);
   }
   return ok();
+}
+
+enum class Stage { kPrepare, kRestricted, kUnrestricted, kFinalize };
+
+mf::TailNormArgs norm_args(const mf_decode_tail_args* a, const TailLayout& L, char* ws,
+                           bool split) {
+  mf::TailNormArgs n{};
+  n.x = ptr<const float>(a->x.address);
+  n.weight = ptr<const float>(a->norm_weight.address);
+  n.epsilon = a->epsilon;
+  n.y = reinterpret_cast<float*>(ws + L.y);
+  n.row_norm = reinterpret_cast<float*>(ws + L.row_norm);
+  n.y_hi = split ? reinterpret_cast<uint16_t*>(ws + L.y_hi) : nullptr;
+  n.y_lo = split ? reinterpret_cast<uint16_t*>(ws + L.y_lo) : nullptr;
+  n.row_state = ptr<const uint32_t>(a->row_state.address);
+  n.offsets = ptr<const uint32_t>(a->state_offsets.address);
+  n.states = static_cast<uint32_t>(a->states);
+  n.nnz = static_cast<uint32_t>(a->nnz);
+  n.max_count = static_cast<uint32_t>(a->max_count);
+  n.V = static_cast<uint32_t>(a->vocab);
+  n.H = static_cast<uint32_t>(a->hidden);
+  n.row_meta = reinterpret_cast<mf::RowMeta*>(ws + L.row_meta);
+  n.fb_map = reinterpret_cast<uint32_t*>(ws + L.fb_map);
+  n.out_token = ptr<uint32_t>(a->out_token.address);
+  n.out_score = ptr<float>(a->out_score.address);
+  n.out_next = ptr<uint32_t>(a->out_next_state.address);
+  return n;
+}
+
+mf::GatherArgs gather_args(const mf_decode_tail_args* a, const TailLayout& L, char* ws) {
+  mf::GatherArgs g{};
+  g.y = reinterpret_cast<const float*>(ws + L.y);
+  g.emb = ptr<const uint16_t>(a->embedding.address);
+  g.tokens = ptr<const uint32_t>(a->state_tokens.address);
+  g.row_meta = reinterpret_cast<const mf::RowMeta*>(ws + L.row_meta);
+  g.records = reinterpret_cast<mf::TileRecord*>(ws + L.records);
+  g.rows = static_cast<uint32_t>(a->rows);
+  g.H = static_cast<uint32_t>(a->hidden);
+  g.V = static_cast<uint32_t>(a->vocab);
+  g.tile = L.tile;
+  g.max_tiles = L.max_tiles;
+  g.slack = underflow_slack(a->hidden);
+  return g;
+}
+
+mf::FinalizeArgs finalize_args(const mf_decode_tail_args* a, const TailLayout& L, char* ws,
+                               bool full) {
+  mf::FinalizeArgs f{};
+  f.y = reinterpret_cast<const float*>(ws + L.y);
+  f.emb = ptr<const uint16_t>(a->embedding.address);
+  f.tokens = ptr<const uint32_t>(a->state_tokens.address);
+  f.row_meta = reinterpret_cast<const mf::RowMeta*>(ws + L.row_meta);
+  f.records = reinterpret_cast<const mf::TileRecord*>(ws + L.records);
+  f.max_tiles = L.max_tiles;
+  f.tile = L.tile;
+  if (!full && a->unrestricted_count > 0) {
+    f.fb_records = reinterpret_cast<const mf::TileRecord*>(ws + L.fb_records);
+    f.fb_map = reinterpret_cast<const uint32_t*>(ws + L.fb_map);
+    f.fb_tiles = L.fb_tiles;
+  }
+  f.lookup_unrestricted = full ? 1 : 0;
+  f.state_next = ptr<const uint32_t>(a->state_next.address);
+  f.next_table = ptr<const int32_t>(a->next_table.address);
+  f.out_token = ptr<uint32_t>(a->out_token.address);
+  f.out_score = ptr<float>(a->out_score.address);
+  f.out_next = ptr<uint32_t>(a->out_next_state.address);
+  f.rows = static_cast<uint32_t>(a->rows);
+  f.H = static_cast<uint32_t>(a->hidden);
+  f.V = static_cast<uint32_t>(a->vocab);
+  f.order = a->order;
+  return f;
+}
+
+mf_status decode_tail_stage(const mf_decode_tail_args* args, uintptr_t stream, Stage stage) {
+  if (stream == 0) return status(MF_INVALID_ARGUMENT);
+  TailLayout L{};
+  mf_status v = validate_tail(args, false, L);
+  if (v.code != MF_OK) return v;
+  v = check_workspace(args, L);
+  if (v.code != MF_OK) return v;
+  const mf_decode_tail_args* a = args;
+  char* ws = ptr<char>(a->workspace.address);
+  const hipStream_t s = native(stream);
+  hipError_t e = hipSuccess;
+  switch (stage) {
+    case Stage::kPrepare:
+      e = mf::launch_tail_norm(norm_args(a, L, ws, a->unrestricted_count > 0),
+                               static_cast<uint32_t>(a->rows), s);
+      break;
+    case Stage::kRestricted: {
+      mf::GatherArgs g = gather_args(a, L, ws);
+      g.coef = dot_bound_coef(a->hidden);
+      e = mf::launch_gather(ScoreSource::kDotF32, g, s);
+      break;
+    }
+    case Stage::kUnrestricted: {
+      if (a->unrestricted_count == 0) break;
+      mf::FallbackArgs f{};
+      f.y_hi = reinterpret_cast<const uint16_t*>(ws + L.y_hi);
+      f.y_lo = reinterpret_cast<const uint16_t*>(ws + L.y_lo);
+      f.row_index = ptr<const uint32_t>(a->unrestricted_rows.address);
+      f.m = static_cast<uint32_t>(a->unrestricted_count);
+      f.rows = static_cast<uint32_t>(a->rows);
+      f.row_norm = reinterpret_cast<const float*>(ws + L.row_norm);
+      f.emb = ptr<const uint16_t>(a->embedding.address);
+      f.H = static_cast<uint32_t>(a->hidden);
+      f.V = static_cast<uint32_t>(a->vocab);
+      f.records = reinterpret_cast<mf::TileRecord*>(ws + L.fb_records);
+      f.fb_map = reinterpret_cast<uint32_t*>(ws + L.fb_map);
+      mfma_bound_coefs(a->hidden, f.coef, f.coef2);
+      f.slack = underflow_slack(a->hidden);
+      e = mf::launch_fallback(f, s);
+      break;
+    }
+    case Stage::kFinalize:
+      e = mf::launch_finalize(finalize_args(a, L, ws, false), s);
+      break;
+  }
+  return launch_status(e);
 }
 
 }  // namespace
@@ -556,112 +671,6 @@ mf_status mf_workspace_init(mf_buffer workspace, uintptr_t stream) {
                                             workspace.bytes & ~uint64_t{15u}, native(stream)));
 }
 
-static void fill_head_common(const mf_decode_tail_args* a, const TailLayout& L, char* ws,
-                             HeadArgs& h) {
-  h.y = reinterpret_cast<const float*>(ws + L.y);
-  h.emb = ptr<const uint16_t>(a->embedding.address);
-  h.row_state = ptr<const uint32_t>(a->row_state.address);
-  h.offsets = ptr<const uint32_t>(a->state_offsets.address);
-  h.tokens = ptr<const uint32_t>(a->state_tokens.address);
-  h.state_next = ptr<const uint32_t>(a->state_next.address);
-  h.next_table = ptr<const int32_t>(a->next_table.address);
-  h.out_token = ptr<uint32_t>(a->out_token.address);
-  h.out_score = ptr<float>(a->out_score.address);
-  h.out_next = ptr<uint32_t>(a->out_next_state.address);
-  h.records = reinterpret_cast<mf::Record*>(ws + L.head_records);
-  h.counters = reinterpret_cast<uint32_t*>(ws + L.head_counters);
-  h.rows = static_cast<uint32_t>(a->rows);
-  h.H = static_cast<uint32_t>(a->hidden);
-  h.V = static_cast<uint32_t>(a->vocab);
-  h.states = static_cast<uint32_t>(a->states);
-  h.nnz = static_cast<uint32_t>(a->nnz);
-  h.chunk = L.chunk;
-  h.max_chunks = L.max_chunks;
-  h.order = a->order;
-}
-
-static mf::PlanArgs plan_args(const mf_decode_tail_args* a, const TailLayout& L, char* ws) {
-  mf::PlanArgs p{};
-  p.row_state = ptr<const uint32_t>(a->row_state.address);
-  p.offsets = ptr<const uint32_t>(a->state_offsets.address);
-  p.states = static_cast<uint32_t>(a->states);
-  p.nnz = static_cast<uint32_t>(a->nnz);
-  p.max_chunks = L.max_chunks;
-  p.chunk = L.chunk;
-  p.head_groups = L.groups;
-  p.chunks_per_row = reinterpret_cast<uint32_t*>(ws + L.chunks_per_row);
-  p.prefix = reinterpret_cast<uint32_t*>(ws + L.prefix);
-  p.start_row = reinterpret_cast<uint32_t*>(ws + L.start_row);
-  p.counter = reinterpret_cast<uint32_t*>(ws + L.plan_counter);
-  p.out_token = ptr<uint32_t>(a->out_token.address);
-  p.out_score = ptr<float>(a->out_score.address);
-  p.out_next = ptr<uint32_t>(a->out_next_state.address);
-  return p;
-}
-
-enum class Stage { kPrepare, kRestricted, kUnrestricted };
-
-static mf_status decode_tail_stage(const mf_decode_tail_args* args, uintptr_t stream,
-                                   Stage stage) {
-  if (stream == 0) return status(MF_INVALID_ARGUMENT);
-  TailLayout L{};
-  mf_status v = validate_tail(args, false, L);
-  if (v.code != MF_OK) return v;
-  v = check_workspace(args, L);
-  if (v.code != MF_OK) return v;
-  const mf_decode_tail_args* a = args;
-  char* ws = ptr<char>(a->workspace.address);
-  const hipStream_t s = native(stream);
-  float* y = reinterpret_cast<float*>(ws + L.y);
-  float* row_norm = reinterpret_cast<float*>(ws + L.row_norm);
-  const mf::PlanArgs plan = plan_args(a, L, ws);
-  hipError_t e = hipSuccess;
-  switch (stage) {
-    case Stage::kPrepare:
-      // final RMSNorm + work plan
-      e = mf::launch_norm_plan(ptr<const float>(a->x.address),
-                               ptr<const float>(a->norm_weight.address), y, row_norm,
-                               static_cast<uint32_t>(a->rows), static_cast<uint32_t>(a->hidden),
-                               a->epsilon, plan, s);
-      break;
-    case Stage::kRestricted: {
-      // restricted rows: CSR gather head
-      HeadArgs h{};
-      fill_head_common(a, L, ws, h);
-      h.coef = dot_bound_coef(a->hidden);
-      h.slack = underflow_slack(a->hidden);
-      h.prefix = plan.prefix;
-      h.start_row = plan.start_row;
-      e = mf::launch_head(ScoreSource::kDotF32, h, L.groups, s);
-      break;
-    }
-    case Stage::kUnrestricted: {
-      // unrestricted rows: MFMA full-vocabulary head
-      if (a->unrestricted_count == 0) break;
-      mf::FallbackArgs f{};
-      f.y = y;
-      f.row_index = ptr<const uint32_t>(a->unrestricted_rows.address);
-      f.m = static_cast<uint32_t>(a->unrestricted_count);
-      f.rows = static_cast<uint32_t>(a->rows);
-      f.row_norm = row_norm;
-      f.emb = ptr<const uint16_t>(a->embedding.address);
-      f.H = static_cast<uint32_t>(a->hidden);
-      f.V = static_cast<uint32_t>(a->vocab);
-      f.records = reinterpret_cast<mf::Record*>(ws + L.fb_records);
-      f.counters = reinterpret_cast<uint32_t*>(ws + L.fb_counters);
-      f.out_token = ptr<uint32_t>(a->out_token.address);
-      f.out_score = ptr<float>(a->out_score.address);
-      f.out_next = ptr<uint32_t>(a->out_next_state.address);
-      mfma_bound_coefs(a->hidden, f.coef, f.coef2);
-      f.slack = underflow_slack(a->hidden);
-      f.order = a->order;
-      e = mf::launch_fallback(f, s);
-      break;
-    }
-  }
-  return launch_status(e);
-}
-
 mf_status mf_decode_tail_prepare(const mf_decode_tail_args* args, uintptr_t stream) {
   return decode_tail_stage(args, stream, Stage::kPrepare);
 }
@@ -674,8 +683,12 @@ mf_status mf_decode_tail_unrestricted(const mf_decode_tail_args* args, uintptr_t
   return decode_tail_stage(args, stream, Stage::kUnrestricted);
 }
 
+mf_status mf_decode_tail_finalize(const mf_decode_tail_args* args, uintptr_t stream) {
+  return decode_tail_stage(args, stream, Stage::kFinalize);
+}
+
 mf_status mf_decode_tail_f16(const mf_decode_tail_args* args, uintptr_t stream) {
-  for (Stage st : {Stage::kPrepare, Stage::kRestricted, Stage::kUnrestricted}) {
+  for (Stage st : {Stage::kPrepare, Stage::kRestricted, Stage::kUnrestricted, Stage::kFinalize}) {
     const mf_status v = decode_tail_stage(args, stream, st);
     if (v.code != MF_OK) return v;
   }
@@ -692,22 +705,16 @@ mf_status mf_decode_tail_full_f16(const mf_decode_tail_args* args, uintptr_t str
   const mf_decode_tail_args* a = args;
   char* ws = ptr<char>(a->workspace.address);
   const hipStream_t s = native(stream);
-  float* y = reinterpret_cast<float*>(ws + L.y);
-  float* row_norm = reinterpret_cast<float*>(ws + L.row_norm);
   float* scores = reinterpret_cast<float*>(ws + L.scores);
   float* tok_norm = reinterpret_cast<float*>(ws + L.tok_norm);
 
-  // 1. final RMSNorm (the plan's outputs are unused here)
-  const mf::PlanArgs plan = plan_args(a, L, ws);
-  hipError_t e = mf::launch_norm_plan(ptr<const float>(a->x.address),
-                                      ptr<const float>(a->norm_weight.address), y, row_norm,
-                                      static_cast<uint32_t>(a->rows),
-                                      static_cast<uint32_t>(a->hidden), a->epsilon, plan, s);
+  // 1. final RMSNorm
+  hipError_t e = mf::launch_tail_norm(norm_args(a, L, ws, false),
+                                      static_cast<uint32_t>(a->rows), s);
   if (e != hipSuccess) return launch_status(e);
-
   // 2. full output projection of every row: FP32 scores [rows, V]
   mf::ProjArgs p{};
-  p.y = y;
+  p.y = reinterpret_cast<const float*>(ws + L.y);
   p.m = static_cast<uint32_t>(a->rows);
   p.rows = static_cast<uint32_t>(a->rows);
   p.emb = ptr<const uint16_t>(a->embedding.address);
@@ -717,17 +724,16 @@ mf_status mf_decode_tail_full_f16(const mf_decode_tail_args* args, uintptr_t str
   p.tok_norm = tok_norm;
   e = mf::launch_projection(p, s);
   if (e != hipSuccess) return launch_status(e);
-
-  // 3. restricted selection over the scores (unrestricted rows: all ids)
-  HeadArgs h{};
-  fill_head_common(a, L, ws, h);
-  h.scores = scores;
-  h.row_norm = row_norm;
-  h.tok_norm = tok_norm;
-  mfma_bound_coefs(a->hidden, h.coef, h.coef2);
-  h.slack = underflow_slack(a->hidden);
-  h.lookup_unrestricted = 1;
-  e = mf::launch_head(ScoreSource::kLookup, h, 0, s);
+  // 3. restricted selection over the scores (unrestricted rows: every id)
+  mf::GatherArgs g = gather_args(a, L, ws);
+  g.scores = scores;
+  g.row_norm = reinterpret_cast<const float*>(ws + L.row_norm);
+  g.tok_norm = tok_norm;
+  mfma_bound_coefs(a->hidden, g.coef, g.coef2);
+  e = mf::launch_gather(ScoreSource::kLookup, g, s);
+  if (e != hipSuccess) return launch_status(e);
+  // 4. merge, reference-order rescore, DFA advance
+  e = mf::launch_finalize(finalize_args(a, L, ws, true), s);
   return launch_status(e);
 }
 

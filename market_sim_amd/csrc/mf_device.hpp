@@ -229,6 +229,46 @@ struct alignas(16) Record {
   uint32_t min_pos;
 };
 
+// Window summary of one tile of candidates (a chunk of a row's list in the
+// gather kernel, or 128 vocabulary ids of an unrestricted row in the MFMA
+// kernel), merged per row by the finalize kernel.  best_lower is the tile's
+// max over candidates of g - b; the members are the candidates with
+// g + b >= best_lower.  kTileRescoreAll: non-finite values or more than
+// kTileMembers members -- the finalize kernel rescores the whole tile.
+constexpr int kTileMembers = 4;
+enum : uint32_t {
+  kTileInvalid = 1u,     // an id >= vocabulary: the whole row is invalid
+  kTileRescoreAll = 2u,
+};
+
+struct alignas(16) TileMember {
+  uint32_t token;
+  uint32_t pos;
+  float lower;
+  float upper;
+};
+
+struct alignas(16) TileRecord {
+  float best_lower;
+  uint32_t flags;
+  uint32_t min_token;
+  uint32_t min_pos;
+  uint32_t begin;     // list position of the tile's first candidate
+  uint32_t count;     // candidates in the tile
+  uint32_t n_members;
+  uint32_t pad;
+  TileMember m[kTileMembers];
+};
+
+// Per-row metadata written by the decode-tail norm kernel.
+enum : uint32_t { kRowRestricted = 1u, kRowUnrestricted = 2u, kRowInvalid = 4u };
+struct alignas(16) RowMeta {
+  uint32_t list_begin;
+  uint32_t count;
+  uint32_t state;
+  uint32_t kind;
+};
+
 __device__ __forceinline__ uint32_t atomic_arrive(uint32_t* counter) {
   return __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL,
                                 __HIP_MEMORY_SCOPE_AGENT);

@@ -1,6 +1,7 @@
-// gfx950 kernels of the restricted head path: final RMSNorm, the CSR
-// restricted head (gather + fast FP32 dot + exact window rescore + merge +
-// DFA advance) and the selections over precomputed logits.
+// gfx950 kernels of the reference operators: RMSNorm, the fixed-width
+// restricted output head (restricted_output_head_f16), the selections over
+// precomputed logits and the small-shape linear_f16.  The decode tail lives
+// in mf_tail.hip.
 //
 // Build: hipcc --offload-arch=gfx950 -ffp-contract=off (see csrc/Makefile).
 // -ffp-contract=off keeps every reference-order multiply-add unfused unless
@@ -76,120 +77,6 @@ __global__ __launch_bounds__(kWave) void rms_norm_kernel(
   }
 }
 
-// The decode-tail norm: the same arithmetic for FP32 rows into y (or a plain
-// copy when weight is null), row norms for the MFMA bounds, and the head's work
-// plan.  Lane 0 classifies its row; the last workgroup to arrive scans the
-// per-row chunk counts and assigns each head workgroup its first row.
-__global__ __launch_bounds__(kWave) void norm_plan_kernel(
-    const float* __restrict__ x, const float* __restrict__ weight,
-    float* __restrict__ y, float* __restrict__ row_norm, uint32_t rows,
-    uint32_t H, float epsilon, PlanArgs plan) {
-  extern __shared__ float xs[];
-  __shared__ float inverse_shared;
-  __shared__ uint32_t last_shared;
-  const uint64_t r = blockIdx.x;
-  const uint32_t lane = threadIdx.x;
-  for (uint32_t c = lane; c < H; c += kWave) xs[c] = x[r * H + c];
-  __syncthreads();
-  if (lane == 0) {
-    if (weight != nullptr) {
-      float sum_squares = 0.0f;
-#pragma unroll 8
-      for (uint32_t c = 0; c < H; ++c) {
-        const float v = xs[c];
-        const float sq = v * v;
-        sum_squares = sum_squares + sq;
-      }
-      const float mean = div_rn(sum_squares, static_cast<float>(H));
-      inverse_shared = div_rn(1.0f, sqrt_rn(mean + epsilon));
-    }
-    // Unrestricted rows are preset invalid too: the MFMA fallback, launched
-    // after the head on the same stream, overwrites the rows it was given.
-    uint32_t chunks = 0u;
-    const uint32_t s = plan.row_state[r];
-    bool invalid = true;
-    if (s != kStateUnrestricted && s < plan.states) {
-      const uint32_t b = plan.offsets[s];
-      const uint32_t e = plan.offsets[s + 1];
-      if (e > b && e <= plan.nnz) {
-        chunks = (e - b + plan.chunk - 1) / plan.chunk;
-        invalid = chunks > plan.max_chunks;
-        if (invalid) chunks = 0u;
-      }
-    }
-    if (invalid) {
-      plan.out_token[r] = kInvalidToken;
-      if (plan.out_score != nullptr) plan.out_score[r] = __builtin_nanf("");
-      if (plan.out_next != nullptr) plan.out_next[r] = kInvalidToken;
-    }
-    plan.chunks_per_row[r] = chunks;
-  }
-  __syncthreads();
-  const float inverse = inverse_shared;
-  float norm_sq = 0.0f;
-  for (uint32_t c = lane; c < H; c += kWave) {
-    float v = xs[c];
-    if (weight != nullptr) {
-      const float scaled = v * inverse;
-      v = scaled * weight[c];
-    }
-    y[r * H + c] = v;
-    norm_sq = __builtin_fmaf(v, v, norm_sq);
-  }
-#pragma unroll
-  for (int m = kWave / 2; m > 0; m >>= 1) norm_sq += __shfl_xor(norm_sq, m);
-  if (lane == 0) {
-    row_norm[r] = __fsqrt_rn(norm_sq) * (1.0f + 0x1p-7f);
-    last_shared = atomic_arrive(plan.counter) == rows - 1 ? 1u : 0u;
-  }
-  __syncthreads();
-  if (last_shared == 0u) return;
-  acquire_agent();
-  // exclusive scan of chunks_per_row -> prefix (one wave, 64 rows per step)
-  uint32_t running = 0u;
-  for (uint32_t base = 0; base < rows; base += kWave) {
-    const uint32_t idx = base + lane;
-    const uint32_t v = idx < rows ? plan.chunks_per_row[idx] : 0u;
-    uint32_t incl = v;
-#pragma unroll
-    for (int d = 1; d < kWave; d <<= 1) {
-      const uint32_t o = __shfl_up(incl, d);
-      if (static_cast<int>(lane) >= d) incl += o;
-    }
-    if (idx < rows) plan.prefix[idx] = running + incl - v;
-    running += __shfl(incl, kWave - 1);
-  }
-  if (lane == 0) {
-    plan.prefix[rows] = running;
-    *plan.counter = 0u;
-  }
-  // head workgroup b owns items [W*b/G, W*(b+1)/G); it starts at the row that
-  // holds item W*b/G, i.e. b in [ceil(p*G/W), ceil(q*G/W)) for a row with
-  // items [p, q).
-  const uint64_t W = running;
-  const uint64_t G = plan.head_groups;
-  if (W == 0) return;
-  uint32_t row_begin_items = 0u;
-  for (uint32_t base = 0; base < rows; base += kWave) {
-    const uint32_t idx = base + lane;
-    const uint32_t v = idx < rows ? plan.chunks_per_row[idx] : 0u;
-    uint32_t incl = v;
-#pragma unroll
-    for (int d = 1; d < kWave; d <<= 1) {
-      const uint32_t o = __shfl_up(incl, d);
-      if (static_cast<int>(lane) >= d) incl += o;
-    }
-    if (idx < rows && v > 0) {
-      const uint64_t p = row_begin_items + incl - v;
-      const uint64_t q = p + v;
-      const uint64_t b_lo = (p * G + W - 1) / W;
-      const uint64_t b_hi = (q * G + W - 1) / W;
-      for (uint64_t b = b_lo; b < b_hi && b < G; ++b) plan.start_row[b] = idx;
-    }
-    row_begin_items += __shfl(incl, kWave - 1);
-  }
-}
-
 // Reference linear_f16 arithmetic on shapes the MFMA tiling does not cover:
 // one output per thread, sequential fma over the input features
 // (tests/cuda/cuda_tests.cu:170-181 order), rounded to FP16.
@@ -214,42 +101,15 @@ __global__ __launch_bounds__(256) void linear_f16_simple_kernel(
 // ---------------------------------------------------------------------------
 
 struct RowList {
-  const uint32_t* ids; // null: virtual list 0..count-1 (whole vocabulary)
+  const uint32_t* ids;
   uint32_t count;
-  uint32_t state;
-  uint32_t list_begin; // offset of the list in state_tokens (CSR mode)
-  int status;          // 0 ok, 1 invalid row, 2 skip (handled elsewhere)
+  int status;  // 0 ok, 1 invalid row
 };
 
-__device__ RowList resolve_row(const HeadArgs& a, uint32_t r, bool lookup) {
-  RowList l{nullptr, 0u, 0u, 0u, 0};
-  if (a.row_state != nullptr) {
-    const uint32_t s = a.row_state[r];
-    l.state = s;
-    if (s == kStateUnrestricted) {
-      if (lookup && a.lookup_unrestricted) {
-        l.count = a.V;
-        return l;
-      }
-      l.status = 2;
-      return l;
-    }
-    if (s >= a.states) {
-      l.status = 1;
-      return l;
-    }
-    const uint32_t b = a.offsets[s];
-    const uint32_t e = a.offsets[s + 1];
-    if (e <= b || e > a.nnz ||
-        (a.max_chunks > 0 && (e - b + a.chunk - 1) / a.chunk > a.max_chunks)) {
-      l.status = 1;
-      return l;
-    }
-    l.ids = a.tokens + b;
-    l.list_begin = b;
-    l.count = e - b;
-    return l;
-  }
+// Fixed-width candidate table of the reference restricted head
+// (greedy.cu:145-151): count 0 or above the maximum makes the row invalid.
+__device__ RowList resolve_row(const HeadArgs& a, uint32_t r) {
+  RowList l{nullptr, 0u, 0};
   const uint32_t c = a.fixed_counts[r];
   if (c == 0 || c > a.max_allowed) {
     l.status = 1;
@@ -434,23 +294,9 @@ __device__ void fast_scores_generic(const HeadArgs& a, const float* ys,
   }
 }
 
-__device__ void fast_scores_lookup(const HeadArgs& a, uint32_t r,
-                                   HeadShared& sh, uint32_t n) {
-  const float* srow = a.scores + static_cast<uint64_t>(r) * a.V;
-  const float yn = a.row_norm[r];
-  for (uint32_t c = threadIdx.x; c < n; c += kThreads) {
-    const uint32_t t = sh.tk[c];
-    sh.sc[c] = srow[t];
-    sh.bd[c] = __builtin_fmaf(a.tok_norm[t], __builtin_fmaf(a.coef, yn, a.coef2), a.slack);
-  }
-}
-
-template <ScoreSource kSrc, int kH, int kG>
-__device__ void fast_scores(const HeadArgs& a, uint32_t r, const float* ys,
-                            HeadShared& sh, uint32_t n) {
-  if constexpr (kSrc == ScoreSource::kLookup) {
-    fast_scores_lookup(a, r, sh, n);
-  } else if constexpr (kH > 0) {
+template <int kH, int kG>
+__device__ void fast_scores(const HeadArgs& a, const float* ys, HeadShared& sh, uint32_t n) {
+  if constexpr (kH > 0) {
     fast_scores_vec<kH, kG, 2>(a, ys, sh, n);
   } else {
     fast_scores_generic(a, ys, sh, n);
@@ -569,31 +415,18 @@ __device__ void finalize_row(const HeadArgs& a, uint32_t r, const RowList& rl,
   best = block_best(sh, best);
   if (tid == 0) {
     uint32_t token = kInvalidToken;
-    uint32_t next = kInvalidToken;
     float score = __builtin_nanf("");
     if (!invalid) {
-      uint32_t pos = best.pos;
       if (best.token == kInvalidToken) {
         token = mt;
-        pos = mp;
         score = canonical_dot_order(a.order, ys, a.emb + static_cast<uint64_t>(mt) * a.H, a.H);
       } else {
         token = best.token;
         score = best.score;
       }
-      if (rl.ids == nullptr) {
-        next = kStateUnrestricted;
-      } else if (a.row_state != nullptr) {
-        if (a.state_next != nullptr) {
-          next = a.state_next[rl.list_begin + pos];
-        } else if (a.next_table != nullptr) {
-          next = static_cast<uint32_t>(a.next_table[static_cast<uint64_t>(rl.state) * a.V + token]);
-        }
-      }
     }
     a.out_token[r] = token;
     if (a.out_score != nullptr) a.out_score[r] = score;
-    if (a.out_next != nullptr) a.out_next[r] = next;
   }
 }
 
@@ -603,108 +436,44 @@ __device__ bool load_block_ids(const HeadArgs& a, const RowList& rl,
                                HeadShared& sh, uint32_t begin, uint32_t n) {
   uint32_t bad = 0u;
   for (uint32_t c = threadIdx.x; c < n; c += kThreads) {
-    const uint32_t t = rl.ids != nullptr ? rl.ids[begin + c] : begin + c;
+    const uint32_t t = rl.ids[begin + c];
     bad |= t >= a.V ? 1u : 0u;
     sh.tk[c] = t < a.V ? t : 0u;
   }
   return block_sum(sh, bad) != 0u;
 }
 
-// One (row, chunk) work item; with max_chunks == 0 the workgroup owns the
-// whole row (all its blocks, records merged in LDS).  ys holds the row's FP32
-// hidden vector when *staged == r.
-template <ScoreSource kSrc, int kH, int kG>
-__device__ void head_item(const HeadArgs& a, uint32_t r, uint32_t k, float* ys,
-                          HeadShared& sh, uint32_t* staged) {
-  const RowList rl = resolve_row(a, r, kSrc == ScoreSource::kLookup);
-  if (rl.status == 2) return;
-  if (rl.status == 1) {
-    if (k == 0 && threadIdx.x == 0) {
-      a.out_token[r] = kInvalidToken;
-      if (a.out_score != nullptr) a.out_score[r] = __builtin_nanf("");
-      if (a.out_next != nullptr) a.out_next[r] = kInvalidToken;
-    }
-    return;
-  }
-  const bool multi = a.max_chunks > 0;
-  const uint32_t nblocks = (rl.count + a.chunk - 1) / a.chunk;
-  if (multi && k >= nblocks) return;
-
-  if (*staged != r) {
-    __syncthreads();
-    for (uint32_t f = threadIdx.x; f < a.H; f += kThreads) {
-      ys[f] = kSrc == ScoreSource::kDotF16Hidden
-                  ? half_to_float(a.hidden16[static_cast<uint64_t>(r) * a.H + f])
-                  : a.y[static_cast<uint64_t>(r) * a.H + f];
-    }
-    *staged = r;
-    __syncthreads();
-  }
-
-  const uint32_t first = multi ? k : 0u;
-  const uint32_t last = multi ? k + 1 : nblocks;
-  for (uint32_t blk = first; blk < last; ++blk) {
-    const uint32_t begin = blk * a.chunk;
-    const uint32_t n = rl.count - begin < a.chunk ? rl.count - begin : a.chunk;
-    const bool invalid = load_block_ids(a, rl, sh, begin, n);
-    if (!invalid) {
-      fast_scores<kSrc, kH, kG>(a, r, ys, sh, n);
-    }
-    __syncthreads();
-    summarize_block(a, ys, sh, n, begin, invalid);
-    if (threadIdx.x == 0) sh.recs[multi ? 0 : blk] = sh.rec;
-    __syncthreads();
-  }
-
-  if (!multi || nblocks == 1) {
-    finalize_row(a, r, rl, ys, sh, multi ? 1u : nblocks);
-    __syncthreads();
-    return;
-  }
-  // several workgroups share the row: publish, and the last one merges
-  Record* row_recs = a.records + static_cast<uint64_t>(r) * a.max_chunks;
-  if (threadIdx.x == 0) {
-    row_recs[k] = sh.rec;
-    const uint32_t arrived = atomic_arrive(&a.counters[r]);
-    sh.last = arrived == nblocks - 1 ? 1u : 0u;
-  }
-  __syncthreads();
-  if (sh.last == 0u) return;
-  acquire_agent();
-  for (uint32_t i = threadIdx.x; i < nblocks; i += kThreads) {
-    sh.recs[i] = row_recs[i];
-  }
-  if (threadIdx.x == 0) a.counters[r] = 0u;
-  __syncthreads();
-  finalize_row(a, r, rl, ys, sh, nblocks);
-  __syncthreads();
-}
-
-// Grid mode: blockIdx.x = k * rows + r.
-template <ScoreSource kSrc, int kH, int kG>
+// One workgroup per row: the row's candidates in blocks of a.chunk, each
+// block summarized into a record in LDS, then merged (finalize_row).
+template <int kH, int kG>
 __global__ __launch_bounds__(kThreads) void head_kernel(HeadArgs a) {
   extern __shared__ float ys[];
   __shared__ HeadShared sh;
-  uint32_t staged = kInvalidToken;
-  head_item<kSrc, kH, kG>(a, blockIdx.x % a.rows, blockIdx.x / a.rows, ys, sh, &staged);
-}
-
-// Planned mode: workgroup b walks its contiguous range of work items.
-template <ScoreSource kSrc, int kH, int kG>
-__global__ __launch_bounds__(kThreads) void head_planned_kernel(HeadArgs a) {
-  extern __shared__ float ys[];
-  __shared__ HeadShared sh;
-  const uint64_t W = a.prefix[a.rows];
-  const uint64_t G = gridDim.x;
-  const uint64_t w0 = W * blockIdx.x / G;
-  const uint64_t w1 = W * (blockIdx.x + 1) / G;
-  if (w0 >= w1) return;
-  uint32_t r = a.start_row[blockIdx.x];
-  uint32_t staged = kInvalidToken;
-  for (uint64_t w = w0; w < w1; ++w) {
-    while (w >= static_cast<uint64_t>(a.prefix[r + 1])) ++r;
-    head_item<kSrc, kH, kG>(a, r, static_cast<uint32_t>(w - a.prefix[r]), ys, sh, &staged);
+  const uint32_t r = blockIdx.x;
+  const RowList rl = resolve_row(a, r);
+  if (rl.status == 1) {
+    if (threadIdx.x == 0) {
+      a.out_token[r] = kInvalidToken;
+      if (a.out_score != nullptr) a.out_score[r] = __builtin_nanf("");
+    }
+    return;
   }
+  for (uint32_t f = threadIdx.x; f < a.H; f += kThreads) {
+    ys[f] = half_to_float(a.hidden16[static_cast<uint64_t>(r) * a.H + f]);
+  }
+  __syncthreads();
+  const uint32_t nblocks = (rl.count + a.chunk - 1) / a.chunk;
+  for (uint32_t blk = 0; blk < nblocks; ++blk) {
+    const uint32_t begin = blk * a.chunk;
+    const uint32_t n = rl.count - begin < a.chunk ? rl.count - begin : a.chunk;
+    const bool invalid = load_block_ids(a, rl, sh, begin, n);
+    if (!invalid) fast_scores<kH, kG>(a, ys, sh, n);
+    __syncthreads();
+    summarize_block(a, ys, sh, n, begin, invalid);
+    if (threadIdx.x == 0) sh.recs[blk] = sh.rec;
+    __syncthreads();
+  }
+  finalize_row(a, r, rl, ys, sh, nblocks);
 }
 
 // ---------------------------------------------------------------------------
@@ -796,52 +565,14 @@ hipError_t launch_rms_norm(const void* input, bool half_input, const void* weigh
   return hipGetLastError();
 }
 
-template <ScoreSource kSrc, int kH, int kG>
-void launch_head_variant(const HeadArgs& args, uint32_t groups, hipStream_t stream) {
-  const size_t lds = static_cast<size_t>(args.H) * sizeof(float);
-  if (args.prefix != nullptr) {
-    hipLaunchKernelGGL((head_planned_kernel<kSrc, kH, kG>), dim3(groups), dim3(kThreads), lds,
-                       stream, args);
-  } else {
-    const uint32_t slots = args.max_chunks > 0 ? args.max_chunks : 1u;
-    hipLaunchKernelGGL((head_kernel<kSrc, kH, kG>), dim3(args.rows * slots), dim3(kThreads), lds,
-                       stream, args);
-  }
-}
-
-hipError_t launch_head(ScoreSource source, const HeadArgs& args, uint32_t groups,
-                       hipStream_t stream) {
+hipError_t launch_head(const HeadArgs& args, hipStream_t stream) {
   const bool aligned = (reinterpret_cast<uintptr_t>(args.emb) & 15u) == 0;
-  switch (source) {
-    case ScoreSource::kDotF32:
-      if (args.H == 576 && aligned) {
-        launch_head_variant<ScoreSource::kDotF32, 576, 8>(args, groups, stream);
-      } else if (args.H == 2048 && aligned) {
-        launch_head_variant<ScoreSource::kDotF32, 2048, 32>(args, groups, stream);
-      } else {
-        launch_head_variant<ScoreSource::kDotF32, 0, 64>(args, groups, stream);
-      }
-      break;
-    case ScoreSource::kDotF16Hidden:
-      if (args.H == 576 && aligned) {
-        launch_head_variant<ScoreSource::kDotF16Hidden, 576, 8>(args, groups, stream);
-      } else {
-        launch_head_variant<ScoreSource::kDotF16Hidden, 0, 64>(args, groups, stream);
-      }
-      break;
-    case ScoreSource::kLookup:
-      launch_head_variant<ScoreSource::kLookup, 0, 64>(args, groups, stream);
-      break;
+  const size_t lds = static_cast<size_t>(args.H) * sizeof(float);
+  if (args.H == 576 && aligned) {
+    hipLaunchKernelGGL((head_kernel<576, 8>), dim3(args.rows), dim3(kThreads), lds, stream, args);
+  } else {
+    hipLaunchKernelGGL((head_kernel<0, 64>), dim3(args.rows), dim3(kThreads), lds, stream, args);
   }
-  return hipGetLastError();
-}
-
-hipError_t launch_norm_plan(const float* x, const float* weight, float* y,
-                            float* row_norm, uint32_t rows, uint32_t hidden,
-                            float epsilon, const PlanArgs& plan, hipStream_t stream) {
-  const size_t lds = static_cast<size_t>(hidden) * sizeof(float);
-  hipLaunchKernelGGL(norm_plan_kernel, dim3(rows), dim3(kWave), lds, stream, x, weight, y,
-                     row_norm, rows, hidden, epsilon, plan);
   return hipGetLastError();
 }
 

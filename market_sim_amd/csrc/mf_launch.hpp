@@ -9,72 +9,32 @@
 namespace mf {
 
 struct Record;
+struct RowMeta;
+struct TileRecord;
 
-// Where a head workgroup reads candidate scores from.
+// Where a decode-tail gather workgroup reads candidate scores from.
 enum class ScoreSource : int {
-  kDotF32 = 0,       // fast dot of FP32 normalized hidden with the FP16 table
-  kDotF16Hidden = 1, // the same with FP16 hidden (legacy restricted head)
-  kLookup = 2,       // FP32 scores already computed by the MFMA projection
+  kDotF32 = 0,  // fast dot of FP32 normalized hidden with the FP16 table
+  kLookup = 2,  // FP32 scores already computed by the MFMA projection
 };
 
+// The fixed-width restricted head of the reference API
+// (restricted_output_head_f16): one workgroup per row, FP16 hidden.
 struct HeadArgs {
-  const float* y;            // [rows, H] FP32 normalized hidden
-  const uint16_t* hidden16;  // [rows, H] FP16 hidden (kDotF16Hidden)
-  const uint16_t* emb;       // [V, H] FP16 table
-  const float* scores;       // [rows, V] (kLookup)
-  const float* row_norm;     // [rows] ||y_r|| upper bounds (kLookup)
-  const float* tok_norm;     // [V] ||e_t|| upper bounds (kLookup)
-  const uint32_t* row_state; // CSR mode when non-null
-  const uint32_t* offsets;
-  const uint32_t* tokens;
-  const uint32_t* fixed_ids;    // fixed-width mode [rows, max_allowed]
+  const uint16_t* hidden16;     // [rows, H]
+  const uint16_t* emb;          // [V, H]
+  const uint32_t* fixed_ids;    // [rows, max_allowed]
   const uint32_t* fixed_counts; // [rows]
-  const uint32_t* state_next;   // [nnz] or null
-  const int32_t* next_table;    // [states, V] or null
   uint32_t* out_token;
   float* out_score;
-  uint32_t* out_next;
-  Record* records;     // [rows, max_chunks] multi-workgroup rows
-  uint32_t* counters;  // [rows] arrival counters (zero between calls)
   uint32_t rows;
   uint32_t H;
   uint32_t V;
-  uint32_t states;
-  uint32_t nnz;        // length of tokens: lists ending past it are invalid
   uint32_t max_allowed;
   uint32_t chunk;      // candidates per block
-  uint32_t max_chunks; // chunk slots per row in the grid; 0 = one workgroup per row
-  float coef;          // fast-score bound: b = coef * A + slack (dot), or
-  float coef2;         //   b = ||e|| * (coef * ||y|| + coef2) + slack (lookup)
+  float coef;          // fast-score bound: b = coef * sum|y e| + slack
   float slack;
   int order;           // 0 fma chain, 1 mul-add chain
-  int lookup_unrestricted; // kLookup: unrestricted rows score the whole vocabulary
-  // Planned mode (CSR rows): work items are (row, chunk) pairs numbered by
-  // prefix[rows + 1]; workgroup b owns items [W*b/G, W*(b+1)/G) and starts
-  // its row walk at start_row[b].  Null prefix: grid of rows x max_chunks.
-  const uint32_t* prefix;
-  const uint32_t* start_row;
-};
-
-// Work plan built by the norm kernel's last workgroup (CSR decode tail):
-// chunks per row, their exclusive prefix, and each head workgroup's first row.
-// Invalid rows (state >= S, empty list) get their outputs written here and no
-// chunk; unrestricted rows get no chunk (the MFMA fallback owns them).
-struct PlanArgs {
-  const uint32_t* row_state;
-  const uint32_t* offsets;
-  uint32_t states;
-  uint32_t nnz;
-  uint32_t max_chunks;      // rows needing more chunks are invalid
-  uint32_t chunk;
-  uint32_t head_groups;     // G
-  uint32_t* chunks_per_row; // [rows]
-  uint32_t* prefix;         // [rows + 1]
-  uint32_t* start_row;      // [G]
-  uint32_t* counter;        // arrival counter (zero between calls)
-  uint32_t* out_token;
-  float* out_score;
-  uint32_t* out_next;
 };
 
 constexpr uint32_t kHeadChunkMax = 1024;
@@ -86,15 +46,7 @@ hipError_t launch_rms_norm(const void* input, bool half_input,
                            bool half_output, float* row_norm, uint32_t rows,
                            uint32_t hidden, float epsilon, hipStream_t stream);
 
-// RMSNorm (or a plain copy when weight is null) of FP32 rows into y with row
-// norms, plus the work plan.
-hipError_t launch_norm_plan(const float* x, const float* weight, float* y,
-                            float* row_norm, uint32_t rows, uint32_t hidden,
-                            float epsilon, const PlanArgs& plan,
-                            hipStream_t stream);
-
-hipError_t launch_head(ScoreSource source, const HeadArgs& args,
-                       uint32_t groups, hipStream_t stream);
+hipError_t launch_head(const HeadArgs& args, hipStream_t stream);
 
 hipError_t launch_linear_f16_simple(const uint16_t* input, const uint16_t* weight,
                                     uint16_t* output, uint32_t rows,
@@ -111,6 +63,78 @@ hipError_t launch_restricted_greedy(const void* logits, bool half,
                                     uint32_t max_allowed, hipStream_t stream);
 
 hipError_t launch_fill_zero(void* address, uint64_t bytes, hipStream_t stream);
+
+// ---- decode tail (mf_tail.hip) ----------------------------------------------
+
+constexpr uint32_t kGatherTileMax = 256;
+
+struct TailNormArgs {
+  const float* x;          // [rows, H]
+  const float* weight;     // [H] or null (x already normalized)
+  float epsilon;
+  float* y;                // [rows, H] reference-order normalized hidden
+  float* row_norm;         // [rows] upper bound of ||y||
+  uint16_t* y_hi;          // [rows, H] FP16 split of unrestricted rows (or null)
+  uint16_t* y_lo;
+  const uint32_t* row_state;
+  const uint32_t* offsets;
+  uint32_t states;
+  uint32_t nnz;
+  uint32_t max_count;      // longer lists make the row invalid
+  uint32_t V;
+  uint32_t H;
+  RowMeta* row_meta;       // [rows]
+  uint32_t* fb_map;        // [rows] row -> unrestricted list index (reset here)
+  uint32_t* out_token;
+  float* out_score;
+  uint32_t* out_next;
+};
+
+struct GatherArgs {
+  const float* y;          // [rows, H]
+  const uint16_t* emb;     // [V, H]
+  const float* scores;     // [rows, V] (lookup)
+  const float* row_norm;   // (lookup)
+  const float* tok_norm;   // (lookup)
+  const uint32_t* tokens;  // state lists
+  const RowMeta* row_meta;
+  TileRecord* records;     // [rows, max_tiles]
+  uint32_t rows;
+  uint32_t H;
+  uint32_t V;
+  uint32_t tile;           // candidates per tile (<= kGatherTileMax)
+  uint32_t max_tiles;
+  float coef;              // dot: b = coef * sum|y e| + slack
+  float coef2;             // lookup: b = ||e|| (coef ||y|| + coef2) + slack
+  float slack;
+};
+
+struct FinalizeArgs {
+  const float* y;
+  const uint16_t* emb;
+  const uint32_t* tokens;
+  const RowMeta* row_meta;
+  const TileRecord* records;     // gather tiles [rows, max_tiles]
+  uint32_t max_tiles;
+  uint32_t tile;
+  const TileRecord* fb_records;  // MFMA tiles [m, fb_tiles] (or null)
+  const uint32_t* fb_map;
+  uint32_t fb_tiles;
+  int lookup_unrestricted;       // unrestricted rows live in records (comparator)
+  const uint32_t* state_next;
+  const int32_t* next_table;
+  uint32_t* out_token;
+  float* out_score;
+  uint32_t* out_next;
+  uint32_t rows;
+  uint32_t H;
+  uint32_t V;
+  int order;
+};
+
+hipError_t launch_tail_norm(const TailNormArgs& args, uint32_t rows, hipStream_t stream);
+hipError_t launch_gather(ScoreSource source, const GatherArgs& args, hipStream_t stream);
+hipError_t launch_finalize(const FinalizeArgs& args, hipStream_t stream);
 
 // ---- MFMA projection (mf_mfma.hip) ----------------------------------------
 
@@ -138,7 +162,8 @@ hipError_t launch_projection(const ProjArgs& args, hipStream_t stream);
 // argmax epilogue, per-tile records and a last-arriver merge per row that
 // rescores the window in the reference order.
 struct FallbackArgs {
-  const float* y;           // [rows, H] normalized hidden (all rows)
+  const uint16_t* y_hi;     // [rows, H] FP16 split of the normalized hidden
+  const uint16_t* y_lo;
   const uint32_t* row_index;// [m] unrestricted rows (entries >= rows are skipped)
   uint32_t m;
   uint32_t rows;
@@ -146,15 +171,11 @@ struct FallbackArgs {
   const uint16_t* emb;
   uint32_t H;
   uint32_t V;
-  Record* records;          // [m, tiles]
-  uint32_t* counters;       // [ceil(m / 32)]
-  uint32_t* out_token;
-  float* out_score;
-  uint32_t* out_next;
+  TileRecord* records;      // [m, tiles]
+  uint32_t* fb_map;         // [rows] written: row -> m
   float coef;               // b = ||e|| * (coef * ||y|| + coef2) + slack
   float coef2;
   float slack;
-  int order;
 };
 
 uint32_t fallback_tiles(uint32_t vocab);

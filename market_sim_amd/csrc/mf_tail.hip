@@ -1,0 +1,586 @@
+// The decode tail on gfx950 (mf_decode_tail_f16):
+//
+//   K1 tail_norm_kernel      final RMSNorm in the reference order, per-row
+//                            metadata (list, kind), FP16 hi/lo split of the
+//                            unrestricted rows for the MFMA head; presets the
+//                            outputs of invalid and unrestricted rows
+//   K2 gather_kernel         streams the allowed embedding rows of one tile
+//                            (a chunk of one row's list) and writes a tile
+//                            record: the candidates whose [g - b, g + b]
+//                            interval reaches the tile's best lower bound
+//   (K4 fallback_kernel, mf_mfma.hip, writes the same records for
+//    unrestricted rows)
+//   K3 finalize_kernel       per row: merges tile records, rescores the
+//                            surviving candidates in the reference order,
+//                            selects (greedy.cu rules), advances the DFA
+//
+// K2 carries no atomics and no reference-order work, so it is a pure stream
+// of embedding rows; the serial reference-order chains live in K1 and K3,
+// where every row runs in parallel.
+#include <hip/hip_runtime.h>
+
+#include "mf_device.hpp"
+#include "mf_launch.hpp"
+
+namespace mf {
+namespace {
+
+constexpr int kThreads = 256;
+
+// Sum of squares in the reference order (operators.cpp:527-531): every square
+// rounded (lanes compute them in parallel into sq[]), then added in column
+// order by one lane, with the LDS reads of the next four values issued ahead
+// of the dependent adds.
+__device__ float sequential_sum(const float* sq, uint32_t H) {
+  float s = 0.0f;
+  uint32_t c = 0;
+  if ((H & 3u) == 0) {
+    const float4* q = reinterpret_cast<const float4*>(sq);
+    const uint32_t n4 = H / 4;
+    float4 cur = q[0];
+    for (uint32_t i = 0; i < n4; ++i) {
+      const float4 nxt = q[i + 1 < n4 ? i + 1 : i];
+      s = s + cur.x;
+      s = s + cur.y;
+      s = s + cur.z;
+      s = s + cur.w;
+      cur = nxt;
+    }
+    c = H;
+  }
+  for (; c < H; ++c) s = s + sq[c];
+  return s;
+}
+
+__global__ __launch_bounds__(kWave) void tail_norm_kernel(TailNormArgs a) {
+  extern __shared__ float lds[];
+  float* xs = lds;
+  float* sq = lds + a.H;
+  __shared__ float inverse_shared;
+  const uint64_t r = blockIdx.x;
+  const uint32_t lane = threadIdx.x;
+  const uint32_t H = a.H;
+  for (uint32_t c = lane; c < H; c += kWave) {
+    const float v = a.x[r * H + c];
+    xs[c] = v;
+    sq[c] = v * v;
+  }
+  __syncthreads();
+  RowMeta meta{0u, 0u, 0u, kRowInvalid};
+  if (lane == 0) {
+    if (a.weight != nullptr) {
+      const float sum_squares = sequential_sum(sq, H);
+      const float mean = div_rn(sum_squares, static_cast<float>(H));
+      inverse_shared = div_rn(1.0f, sqrt_rn(mean + a.epsilon));
+    }
+    const uint32_t s = a.row_state[r];
+    meta.state = s;
+    if (s == kStateUnrestricted) {
+      meta.kind = kRowUnrestricted;
+      meta.count = a.V;
+    } else if (s < a.states) {
+      const uint32_t b = a.offsets[s];
+      const uint32_t e = a.offsets[s + 1];
+      if (e > b && e <= a.nnz && e - b <= a.max_count) {
+        meta = RowMeta{b, e - b, s, kRowRestricted};
+      }
+    }
+    a.row_meta[r] = meta;
+    if (meta.kind != kRowRestricted) {
+      // invalid rows keep these; unrestricted rows are overwritten by the
+      // finalize kernel when the MFMA head was given them
+      a.out_token[r] = kInvalidToken;
+      if (a.out_score != nullptr) a.out_score[r] = __builtin_nanf("");
+      if (a.out_next != nullptr) a.out_next[r] = kInvalidToken;
+    }
+    if (a.fb_map != nullptr) a.fb_map[r] = kInvalidToken;
+  }
+  __syncthreads();
+  const float inverse = inverse_shared;
+  const bool split = a.y_hi != nullptr && a.row_state[r] == kStateUnrestricted;
+  float norm_sq = 0.0f;
+  for (uint32_t c = lane; c < H; c += kWave) {
+    float v = xs[c];
+    if (a.weight != nullptr) {
+      const float scaled = v * inverse;
+      v = scaled * a.weight[c];
+    }
+    a.y[r * H + c] = v;
+    norm_sq = __builtin_fmaf(v, v, norm_sq);
+    if (split) {
+      const _Float16 hi = static_cast<_Float16>(v);
+      a.y_hi[r * H + c] = __builtin_bit_cast(uint16_t, hi);
+      a.y_lo[r * H + c] = float_to_half_rne(v - static_cast<float>(hi));
+    }
+  }
+#pragma unroll
+  for (int m = kWave / 2; m > 0; m >>= 1) norm_sq += __shfl_xor(norm_sq, m);
+  if (lane == 0) {
+    // FP32 sum of H squares is within a relative H 2^-24 of the exact value;
+    // the factor covers that and the sqrt for any H <= 2^16
+    a.row_norm[r] = __fsqrt_rn(norm_sq) * (1.0f + 0x1p-7f);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// K2: gather
+// ---------------------------------------------------------------------------
+
+struct GatherShared {
+  float sc[kGatherTileMax];
+  float bd[kGatherTileMax];
+  uint32_t tk[kGatherTileMax];
+  uint32_t bad;
+};
+
+__device__ __forceinline__ float half_lane(const uint4& q, int k) {
+  const uint16_t* h = reinterpret_cast<const uint16_t*>(&q);
+  return half_to_float(h[k]);
+}
+
+// Fast scores, H known at compile time: G lanes per candidate, each lane
+// owning L = H / (8 G) 16-byte slices (slice i*G + lane: a group reads G*16
+// contiguous bytes per load); U candidates per group in flight.
+template <int H, int G, int U>
+__device__ void gather_scores_vec(const GatherArgs& a, const float* ys, GatherShared& sh,
+                                  uint32_t n) {
+  constexpr int L = H / (8 * G);
+  constexpr int kGroups = kThreads / G;
+  static_assert(L * 8 * G == H, "H must split into 16-byte lane slices");
+  const int lane = threadIdx.x % G;
+  const int grp = threadIdx.x / G;
+  float yv[L][8];
+#pragma unroll
+  for (int i = 0; i < L; ++i) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) yv[i][k] = ys[(i * G + lane) * 8 + k];
+  }
+  for (uint32_t base = 0; base < n; base += kGroups * U) {
+    uint4 ev[U][L];
+    bool ok[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t c = base + u * kGroups + grp;
+      ok[u] = c < n;
+      const uint32_t t = ok[u] ? sh.tk[c] : 0u;
+      const uint4* row = reinterpret_cast<const uint4*>(a.emb + static_cast<uint64_t>(t) * H) + lane;
+#pragma unroll
+      for (int i = 0; i < L; ++i) ev[u][i] = ok[u] ? row[i * G] : uint4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float acc = 0.0f;
+      float acca = 0.0f;
+#pragma unroll
+      for (int i = 0; i < L; ++i) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const float e = half_lane(ev[u][i], k);
+          acc = __builtin_fmaf(e, yv[i][k], acc);
+          acca = __builtin_fmaf(__builtin_fabsf(e), __builtin_fabsf(yv[i][k]), acca);
+        }
+      }
+#pragma unroll
+      for (int m = G / 2; m > 0; m >>= 1) {
+        acc += __shfl_xor(acc, m, G);
+        acca += __shfl_xor(acca, m, G);
+      }
+      const uint32_t c = base + u * kGroups + grp;
+      if (lane == 0 && ok[u]) {
+        sh.sc[c] = acc;
+        sh.bd[c] = __builtin_fmaf(a.coef, acca, a.slack);
+      }
+    }
+  }
+}
+
+// Fast scores for any H: one wave per candidate, element-strided.
+__device__ void gather_scores_generic(const GatherArgs& a, const float* ys, GatherShared& sh,
+                                      uint32_t n) {
+  const int lane = threadIdx.x % kWave;
+  const int w = threadIdx.x / kWave;
+  for (uint32_t c = w; c < n; c += kThreads / kWave) {
+    const uint16_t* row = a.emb + static_cast<uint64_t>(sh.tk[c]) * a.H;
+    float acc = 0.0f;
+    float acca = 0.0f;
+    for (uint32_t f = lane; f < a.H; f += kWave) {
+      const float e = half_to_float(row[f]);
+      acc = __builtin_fmaf(e, ys[f], acc);
+      acca = __builtin_fmaf(__builtin_fabsf(e), __builtin_fabsf(ys[f]), acca);
+    }
+#pragma unroll
+    for (int m = kWave / 2; m > 0; m >>= 1) {
+      acc += __shfl_xor(acc, m);
+      acca += __shfl_xor(acca, m);
+    }
+    if (lane == 0) {
+      sh.sc[c] = acc;
+      sh.bd[c] = __builtin_fmaf(a.coef, acca, a.slack);
+    }
+  }
+}
+
+// Scores already computed by the MFMA projection (the full-head comparator).
+__device__ void gather_scores_lookup(const GatherArgs& a, uint32_t r, GatherShared& sh,
+                                     uint32_t n) {
+  const float* srow = a.scores + static_cast<uint64_t>(r) * a.V;
+  const float yn = a.row_norm[r];
+  for (uint32_t c = threadIdx.x; c < n; c += kThreads) {
+    const uint32_t t = sh.tk[c];
+    sh.sc[c] = srow[t];
+    sh.bd[c] = __builtin_fmaf(a.tok_norm[t], __builtin_fmaf(a.coef, yn, a.coef2), a.slack);
+  }
+}
+
+template <ScoreSource kSrc, int kH, int kG>
+__global__ __launch_bounds__(kThreads) void gather_kernel(GatherArgs a) {
+  extern __shared__ float ys[];
+  __shared__ GatherShared sh;
+  const uint32_t r = blockIdx.x % a.rows;
+  const uint32_t k = blockIdx.x / a.rows;
+  const RowMeta meta = a.row_meta[r];
+  const bool lookup = kSrc == ScoreSource::kLookup;
+  if (!(meta.kind & kRowRestricted) && !(lookup && (meta.kind & kRowUnrestricted))) return;
+  const uint32_t begin = k * a.tile;
+  if (begin >= meta.count) return;
+  const uint32_t n = meta.count - begin < a.tile ? meta.count - begin : a.tile;
+  const bool virtual_list = meta.kind & kRowUnrestricted;
+
+  if (threadIdx.x == 0) sh.bad = 0u;
+  __syncthreads();
+  if constexpr (!lookup) {
+    for (uint32_t f = threadIdx.x; f < a.H; f += kThreads) {
+      ys[f] = a.y[static_cast<uint64_t>(r) * a.H + f];
+    }
+  }
+  uint32_t bad = 0u;
+  for (uint32_t c = threadIdx.x; c < n; c += kThreads) {
+    const uint32_t t = virtual_list ? begin + c : a.tokens[meta.list_begin + begin + c];
+    bad |= t >= a.V ? 1u : 0u;
+    sh.tk[c] = t < a.V ? t : 0u;
+  }
+  if (bad) atomicOr(&sh.bad, 1u);
+  __syncthreads();
+  const bool invalid = sh.bad != 0u;
+  if (!invalid) {
+    if constexpr (lookup) {
+      gather_scores_lookup(a, r, sh, n);
+    } else if constexpr (kH > 0) {
+      gather_scores_vec<kH, kG, 2>(a, ys, sh, n);
+    } else {
+      gather_scores_generic(a, ys, sh, n);
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x >= kWave) return;
+
+  // wave 0 summarizes the tile
+  const uint32_t lane = threadIdx.x;
+  TileRecord* rec = a.records + static_cast<uint64_t>(r) * a.max_tiles + k;
+  uint32_t fin = 1u;
+  float lo = -__builtin_huge_valf();
+  uint32_t mt = kInvalidToken;
+  uint32_t mp = 0u;
+  for (uint32_t c = lane; c < n; c += kWave) {
+    const float g = sh.sc[c];
+    const float b = sh.bd[c];
+    fin &= (__builtin_isfinite(g) && __builtin_isfinite(b) && b < 0x1p100f) ? 1u : 0u;
+    lo = __builtin_fmaxf(lo, g - b);
+    if (sh.tk[c] < mt) {
+      mt = sh.tk[c];
+      mp = begin + c;
+    }
+  }
+  const bool all_finite = wave_sum_u32(fin ^ 1u) == 0u;
+  const float L = wave_max(lo);
+  wave_min_token(mt, mp);
+  // members: candidates with g + b >= L, ranked in list order by ballot
+  const bool ordinary = all_finite && !invalid;
+  uint32_t total = 0u;
+  for (uint32_t c0 = 0; c0 < n; c0 += kWave) {
+    const uint32_t c = c0 + lane;
+    const bool member = ordinary && c < n && sh.sc[c] + sh.bd[c] >= L;
+    const uint64_t mask = __ballot(member);
+    if (member) {
+      const uint32_t rank = total + __popcll(mask & ((1ull << lane) - 1ull));
+      if (rank < kTileMembers) {
+        const float g = sh.sc[c];
+        const float b = sh.bd[c];
+        rec->m[rank] = TileMember{sh.tk[c], begin + c, g - b, g + b};
+      }
+    }
+    total += __popcll(mask);
+  }
+  if (lane == 0) {
+    uint32_t flags = 0u;
+    if (invalid) flags |= kTileInvalid;
+    if (!invalid && (!all_finite || total > kTileMembers)) flags |= kTileRescoreAll;
+    rec->best_lower = L;
+    rec->flags = flags;
+    rec->min_token = mt;
+    rec->min_pos = mp;
+    rec->begin = begin;
+    rec->count = n;
+    rec->n_members = flags ? 0u : total;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// K3: finalize
+// ---------------------------------------------------------------------------
+
+constexpr int kStage = 8;  // embedding rows staged in LDS per rescore pass
+
+// Reference-order chain over LDS-resident FP32 y and FP16 row (see
+// canonical_dot): same arithmetic, LDS reads issued a vector ahead.
+template <bool kMulAdd>
+__device__ float chain_lds(const float* ys, const uint16_t* row, uint32_t H) {
+  float s = 0.0f;
+  uint32_t f = 0;
+  if ((H & 7u) == 0) {
+    const uint4* e = reinterpret_cast<const uint4*>(row);
+    const float4* y = reinterpret_cast<const float4*>(ys);
+    const uint32_t n8 = H / 8;
+    uint4 ce = e[0];
+    float4 cy0 = y[0], cy1 = y[1];
+    for (uint32_t i = 0; i < n8; ++i) {
+      const uint32_t j = i + 1 < n8 ? i + 1 : i;
+      const uint4 ne = e[j];
+      const float4 ny0 = y[2 * j], ny1 = y[2 * j + 1];
+      const float yv[8] = {cy0.x, cy0.y, cy0.z, cy0.w, cy1.x, cy1.y, cy1.z, cy1.w};
+      const uint16_t* h = reinterpret_cast<const uint16_t*>(&ce);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) s = order_step<kMulAdd>(s, yv[k], half_to_float(h[k]));
+      ce = ne;
+      cy0 = ny0;
+      cy1 = ny1;
+    }
+    f = H;
+  }
+  for (; f < H; ++f) s = order_step<kMulAdd>(s, ys[f], half_to_float(row[f]));
+  return s;
+}
+
+constexpr uint32_t kCandMax = kWave * kTileMembers;
+
+struct FinalizeShared {
+  uint32_t cand_token[kCandMax];
+  uint32_t cand_pos[kCandMax];
+  uint32_t n_cand;
+  uint32_t token;
+  uint32_t pos;
+  float score;
+  uint32_t need_score;
+};
+
+// Rescores candidates cand_token[0..n) of one row in the reference order,
+// kStage rows at a time staged in LDS; returns the wave's best.
+__device__ Best rescore_candidates(const FinalizeArgs& a, const float* ys, uint16_t* es,
+                                   const FinalizeShared& sh, uint32_t n) {
+  const uint32_t lane = threadIdx.x;
+  const uint32_t H = a.H;
+  Best best = best_identity();
+  for (uint32_t base = 0; base < n; base += kStage) {
+    const uint32_t m = n - base < kStage ? n - base : kStage;
+    __syncthreads();
+    if ((H & 7u) == 0) {
+      const uint32_t per = H / 8;
+      for (uint32_t q = lane; q < m * per; q += kWave) {
+        const uint32_t j = q / per;
+        const uint32_t i = q % per;
+        reinterpret_cast<uint4*>(es + j * H)[i] =
+            reinterpret_cast<const uint4*>(a.emb + static_cast<uint64_t>(sh.cand_token[base + j]) * H)[i];
+      }
+    } else {
+      for (uint32_t q = lane; q < m * H; q += kWave) {
+        const uint32_t j = q / H;
+        es[q] = a.emb[static_cast<uint64_t>(sh.cand_token[base + j]) * H + (q % H)];
+      }
+    }
+    __syncthreads();
+    if (lane < m) {
+      const float s = a.order == 1 ? chain_lds<true>(ys, es + lane * H, H)
+                                   : chain_lds<false>(ys, es + lane * H, H);
+      best = best_of(best, best_leaf(s, sh.cand_token[base + lane], sh.cand_pos[base + lane]));
+    }
+  }
+  return wave_best(best);
+}
+
+__global__ __launch_bounds__(kWave) void finalize_kernel(FinalizeArgs a) {
+  extern __shared__ float lds[];
+  float* ys = lds;                                            // H floats
+  uint16_t* es = reinterpret_cast<uint16_t*>(lds + a.H);      // kStage rows
+  __shared__ FinalizeShared sh;
+  const uint32_t r = blockIdx.x;
+  const uint32_t lane = threadIdx.x;
+  const RowMeta meta = a.row_meta[r];
+  const TileRecord* recs;
+  uint32_t ntiles;
+  if (meta.kind & kRowRestricted) {
+    recs = a.records + static_cast<uint64_t>(r) * a.max_tiles;
+    ntiles = (meta.count + a.tile - 1) / a.tile;
+  } else if ((meta.kind & kRowUnrestricted) && a.fb_records != nullptr) {
+    const uint32_t m = a.fb_map[r];
+    if (m == kInvalidToken) return;
+    recs = a.fb_records + static_cast<uint64_t>(m) * a.fb_tiles;
+    ntiles = a.fb_tiles;
+  } else if ((meta.kind & kRowUnrestricted) && a.lookup_unrestricted) {
+    recs = a.records + static_cast<uint64_t>(r) * a.max_tiles;
+    ntiles = (meta.count + a.tile - 1) / a.tile;
+  } else {
+    return;
+  }
+  const bool virtual_list = meta.kind & kRowUnrestricted;
+  for (uint32_t f = lane; f < a.H; f += kWave) ys[f] = a.y[static_cast<uint64_t>(r) * a.H + f];
+
+  __syncthreads();
+  // pass 1: validity, the best lower bound of ordinary tiles, lowest id
+  uint32_t inv = 0u;
+  uint32_t any_all = 0u;
+  float lg = -__builtin_huge_valf();
+  uint32_t mt = kInvalidToken;
+  uint32_t mp = 0u;
+  for (uint32_t t = lane; t < ntiles; t += kWave) {
+    const TileRecord& q = recs[t];
+    inv |= (q.flags & kTileInvalid) ? 1u : 0u;
+    any_all |= (q.flags & kTileRescoreAll) ? 1u : 0u;
+    if (q.flags == 0u) lg = __builtin_fmaxf(lg, q.best_lower);
+    if (q.min_token < mt) {
+      mt = q.min_token;
+      mp = q.min_pos;
+    }
+  }
+  const bool invalid = wave_sum_u32(inv) != 0u;
+  if (invalid) {
+    // an id outside the vocabulary makes the row invalid (greedy.cu:163-166)
+    if (lane == 0) {
+      a.out_token[r] = kInvalidToken;
+      if (a.out_score != nullptr) a.out_score[r] = __builtin_nanf("");
+      if (a.out_next != nullptr) a.out_next[r] = kInvalidToken;
+    }
+    return;
+  }
+  const bool has_all = wave_sum_u32(any_all) != 0u;
+  lg = wave_max(lg);
+  wave_min_token(mt, mp);
+  __syncthreads();
+
+  // tiles that need every candidate rescored (non-finite values, crowded
+  // windows): exact scores, which then also bound the window
+  Best best = best_identity();
+  if (has_all) {
+    for (uint32_t t = 0; t < ntiles; ++t) {
+      const TileRecord& q = recs[t];
+      if (!(q.flags & kTileRescoreAll)) continue;
+      for (uint32_t c0 = 0; c0 < q.count; c0 += kWave) {
+        const uint32_t c = c0 + lane;
+        if (lane == 0) sh.n_cand = q.count - c0 < kWave ? q.count - c0 : kWave;
+        if (c < q.count) {
+          const uint32_t p = q.begin + c;
+          sh.cand_token[lane] = virtual_list ? p : a.tokens[meta.list_begin + p];
+          sh.cand_pos[lane] = p;
+        }
+        __syncthreads();
+        best = best_of(best, rescore_candidates(a, ys, es, sh, sh.n_cand));
+      }
+    }
+    if (best.token != kInvalidToken) lg = __builtin_fmaxf(lg, best.score);
+  }
+
+  // ordinary tiles: members whose upper bound reaches lg (at most
+  // kTileMembers per tile, so one pass over 64 tiles fits kCandMax)
+  for (uint32_t t0 = 0; t0 < ntiles; t0 += kWave) {
+    if (lane == 0) sh.n_cand = 0u;
+    __syncthreads();
+    const uint32_t t = t0 + lane;
+    if (t < ntiles) {
+      const TileRecord& q = recs[t];
+      if (q.flags == 0u) {
+        const uint32_t nm = q.n_members < kTileMembers ? q.n_members : kTileMembers;
+        for (uint32_t j = 0; j < nm; ++j) {
+          const TileMember mm = q.m[j];
+          if (mm.upper >= lg) {
+            const uint32_t slot = atomicAdd(&sh.n_cand, 1u);
+            sh.cand_token[slot] = mm.token;
+            sh.cand_pos[slot] = mm.pos;
+          }
+        }
+      }
+    }
+    __syncthreads();
+    const uint32_t nc = sh.n_cand;
+    if (nc > 0) best = best_of(best, rescore_candidates(a, ys, es, sh, nc));
+    __syncthreads();
+  }
+
+  if (lane == 0) {
+    sh.need_score = best.token == kInvalidToken ? 1u : 0u;
+    sh.token = sh.need_score ? mt : best.token;
+    sh.pos = sh.need_score ? mp : best.pos;
+    sh.score = best.score;
+  }
+  __syncthreads();
+  // a row whose scores are all NaN selects its lowest id (greedy.cu:206-211)
+  // and reports that id's reference-order score
+  const uint32_t token = sh.token;
+  const uint32_t pos = sh.pos;
+  float score = sh.score;
+  if (sh.need_score) {
+    const uint32_t H = a.H;
+    for (uint32_t q = lane; q < H; q += kWave) es[q] = a.emb[static_cast<uint64_t>(token) * H + q];
+    __syncthreads();
+    score = a.order == 1 ? chain_lds<true>(ys, es, H) : chain_lds<false>(ys, es, H);
+  }
+  if (lane == 0) {
+    uint32_t next = kInvalidToken;
+    if (virtual_list) {
+      next = kStateUnrestricted;
+    } else if (a.state_next != nullptr) {
+      next = a.state_next[meta.list_begin + pos];
+    } else if (a.next_table != nullptr) {
+      next = static_cast<uint32_t>(a.next_table[static_cast<uint64_t>(meta.state) * a.V + token]);
+    }
+    a.out_token[r] = token;
+    if (a.out_score != nullptr) a.out_score[r] = score;
+    if (a.out_next != nullptr) a.out_next[r] = next;
+  }
+}
+
+} // namespace
+
+hipError_t launch_tail_norm(const TailNormArgs& args, uint32_t rows, hipStream_t stream) {
+  const size_t lds = 2u * static_cast<size_t>(args.H) * sizeof(float);
+  hipLaunchKernelGGL(tail_norm_kernel, dim3(rows), dim3(kWave), lds, stream, args);
+  return hipGetLastError();
+}
+
+template <ScoreSource kSrc, int kH, int kG>
+static void launch_gather_variant(const GatherArgs& a, hipStream_t stream) {
+  const size_t lds = kSrc == ScoreSource::kLookup ? 0 : static_cast<size_t>(a.H) * sizeof(float);
+  hipLaunchKernelGGL((gather_kernel<kSrc, kH, kG>), dim3(a.rows * a.max_tiles), dim3(kThreads),
+                     lds, stream, a);
+}
+
+hipError_t launch_gather(ScoreSource source, const GatherArgs& a, hipStream_t stream) {
+  const bool aligned = (reinterpret_cast<uintptr_t>(a.emb) & 15u) == 0;
+  if (source == ScoreSource::kLookup) {
+    launch_gather_variant<ScoreSource::kLookup, 0, 64>(a, stream);
+  } else if (a.H == 576 && aligned) {
+    launch_gather_variant<ScoreSource::kDotF32, 576, 8>(a, stream);
+  } else if (a.H == 2048 && aligned) {
+    launch_gather_variant<ScoreSource::kDotF32, 2048, 32>(a, stream);
+  } else {
+    launch_gather_variant<ScoreSource::kDotF32, 0, 64>(a, stream);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_finalize(const FinalizeArgs& a, hipStream_t stream) {
+  const size_t lds = static_cast<size_t>(a.H) * sizeof(float) +
+                     static_cast<size_t>(kStage) * a.H * sizeof(uint16_t);
+  hipLaunchKernelGGL(finalize_kernel, dim3(a.rows), dim3(kWave), lds, stream, a);
+  return hipGetLastError();
+}
+
+} // namespace mf

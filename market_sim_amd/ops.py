@@ -218,5 +218,9 @@ def decode_tail_unrestricted(args: abi.DecodeTailArgs, stream: int) -> Status:
     return abi.lib().mf_decode_tail_unrestricted(ctypes.byref(args), stream)
 
 
+def decode_tail_finalize(args: abi.DecodeTailArgs, stream: int) -> Status:
+    return abi.lib().mf_decode_tail_finalize(ctypes.byref(args), stream)
+
+
 def decode_tail_full_f16(args: abi.DecodeTailArgs, stream: int) -> Status:
     return abi.lib().mf_decode_tail_full_f16(ctypes.byref(args), stream)
