@@ -5,6 +5,7 @@
 // src/cuda/linear.cu:40-81, src/cuda/device_buffer.cu:15-103), then launches.
 // Nothing here allocates device memory except mf_device_alloc itself, and
 // nothing synchronizes except mf_stream_synchronize.
+#include <atomic>
 #include <cmath>
 #include <cstdint>
 #include <cstring>
@@ -91,6 +92,22 @@ void mfma_bound_coefs(uint64_t H, float& coef, float& coef2) {
 // Absolute term for underflow: each of up to 2H operations may lose 2^-126.
 float underflow_slack(uint64_t H) {
   return static_cast<float>(4.0 * static_cast<double>(H) * std::ldexp(1.0, -126));
+}
+
+// Compute units of the current device (cached per device id).
+uint32_t device_cus() {
+  static std::atomic<int> cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0) {
+      n = 256;
+    }
+    cached[dev].store(n, std::memory_order_relaxed);
+  }
+  return static_cast<uint32_t>(n);
 }
 
 uint32_t head_chunk(uint64_t H, uint64_t max_count) {
@@ -388,7 +405,7 @@ mf_status mf_linear_f16(mf_buffer input, mf_buffer weight, mf_buffer output, uin
       input.address == output.address || weight.address == output.address) {
     return status(MF_INVALID_ARGUMENT);
   }
-  const bool mfma_shape = (input_features % 16u) == 0 && (input.address % 16u) == 0 &&
+  const bool mfma_shape = (input_features % 64u) == 0 && (input.address % 16u) == 0 &&
                           (weight.address % 16u) == 0 && output_features <= kU32Max &&
                           rows <= kU32Max;
   if (mfma_shape) {
@@ -440,10 +457,11 @@ mf_status validate_tail(const mf_decode_tail_args* a, bool full, TailLayout& L) 
       a->rows > kIntMax || a->unrestricted_count > a->rows) {
     return status(MF_RESOURCE_LIMIT);
   }
-  // limits of this build: the hidden row is staged in LDS (H <= 8192, and
-  // H % 16 == 0 for the MFMA K split), lists are at most the vocabulary
-  if (a->hidden > mf::kHeadMaxHidden || (a->hidden % 16u) != 0 || a->max_count > a->vocab ||
-      a->rows > 65535u) {
+  // limits of this build: the hidden row is staged in LDS (H <= 8192), the
+  // MFMA heads take K in chunks of 64 features, lists are at most the
+  // vocabulary
+  if (a->hidden > mf::kHeadMaxHidden || a->max_count > a->vocab || a->rows > 65535u ||
+      ((a->unrestricted_count > 0 || full) && (a->hidden % 64u) != 0)) {
     return status(MF_RESOURCE_LIMIT);
   }
   uint64_t xe = 0, ee = 0, te = 0;
@@ -564,6 +582,8 @@ mf::GatherArgs gather_args(const mf_decode_tail_args* a, const TailLayout& L, ch
   g.tile = L.tile;
   g.max_tiles = L.max_tiles;
   g.slack = underflow_slack(a->hidden);
+  // persistent workgroups: the launcher multiplies by the resident count
+  g.groups = device_cus();
   return g;
 }
 
@@ -730,6 +750,7 @@ mf_status mf_decode_tail_full_f16(const mf_decode_tail_args* args, uintptr_t str
   g.row_norm = reinterpret_cast<const float*>(ws + L.row_norm);
   g.tok_norm = tok_norm;
   mfma_bound_coefs(a->hidden, g.coef, g.coef2);
+  g.groups = device_cus();
   e = mf::launch_gather(ScoreSource::kLookup, g, s);
   if (e != hipSuccess) return launch_status(e);
   // 4. merge, reference-order rescore, DFA advance

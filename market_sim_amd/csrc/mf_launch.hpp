@@ -67,6 +67,7 @@ hipError_t launch_fill_zero(void* address, uint64_t bytes, hipStream_t stream);
 // ---- decode tail (mf_tail.hip) ----------------------------------------------
 
 constexpr uint32_t kGatherTileMax = 256;
+constexpr uint32_t kPlanRowsMax = 1024;  // rows the gather plans in LDS
 
 struct TailNormArgs {
   const float* x;          // [rows, H]
@@ -104,6 +105,7 @@ struct GatherArgs {
   uint32_t V;
   uint32_t tile;           // candidates per tile (<= kGatherTileMax)
   uint32_t max_tiles;
+  uint32_t groups;         // compute units for the planned mode (0 = grid mode)
   float coef;              // dot: b = coef * sum|y e| + slack
   float coef2;             // lookup: b = ||e|| (coef ||y|| + coef2) + slack
   float slack;

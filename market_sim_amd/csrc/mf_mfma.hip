@@ -7,18 +7,17 @@
 //
 // Tiling: a 256-thread workgroup owns 32 A rows (hidden vectors) x 128
 // tokens; each wave computes one 32x32 block with v_mfma_f32_32x32x16_f16.
+// K runs in chunks of 64 features.  Per chunk the workgroup stages the
+// 128 x 64 FP16 slice of E and the 32 x 64 A slice in LDS (double-buffered,
+// rows padded to 144 bytes so b128 reads are bank-conflict free): eight
+// consecutive lanes load one token's 128 contiguous bytes, so every HBM line
+// is fetched once, and the next chunk's global loads are in flight while the
+// current chunk's MFMAs run.
+//
 // FP32 hidden values enter as the FP16 pair hi = rne(y), lo = rne(y - hi)
 // (two MFMAs per step), so the fast score is accurate to ~2^-22 relative
 // before the reference-order rescore.
-//
-// K permutation: a dot product does not depend on which features the
-// hardware pairs in one step, only on A and B using the same pairing.  Lane
-// group g (lanes 32g..32g+31) supplies at step s the features g*H/2 + 8s..+7,
-// so each lane streams one contiguous half row of E.  A chunk of kChunk steps
-// has all its B fragments loaded into registers before its MFMAs.
 #include <hip/hip_runtime.h>
-
-#include <type_traits>
 
 #include "mf_device.hpp"
 #include "mf_launch.hpp"
@@ -32,15 +31,19 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 constexpr int kThreads = 256;
 constexpr int kTileTokens = 128;
 constexpr int kMTile = 32;
-constexpr int kMaxChunk = 18;
+constexpr int kKC = 64;          // features per chunk
+constexpr int kRowHalves = 72;   // padded LDS row: 64 + 8 halves = 144 B
 
 struct ProjShared {
   union {
-    half8_t a[2][2][kMaxChunk][kMTile];  // [hi|lo][group][step][row] 36,864 B
+    struct {
+      _Float16 b[2][kTileTokens][kRowHalves];   // 36,864 B
+      _Float16 a[2][2][kMTile][kRowHalves];     // [buf][hi|lo] 18,432 B
+    } k;
     struct {
       float g[kMTile][kTileTokens];
       float b[kMTile][kTileTokens];
-    } epi;                                // 32,768 B
+    } epi;                                      // 32,768 B
   };
 };
 
@@ -56,91 +59,107 @@ struct AView {
   uint32_t H;
 };
 
-__device__ __forceinline__ half8_t zero_half8() {
-  half8_t z;
-#pragma unroll
-  for (int k = 0; k < 8; ++k) z[k] = static_cast<_Float16>(0.0f);
-  return z;
-}
+// Per-thread registers holding one chunk in flight: 4 B pieces (16 B each)
+// and the A piece (hi and lo, 16 B each).
+struct ChunkRegs {
+  uint4 b[4];
+  uint4 ahi;
+  uint4 alo;
+};
 
-template <ASrc kA, int kChunk>
-__device__ void stage_a(const AView& A, uint32_t m0, uint32_t s0, ProjShared& sh) {
-  constexpr uint32_t kItems = 2u * kChunk * kMTile;
-  const uint32_t half_h = A.H / 2;
-  for (uint32_t q = threadIdx.x; q < kItems; q += kThreads) {
-    const uint32_t i = q % kMTile;
-    const uint32_t rest = q / kMTile;
-    const uint32_t s = rest % kChunk;
-    const uint32_t g = rest / kChunk;
-    const uint32_t f0 = g * half_h + 8u * (s0 + s);
-    const uint32_t row = m0 + i < A.m ? (A.row_index != nullptr ? A.row_index[m0 + i] : m0 + i)
-                                      : 0xFFFFFFFFu;
-    half8_t hi = zero_half8();
-    half8_t lo = zero_half8();
-    if (row < A.rows) {
-      const uint64_t o = static_cast<uint64_t>(row) * A.H + f0;
-      if constexpr (kA == ASrc::kF32Split) {
-        const float4* src = reinterpret_cast<const float4*>(A.y + o);
-        const float4 v0 = src[0];
-        const float4 v1 = src[1];
-        const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+template <ASrc kA>
+__device__ __forceinline__ void load_chunk(const AView& A, const uint16_t* emb, uint32_t V,
+                                           uint32_t tok0, uint32_t m0, uint32_t c,
+                                           ChunkRegs& r) {
+  const uint32_t t = threadIdx.x;
+  const uint32_t part = t % 8;
+  const uint32_t f = c * kKC + part * 8;
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          const _Float16 h = static_cast<_Float16>(v[k]);
-          hi[k] = h;
-          lo[k] = static_cast<_Float16>(v[k] - static_cast<float>(h));
-        }
-      } else {
-        hi = *reinterpret_cast<const half8_t*>(A.hi + o);
-        if constexpr (kA == ASrc::kF16Pair) lo = *reinterpret_cast<const half8_t*>(A.lo + o);
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t token = tok0 + t / 8 + 32 * j;
+    r.b[j] = token < V ? *reinterpret_cast<const uint4*>(emb + static_cast<uint64_t>(token) * A.H + f)
+                       : uint4{0u, 0u, 0u, 0u};
+  }
+  // A: 32 rows x 8 pieces = 256 pieces, one per thread
+  const uint32_t i = t / 8;
+  const uint32_t row = m0 + i < A.m ? (A.row_index != nullptr ? A.row_index[m0 + i] : m0 + i)
+                                    : 0xFFFFFFFFu;
+  r.ahi = uint4{0u, 0u, 0u, 0u};
+  r.alo = uint4{0u, 0u, 0u, 0u};
+  if (row < A.rows) {
+    const uint64_t o = static_cast<uint64_t>(row) * A.H + f;
+    if constexpr (kA == ASrc::kF32Split) {
+      const float4* src = reinterpret_cast<const float4*>(A.y + o);
+      const float4 v0 = src[0];
+      const float4 v1 = src[1];
+      const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+      half8_t hi, lo;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const _Float16 h = static_cast<_Float16>(v[k]);
+        hi[k] = h;
+        lo[k] = static_cast<_Float16>(v[k] - static_cast<float>(h));
       }
+      r.ahi = __builtin_bit_cast(uint4, hi);
+      r.alo = __builtin_bit_cast(uint4, lo);
+    } else {
+      r.ahi = *reinterpret_cast<const uint4*>(A.hi + o);
+      if constexpr (kA == ASrc::kF16Pair) r.alo = *reinterpret_cast<const uint4*>(A.lo + o);
     }
-    sh.a[0][g][s][i] = hi;
-    sh.a[1][g][s][i] = lo;
   }
 }
 
-// One 32x32 block per wave; returns the accumulator and the lane's sum of
-// squares of its B values (the token norm, combined across lane groups).
-template <ASrc kA, int kChunk>
+__device__ __forceinline__ void store_chunk(ProjShared& sh, int buf, const ChunkRegs& r) {
+  const uint32_t t = threadIdx.x;
+  const uint32_t part = t % 8;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    *reinterpret_cast<uint4*>(&sh.k.b[buf][t / 8 + 32 * j][part * 8]) = r.b[j];
+  }
+  *reinterpret_cast<uint4*>(&sh.k.a[buf][0][t / 8][part * 8]) = r.ahi;
+  *reinterpret_cast<uint4*>(&sh.k.a[buf][1][t / 8][part * 8]) = r.alo;
+}
+
+// The wave's 32 x 32 block (rows m0.., tokens tok0 + 32 * wave ..).  Returns
+// the accumulator and the lane's sum of squares of its B values; combined
+// across the two lane groups that is ||e_token||^2 of token lane % 32.
+template <ASrc kA>
 __device__ floatx16 project_block(const AView& A, const uint16_t* emb, uint32_t V,
-                                  uint32_t m0, uint32_t token, ProjShared& sh,
-                                  float& tok_sq) {
+                                  uint32_t m0, uint32_t tok0, ProjShared& sh, float& tok_sq) {
   const int lane = threadIdx.x % 64;
+  const int wave = threadIdx.x / 64;
   const int g = lane / 32;
   const int i = lane % 32;
-  const bool tok_ok = token < V;
-  const uint32_t H = A.H;
-  const uint16_t* brow = emb + static_cast<uint64_t>(tok_ok ? token : 0u) * H +
-                         static_cast<uint64_t>(g) * (H / 2);
   floatx16 acc;
 #pragma unroll
   for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
   tok_sq = 0.0f;
-  const uint32_t steps = H / 16;
-  for (uint32_t s0 = 0; s0 < steps; s0 += kChunk) {
-    half8_t b[kChunk];
+  const uint32_t chunks = A.H / kKC;
+  ChunkRegs regs;
+  load_chunk<kA>(A, emb, V, tok0, m0, 0, regs);
+  store_chunk(sh, 0, regs);
+  __syncthreads();
+  for (uint32_t c = 0; c < chunks; ++c) {
+    const int buf = c & 1;
+    if (c + 1 < chunks) load_chunk<kA>(A, emb, V, tok0, m0, c + 1, regs);
 #pragma unroll
-    for (int s = 0; s < kChunk; ++s) {
-      b[s] = tok_ok ? *reinterpret_cast<const half8_t*>(brow + 8u * (s0 + s)) : zero_half8();
-    }
-    __syncthreads();
-    stage_a<kA, kChunk>(A, m0, s0, sh);
-    __syncthreads();
-#pragma unroll
-    for (int s = 0; s < kChunk; ++s) {
+    for (int s = 0; s < kKC / 16; ++s) {
+      const half8_t b = *reinterpret_cast<const half8_t*>(&sh.k.b[buf][wave * 32 + i][s * 16 + g * 8]);
+      const half8_t ahi = *reinterpret_cast<const half8_t*>(&sh.k.a[buf][0][i][s * 16 + g * 8]);
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
-        const float e = static_cast<float>(b[s][k]);
+        const float e = static_cast<float>(b[k]);
         tok_sq = __builtin_fmaf(e, e, tok_sq);
       }
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(sh.a[0][g][s][i], b[s], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ahi, b, acc, 0, 0, 0);
       if constexpr (kA != ASrc::kF16) {
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(sh.a[1][g][s][i], b[s], acc, 0, 0, 0);
+        const half8_t alo = *reinterpret_cast<const half8_t*>(&sh.k.a[buf][1][i][s * 16 + g * 8]);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(alo, b, acc, 0, 0, 0);
       }
     }
+    if (c + 1 < chunks) store_chunk(sh, buf ^ 1, regs);
+    __syncthreads();
   }
-  __syncthreads();
   tok_sq += __shfl_xor(tok_sq, 32);
   return acc;
 }
@@ -151,16 +170,17 @@ __device__ __forceinline__ int acc_row(int v, int lane) {
   return 8 * (v / 4) + 4 * (lane / 32) + (v % 4);
 }
 
-template <ASrc kA, int kChunk>
+template <ASrc kA>
 __global__ __launch_bounds__(kThreads) void projection_kernel(ProjArgs p) {
   __shared__ ProjShared sh;
   const uint32_t m0 = blockIdx.y * kMTile;
   const int lane = threadIdx.x % 64;
   const int wave = threadIdx.x / 64;
-  const uint32_t token = blockIdx.x * kTileTokens + wave * 32 + (lane % 32);
+  const uint32_t tok0 = blockIdx.x * kTileTokens;
+  const uint32_t token = tok0 + wave * 32 + (lane % 32);
   const AView A{p.y, p.a16, nullptr, p.row_index, p.m, p.rows, p.H};
   float tok_sq;
-  const floatx16 acc = project_block<kA, kChunk>(A, p.emb, p.V, m0, token, sh, tok_sq);
+  const floatx16 acc = project_block<kA>(A, p.emb, p.V, m0, tok0, sh, tok_sq);
   if (token >= p.V) return;
   if (p.tok_norm != nullptr && blockIdx.y == 0 && lane < 32) {
     p.tok_norm[token] = __fsqrt_rn(tok_sq) * (1.0f + 0x1p-7f);
@@ -188,7 +208,6 @@ __device__ __forceinline__ uint32_t group8_and(uint32_t v) {
   return v;
 }
 
-template <int kChunk>
 __global__ __launch_bounds__(kThreads) void fallback_kernel(FallbackArgs f) {
   __shared__ ProjShared sh;
   const uint32_t tile = blockIdx.x;
@@ -196,17 +215,17 @@ __global__ __launch_bounds__(kThreads) void fallback_kernel(FallbackArgs f) {
   const uint32_t tiles = gridDim.x;
   const int lane = threadIdx.x % 64;
   const int wave = threadIdx.x / 64;
-  const uint32_t token = tile * kTileTokens + wave * 32 + (lane % 32);
+  const uint32_t tok0 = tile * kTileTokens;
   const AView A{nullptr, f.y_hi, f.y_lo, f.row_index, f.m, f.rows, f.H};
   float tok_sq;
-  const floatx16 acc = project_block<ASrc::kF16Pair, kChunk>(A, f.emb, f.V, m0, token, sh, tok_sq);
+  const floatx16 acc = project_block<ASrc::kF16Pair>(A, f.emb, f.V, m0, tok0, sh, tok_sq);
 
   if (tile == 0 && threadIdx.x < kMTile && m0 + threadIdx.x < f.m) {
     const uint32_t row = f.row_index[m0 + threadIdx.x];
     if (row < f.rows) f.fb_map[row] = m0 + threadIdx.x;
   }
 
-  // scores and bounds into LDS (the A staging area is free after the loop)
+  // scores and bounds into LDS (the staging area is free after the loop)
   const float tok_norm = __fsqrt_rn(tok_sq) * (1.0f + 0x1p-7f);
 #pragma unroll
   for (int v = 0; v < 16; ++v) {
@@ -225,7 +244,6 @@ __global__ __launch_bounds__(kThreads) void fallback_kernel(FallbackArgs f) {
   // per row (8 lanes, 16 tokens each): the tile's window record
   const uint32_t i = threadIdx.x / 8;
   const uint32_t sub = threadIdx.x % 8;
-  const uint32_t tok0 = tile * kTileTokens;
   const uint32_t nt = f.V - tok0 < kTileTokens ? f.V - tok0 : kTileTokens;
   uint32_t fin = 1u;
   float lo = -__builtin_huge_valf();
@@ -273,16 +291,6 @@ __global__ __launch_bounds__(kThreads) void fallback_kernel(FallbackArgs f) {
   }
 }
 
-// Largest supported chunk that divides the step count.
-template <typename F>
-hipError_t with_chunk(uint32_t steps, F&& launch) {
-  if (steps % 18 == 0) return launch(std::integral_constant<int, 18>{});
-  if (steps % 16 == 0) return launch(std::integral_constant<int, 16>{});
-  if (steps % 8 == 0) return launch(std::integral_constant<int, 8>{});
-  if (steps % 4 == 0) return launch(std::integral_constant<int, 4>{});
-  return launch(std::integral_constant<int, 1>{});
-}
-
 } // namespace
 
 uint32_t fallback_tiles(uint32_t vocab) {
@@ -290,27 +298,22 @@ uint32_t fallback_tiles(uint32_t vocab) {
 }
 
 hipError_t launch_projection(const ProjArgs& args, hipStream_t stream) {
+  if (args.H % kKC != 0) return hipErrorInvalidValue;
   const dim3 grid(fallback_tiles(args.V), (args.m + kMTile - 1) / kMTile);
-  return with_chunk(args.H / 16, [&](auto chunk) {
-    constexpr int C = decltype(chunk)::value;
-    if (args.a16 != nullptr) {
-      hipLaunchKernelGGL((projection_kernel<ASrc::kF16, C>), grid, dim3(kThreads), 0, stream, args);
-    } else {
-      hipLaunchKernelGGL((projection_kernel<ASrc::kF32Split, C>), grid, dim3(kThreads), 0, stream,
-                         args);
-    }
-    return hipGetLastError();
-  });
+  if (args.a16 != nullptr) {
+    hipLaunchKernelGGL((projection_kernel<ASrc::kF16>), grid, dim3(kThreads), 0, stream, args);
+  } else {
+    hipLaunchKernelGGL((projection_kernel<ASrc::kF32Split>), grid, dim3(kThreads), 0, stream, args);
+  }
+  return hipGetLastError();
 }
 
 hipError_t launch_fallback(const FallbackArgs& args, hipStream_t stream) {
   if (args.m == 0) return hipSuccess;
+  if (args.H % kKC != 0) return hipErrorInvalidValue;
   const dim3 grid(fallback_tiles(args.V), (args.m + kMTile - 1) / kMTile);
-  return with_chunk(args.H / 16, [&](auto chunk) {
-    constexpr int C = decltype(chunk)::value;
-    hipLaunchKernelGGL((fallback_kernel<C>), grid, dim3(kThreads), 0, stream, args);
-    return hipGetLastError();
-  });
+  hipLaunchKernelGGL(fallback_kernel, grid, dim3(kThreads), 0, stream, args);
+  return hipGetLastError();
 }
 
 } // namespace mf

@@ -34,17 +34,22 @@ constexpr int kThreads = 256;
 __device__ float sequential_sum(const float* sq, uint32_t H) {
   float s = 0.0f;
   uint32_t c = 0;
-  if ((H & 3u) == 0) {
+  if ((H & 15u) == 0) {
+    // 16 values per step; the next 16 are read while these are added
     const float4* q = reinterpret_cast<const float4*>(sq);
-    const uint32_t n4 = H / 4;
-    float4 cur = q[0];
-    for (uint32_t i = 0; i < n4; ++i) {
-      const float4 nxt = q[i + 1 < n4 ? i + 1 : i];
-      s = s + cur.x;
-      s = s + cur.y;
-      s = s + cur.z;
-      s = s + cur.w;
-      cur = nxt;
+    const uint32_t n16 = H / 16;
+    float4 c0 = q[0], c1 = q[1], c2 = q[2], c3 = q[3];
+    for (uint32_t i = 0; i < n16; ++i) {
+      const uint32_t j = (i + 1 < n16 ? i + 1 : i) * 4;
+      const float4 n0 = q[j], n1 = q[j + 1], n2 = q[j + 2], n3 = q[j + 3];
+      const float v[16] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w,
+                           c2.x, c2.y, c2.z, c2.w, c3.x, c3.y, c3.z, c3.w};
+#pragma unroll
+      for (int k = 0; k < 16; ++k) s = s + v[k];
+      c0 = n0;
+      c1 = n1;
+      c2 = n2;
+      c3 = n3;
     }
     c = H;
   }
@@ -68,22 +73,24 @@ __global__ __launch_bounds__(kWave) void tail_norm_kernel(TailNormArgs a) {
   __syncthreads();
   RowMeta meta{0u, 0u, 0u, kRowInvalid};
   if (lane == 0) {
+    // metadata loads first: they resolve while the serial sum runs
+    const uint32_t s = a.row_state[r];
+    uint32_t b = 0u, e = 0u;
+    if (s < a.states) {
+      b = a.offsets[s];
+      e = a.offsets[s + 1];
+    }
     if (a.weight != nullptr) {
       const float sum_squares = sequential_sum(sq, H);
       const float mean = div_rn(sum_squares, static_cast<float>(H));
       inverse_shared = div_rn(1.0f, sqrt_rn(mean + a.epsilon));
     }
-    const uint32_t s = a.row_state[r];
     meta.state = s;
     if (s == kStateUnrestricted) {
       meta.kind = kRowUnrestricted;
       meta.count = a.V;
-    } else if (s < a.states) {
-      const uint32_t b = a.offsets[s];
-      const uint32_t e = a.offsets[s + 1];
-      if (e > b && e <= a.nnz && e - b <= a.max_count) {
-        meta = RowMeta{b, e - b, s, kRowRestricted};
-      }
+    } else if (s < a.states && e > b && e <= a.nnz && e - b <= a.max_count) {
+      meta = RowMeta{b, e - b, s, kRowRestricted};
     }
     a.row_meta[r] = meta;
     if (meta.kind != kRowRestricted) {
@@ -232,36 +239,31 @@ __device__ void gather_scores_lookup(const GatherArgs& a, uint32_t r, GatherShar
   }
 }
 
+// One tile: candidates [k*tile, k*tile + n) of row r's list.  All threads
+// call; wave 0 writes the record.  ys keeps row `staged`'s hidden vector.
 template <ScoreSource kSrc, int kH, int kG>
-__global__ __launch_bounds__(kThreads) void gather_kernel(GatherArgs a) {
-  extern __shared__ float ys[];
-  __shared__ GatherShared sh;
-  const uint32_t r = blockIdx.x % a.rows;
-  const uint32_t k = blockIdx.x / a.rows;
-  const RowMeta meta = a.row_meta[r];
-  const bool lookup = kSrc == ScoreSource::kLookup;
-  if (!(meta.kind & kRowRestricted) && !(lookup && (meta.kind & kRowUnrestricted))) return;
+__device__ void gather_tile(const GatherArgs& a, uint32_t r, uint32_t k, uint32_t list_begin,
+                            uint32_t count, bool virtual_list, float* ys, GatherShared& sh,
+                            uint32_t& staged) {
+  constexpr bool lookup = kSrc == ScoreSource::kLookup;
   const uint32_t begin = k * a.tile;
-  if (begin >= meta.count) return;
-  const uint32_t n = meta.count - begin < a.tile ? meta.count - begin : a.tile;
-  const bool virtual_list = meta.kind & kRowUnrestricted;
-
-  if (threadIdx.x == 0) sh.bad = 0u;
-  __syncthreads();
+  const uint32_t n = count - begin < a.tile ? count - begin : a.tile;
+  __syncthreads();  // the previous tile is done with sh and ys
   if constexpr (!lookup) {
-    for (uint32_t f = threadIdx.x; f < a.H; f += kThreads) {
-      ys[f] = a.y[static_cast<uint64_t>(r) * a.H + f];
+    if (staged != r) {
+      for (uint32_t f = threadIdx.x; f < a.H; f += kThreads) {
+        ys[f] = a.y[static_cast<uint64_t>(r) * a.H + f];
+      }
+      staged = r;
     }
   }
   uint32_t bad = 0u;
   for (uint32_t c = threadIdx.x; c < n; c += kThreads) {
-    const uint32_t t = virtual_list ? begin + c : a.tokens[meta.list_begin + begin + c];
+    const uint32_t t = virtual_list ? begin + c : a.tokens[list_begin + begin + c];
     bad |= t >= a.V ? 1u : 0u;
     sh.tk[c] = t < a.V ? t : 0u;
   }
-  if (bad) atomicOr(&sh.bad, 1u);
-  __syncthreads();
-  const bool invalid = sh.bad != 0u;
+  const bool invalid = __syncthreads_or(bad) != 0;
   if (!invalid) {
     if constexpr (lookup) {
       gather_scores_lookup(a, r, sh, n);
@@ -325,6 +327,93 @@ __global__ __launch_bounds__(kThreads) void gather_kernel(GatherArgs a) {
   }
 }
 
+__device__ __forceinline__ bool gathered(const RowMeta& m, bool lookup) {
+  return (m.kind & kRowRestricted) || (lookup && (m.kind & kRowUnrestricted));
+}
+
+// Grid mode (any number of rows): blockIdx.x = k * rows + r.
+template <ScoreSource kSrc, int kH, int kG>
+__global__ __launch_bounds__(kThreads) void gather_kernel(GatherArgs a) {
+  extern __shared__ float ys[];
+  __shared__ GatherShared sh;
+  const uint32_t r = blockIdx.x % a.rows;
+  const uint32_t k = blockIdx.x / a.rows;
+  const RowMeta meta = a.row_meta[r];
+  if (!gathered(meta, kSrc == ScoreSource::kLookup) || k * a.tile >= meta.count) return;
+  uint32_t staged = kInvalidToken;
+  gather_tile<kSrc, kH, kG>(a, r, k, meta.list_begin, meta.count,
+                            (meta.kind & kRowUnrestricted) != 0, ys, sh, staged);
+}
+
+// Planned mode (rows <= kPlanRowsMax): every workgroup reads all row
+// metadata, scans the tile counts in LDS (the same prefix in every
+// workgroup, so no workgroup waits on another) and walks its contiguous
+// range [W*b/G, W*(b+1)/G) of the W tiles -- no idle workgroups, and
+// consecutive tiles of one row reuse the staged hidden vector.
+template <ScoreSource kSrc, int kH, int kG>
+__global__ __launch_bounds__(kThreads) void gather_planned_kernel(GatherArgs a) {
+  extern __shared__ float ys[];
+  __shared__ GatherShared sh;
+  __shared__ uint32_t prefix[kPlanRowsMax + 1];
+  __shared__ uint32_t pbegin[kPlanRowsMax];
+  __shared__ uint32_t pcount[kPlanRowsMax];
+  __shared__ uint32_t pkind[kPlanRowsMax];
+  __shared__ uint32_t wave_total[kThreads / kWave];
+  constexpr bool lookup = kSrc == ScoreSource::kLookup;
+  const uint32_t rows = a.rows;
+  const uint32_t tid = threadIdx.x;
+  for (uint32_t r = tid; r < rows; r += kThreads) {
+    const RowMeta m = a.row_meta[r];
+    const bool use = gathered(m, lookup);
+    pbegin[r] = m.list_begin;
+    pcount[r] = use ? m.count : 0u;
+    pkind[r] = m.kind;
+    prefix[r + 1] = use ? (m.count + a.tile - 1) / a.tile : 0u;
+  }
+  __syncthreads();
+  // in-place inclusive scan of prefix[1..rows]: thread segments + block scan
+  const uint32_t seg = (rows + kThreads - 1) / kThreads;
+  const uint32_t s0 = tid * seg < rows ? tid * seg : rows;
+  const uint32_t s1 = s0 + seg < rows ? s0 + seg : rows;
+  uint32_t local = 0u;
+  for (uint32_t i = s0; i < s1; ++i) local += prefix[i + 1];
+  uint32_t incl = local;
+  const uint32_t lane = tid % kWave;
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const uint32_t o = __shfl_up(incl, d);
+    if (static_cast<int>(lane) >= d) incl += o;
+  }
+  if (lane == kWave - 1) wave_total[tid / kWave] = incl;
+  __syncthreads();
+  uint32_t run = incl - local;
+  for (uint32_t w = 0; w < tid / kWave; ++w) run += wave_total[w];
+  for (uint32_t i = s0; i < s1; ++i) {
+    run += prefix[i + 1];
+    prefix[i + 1] = run;
+  }
+  if (tid == 0) prefix[0] = 0u;
+  __syncthreads();
+  const uint64_t W = prefix[rows];
+  const uint64_t G = gridDim.x;
+  const uint32_t w0 = static_cast<uint32_t>(W * blockIdx.x / G);
+  const uint32_t w1 = static_cast<uint32_t>(W * (blockIdx.x + 1) / G);
+  if (w0 >= w1) return;
+  // the row holding tile w0: largest r with prefix[r] <= w0 < prefix[r + 1]
+  uint32_t lo = 0u, hi = rows;
+  while (lo < hi) {
+    const uint32_t mid = (lo + hi) / 2;
+    if (prefix[mid + 1] <= w0) lo = mid + 1; else hi = mid;
+  }
+  uint32_t r = lo;
+  uint32_t staged = kInvalidToken;
+  for (uint32_t w = w0; w < w1; ++w) {
+    while (prefix[r + 1] <= w) ++r;
+    gather_tile<kSrc, kH, kG>(a, r, w - prefix[r], pbegin[r], pcount[r],
+                              (pkind[r] & kRowUnrestricted) != 0, ys, sh, staged);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // K3: finalize
 // ---------------------------------------------------------------------------
@@ -361,7 +450,7 @@ __device__ float chain_lds(const float* ys, const uint16_t* row, uint32_t H) {
   return s;
 }
 
-constexpr uint32_t kCandMax = kWave * kTileMembers;
+constexpr uint32_t kCandMax = 2 * kWave * kTileMembers;
 
 struct FinalizeShared {
   uint32_t cand_token[kCandMax];
@@ -489,10 +578,10 @@ __global__ __launch_bounds__(kWave) void finalize_kernel(FinalizeArgs a) {
   }
 
   // ordinary tiles: members whose upper bound reaches lg (at most
-  // kTileMembers per tile, so one pass over 64 tiles fits kCandMax)
+  // kTileMembers per tile); collected over all tiles, then rescored together
+  if (lane == 0) sh.n_cand = 0u;
+  __syncthreads();
   for (uint32_t t0 = 0; t0 < ntiles; t0 += kWave) {
-    if (lane == 0) sh.n_cand = 0u;
-    __syncthreads();
     const uint32_t t = t0 + lane;
     if (t < ntiles) {
       const TileRecord& q = recs[t];
@@ -510,8 +599,13 @@ __global__ __launch_bounds__(kWave) void finalize_kernel(FinalizeArgs a) {
     }
     __syncthreads();
     const uint32_t nc = sh.n_cand;
-    if (nc > 0) best = best_of(best, rescore_candidates(a, ys, es, sh, nc));
-    __syncthreads();
+    // flush when the next sweep could overflow the buffer, and at the end
+    if (nc > 0 && (nc > kCandMax - kWave * kTileMembers || t0 + kWave >= ntiles)) {
+      best = best_of(best, rescore_candidates(a, ys, es, sh, nc));
+      __syncthreads();
+      if (lane == 0) sh.n_cand = 0u;
+      __syncthreads();
+    }
   }
 
   if (lane == 0) {
@@ -558,8 +652,27 @@ hipError_t launch_tail_norm(const TailNormArgs& args, uint32_t rows, hipStream_t
 template <ScoreSource kSrc, int kH, int kG>
 static void launch_gather_variant(const GatherArgs& a, hipStream_t stream) {
   const size_t lds = kSrc == ScoreSource::kLookup ? 0 : static_cast<size_t>(a.H) * sizeof(float);
-  hipLaunchKernelGGL((gather_kernel<kSrc, kH, kG>), dim3(a.rows * a.max_tiles), dim3(kThreads),
-                     lds, stream, a);
+  const uint64_t slots = static_cast<uint64_t>(a.rows) * a.max_tiles;
+  if (a.rows <= kPlanRowsMax && a.groups > 0) {
+    // persistent grid: compute units x resident workgroups of this variant
+    static int resident = 0;
+    if (resident == 0) {
+      int n = 0;
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+              &n, reinterpret_cast<const void*>(gather_planned_kernel<kSrc, kH, kG>), kThreads,
+              lds) != hipSuccess || n <= 0) {
+        n = 2;
+      }
+      resident = n;
+    }
+    const uint64_t want = static_cast<uint64_t>(a.groups) * static_cast<uint64_t>(resident);
+    const uint32_t g = static_cast<uint32_t>(slots < want ? slots : want);
+    hipLaunchKernelGGL((gather_planned_kernel<kSrc, kH, kG>), dim3(g), dim3(kThreads), lds,
+                       stream, a);
+  } else {
+    hipLaunchKernelGGL((gather_kernel<kSrc, kH, kG>), dim3(static_cast<uint32_t>(slots)),
+                       dim3(kThreads), lds, stream, a);
+  }
 }
 
 hipError_t launch_gather(ScoreSource source, const GatherArgs& a, hipStream_t stream) {
