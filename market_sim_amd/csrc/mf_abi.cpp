@@ -443,7 +443,13 @@ bool optional_is(const mf_buffer& b, uint64_t bytes) {
   return b.address == 0 || b.bytes == bytes;
 }
 
-uint32_t gather_tile(uint64_t H) { return H == 2048 ? 128u : 64u; }
+// The restricted gather runs on MFMA when H is a multiple of the 32-feature
+// MFMA step (64-candidate wave tiles); otherwise on the VALU dot.
+bool mfma_gather(uint64_t H) { return H % 32u == 0; }
+uint32_t gather_tile(uint64_t H) {
+  if (mfma_gather(H)) return mf::kGatherWaveTile;
+  return H == 2048 ? 128u : 64u;
+}
 
 // Validation common to both decode-tail entry points; fills the layout.
 mf_status validate_tail(const mf_decode_tail_args* a, bool full, TailLayout& L) {
@@ -523,8 +529,9 @@ mf_status validate_tail(const mf_decode_tail_args* a, bool full, TailLayout& L) 
   L.y = take(xe * 4u);
   L.row_norm = take(rows * 4u);
   L.row_meta = take(rows * sizeof(mf::RowMeta));
-  L.y_hi = take(fb_rows > 0 ? xe * 2u : 0u);
-  L.y_lo = take(fb_rows > 0 ? xe * 2u : 0u);
+  const bool split = fb_rows > 0 || (!full && mfma_gather(a->hidden));
+  L.y_hi = take(split ? xe * 2u : 0u);
+  L.y_lo = take(split ? xe * 2u : 0u);
   L.fb_map = take(rows * 4u);
   L.records = take(rows * L.max_tiles * sizeof(mf::TileRecord));
   L.fb_records = take(fb_rows * L.fb_tiles * sizeof(mf::TileRecord));
@@ -628,13 +635,22 @@ mf_status decode_tail_stage(const mf_decode_tail_args* args, uintptr_t stream, S
   hipError_t e = hipSuccess;
   switch (stage) {
     case Stage::kPrepare:
-      e = mf::launch_tail_norm(norm_args(a, L, ws, a->unrestricted_count > 0),
+      e = mf::launch_tail_norm(norm_args(a, L, ws, a->unrestricted_count > 0 ||
+                                                       mfma_gather(a->hidden)),
                                static_cast<uint32_t>(a->rows), s);
       break;
     case Stage::kRestricted: {
       mf::GatherArgs g = gather_args(a, L, ws);
-      g.coef = dot_bound_coef(a->hidden);
-      e = mf::launch_gather(ScoreSource::kDotF32, g, s);
+      if (mfma_gather(a->hidden)) {
+        g.y_hi = reinterpret_cast<const uint16_t*>(ws + L.y_hi);
+        g.y_lo = reinterpret_cast<const uint16_t*>(ws + L.y_lo);
+        g.row_norm = reinterpret_cast<const float*>(ws + L.row_norm);
+        mfma_bound_coefs(a->hidden, g.coef, g.coef2);
+        e = mf::launch_gather(ScoreSource::kMfma, g, s);
+      } else {
+        g.coef = dot_bound_coef(a->hidden);
+        e = mf::launch_gather(ScoreSource::kDotF32, g, s);
+      }
       break;
     }
     case Stage::kUnrestricted: {

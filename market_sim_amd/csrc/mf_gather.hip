@@ -1,0 +1,256 @@
+// The restricted gather on the matrix cores (restricted stage of
+// mf_decode_tail_f16 when H % 32 == 0).
+//
+// A wave owns one tile: up to 64 consecutive candidates of one row's list,
+// the granularity of the window records the finalize kernel merges.  It
+// scores them 16 at a time with v_mfma_f32_16x16x32_f16:
+//
+//   scores  A = [y_hi; y_lo; 0 ...] (16 x 32)  x  B = 16 embedding rows
+//           -> D[0][t] + D[1][t] = y . e_t with the FP32 y split into the
+//              FP16 pair hi = rne(y), lo = rne(y - hi)
+//   norms   A = B = the same 16 embedding rows
+//           -> the Gram diagonal D[t][t] = ||e_t||^2 (FP16 products are exact
+//              in FP32), which bounds the error of both the fast score and
+//              the reference-order score (Cauchy-Schwarz)
+//
+// The operand registers are filled straight from HBM: in the 16x16x32 layout
+// lane l holds 8 consecutive features of column l % 16 at k-block l / 16, so
+// the four lanes of one token read 64 contiguous bytes per step and the next
+// step the rest of the 128-byte line.  No LDS, no barriers after the plan:
+// the loads of the next (block, chunk) unit are in flight while the current
+// unit's MFMAs run, and waves never wait on one another.
+#include <hip/hip_runtime.h>
+
+#include "mf_device.hpp"
+#include "mf_launch.hpp"
+#include "mf_plan.hpp"
+
+namespace mf {
+namespace {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / kWave;
+constexpr uint32_t kBlock = 16;  // tokens per MFMA block
+constexpr uint32_t kStep = 32;   // features per MFMA step
+
+// One unit: KC steps of the A and B operands of one block.
+template <int KC>
+struct Operands {
+  half8_t a[KC];
+  half8_t b[KC];
+};
+
+template <int KC>
+__device__ __forceinline__ void load_unit(const uint16_t* brow, const uint16_t* arow,
+                                          bool a_live, uint32_t f0, Operands<KC>& o) {
+#pragma unroll
+  for (int s = 0; s < KC; ++s) {
+    o.b[s] = *reinterpret_cast<const half8_t*>(brow + f0 + s * kStep);
+  }
+#pragma unroll
+  for (int s = 0; s < KC; ++s) {
+    o.a[s] = a_live ? *reinterpret_cast<const half8_t*>(arow + f0 + s * kStep)
+                    : half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+  }
+}
+
+template <int KC>
+__device__ __forceinline__ void mma_unit(const Operands<KC>& o, floatx4& sc, floatx4& gram) {
+#pragma unroll
+  for (int s = 0; s < KC; ++s) {
+    sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.a[s], o.b[s], sc, 0, 0, 0);
+    gram = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.b[s], o.b[s], gram, 0, 0, 0);
+  }
+}
+
+// Block j done: lane 16 j + c takes column c's score and squared norm.  In
+// the 16x16 output layout lane s holds D[4 (s / 16) + i][s % 16], i < 4: the
+// score parts D[0][c], D[1][c] sit in lane c, the diagonal D[c][c] in lane
+// c + 16 (c / 4), element c % 4.
+__device__ __forceinline__ void finish_block(uint32_t j, uint32_t lane, floatx4& sc,
+                                             floatx4& gram, float& g_mine, float& sq_mine) {
+  const uint32_t col = lane % kBlock;
+  const float g = sc[0] + sc[1];
+  const uint32_t e = col % 4u;
+  const float d = e == 0u ? gram[0] : (e == 1u ? gram[1] : (e == 2u ? gram[2] : gram[3]));
+  const float gv = __shfl(g, static_cast<int>(col));
+  const float dv = __shfl(d, static_cast<int>(col + kBlock * (col / 4u)));
+  if (lane / kBlock == j) {
+    g_mine = gv;
+    sq_mine = dv;
+  }
+  sc = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  gram = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+}
+
+// Tile k of row r: candidates [64 k, 64 k + n) of the row's list.
+template <int KC>
+__device__ void mfma_tile(const GatherArgs& a, uint32_t r, uint32_t k, uint32_t list_begin,
+                          uint32_t count) {
+  const uint32_t lane = threadIdx.x % kWave;
+  const uint32_t begin = k * kGatherWaveTile;
+  const uint32_t n = count - begin < kGatherWaveTile ? count - begin : kGatherWaveTile;
+  const bool live = lane < n;
+  const uint32_t t = live ? a.tokens[list_begin + begin + lane] : 0u;
+  const float yn = a.row_norm[r];
+  TileRecord* rec = a.records + static_cast<uint64_t>(r) * a.max_tiles + k;
+  if (__ballot(live && t >= a.V) != 0ull) {
+    // an id outside the vocabulary: the row's result is the invalid sentinel
+    if (lane == 0) {
+      rec->best_lower = -__builtin_huge_valf();
+      rec->flags = kTileInvalid;
+      rec->min_token = kInvalidToken;
+      rec->min_pos = begin;
+      rec->begin = begin;
+      rec->count = n;
+      rec->n_members = 0u;
+    }
+    return;
+  }
+
+  const uint32_t H = a.H;
+  const uint32_t chunks = H / (kStep * KC);
+  const uint32_t nblocks = (n + kBlock - 1) / kBlock;
+  const uint32_t units = nblocks * chunks;
+  const uint32_t kb = lane / kBlock;   // k-block: features 8 kb .. 8 kb + 7 of a step
+  const uint32_t col = lane % kBlock;  // B column (token) and A row of this lane
+  const bool a_live = col < 2u;        // A rows 0 (hi) and 1 (lo); the rest are zero
+  const uint16_t* arow = (col == 0u ? a.y_hi : a.y_lo) + static_cast<uint64_t>(r) * H + kb * 8u;
+  auto brow_of = [&](uint32_t j) {
+    const uint32_t bt = static_cast<uint32_t>(__shfl(static_cast<int>(t),
+                                                     static_cast<int>(j * kBlock + col)));
+    return a.emb + static_cast<uint64_t>(bt) * H + kb * 8u;
+  };
+
+  Operands<KC> o0, o1;
+  floatx4 sc = {0.0f, 0.0f, 0.0f, 0.0f};
+  floatx4 gram = {0.0f, 0.0f, 0.0f, 0.0f};
+  float g_mine = 0.0f;
+  float sq_mine = 0.0f;
+  const uint32_t unit_f = kStep * KC;
+  const uint16_t* brow = brow_of(0);
+  load_unit<KC>(brow, arow, a_live, 0u, o0);
+  for (uint32_t q = 0; q < units; q += 2) {
+    if (q + 1 < units) {
+      const uint32_t c1 = (q + 1) % chunks;
+      if (c1 == 0u) brow = brow_of((q + 1) / chunks);
+      load_unit<KC>(brow, arow, a_live, c1 * unit_f, o1);
+    }
+    mma_unit<KC>(o0, sc, gram);
+    if (q % chunks == chunks - 1u) finish_block(q / chunks, lane, sc, gram, g_mine, sq_mine);
+    if (q + 2 < units) {
+      const uint32_t c2 = (q + 2) % chunks;
+      if (c2 == 0u) brow = brow_of((q + 2) / chunks);
+      load_unit<KC>(brow, arow, a_live, c2 * unit_f, o0);
+    }
+    if (q + 1 < units) {
+      mma_unit<KC>(o1, sc, gram);
+      if ((q + 1) % chunks == chunks - 1u) {
+        finish_block((q + 1) / chunks, lane, sc, gram, g_mine, sq_mine);
+      }
+    }
+  }
+
+  // window summary of the tile (the candidate of lane l is list position
+  // begin + l); the bound is |g - r| <= ||e|| (coef ||y|| + coef2) + slack
+  const float tn = __fsqrt_rn(sq_mine) * (1.0f + 0x1p-7f);
+  const float g = g_mine;
+  const float b = __builtin_fmaf(tn, __builtin_fmaf(a.coef, yn, a.coef2), a.slack);
+  const bool fin = !live || (__builtin_isfinite(g) && __builtin_isfinite(b) && b < 0x1p100f);
+  const bool all_finite = __ballot(!fin) == 0ull;
+  const float L = wave_max(live ? g - b : -__builtin_huge_valf());
+  uint32_t mt = live ? t : kInvalidToken;
+  uint32_t mp = begin + lane;
+  wave_min_token(mt, mp);
+  const bool member = all_finite && live && g + b >= L;
+  const uint64_t mask = __ballot(member);
+  const uint32_t total = static_cast<uint32_t>(__popcll(mask));
+  const bool ordinary = all_finite && total <= static_cast<uint32_t>(kTileMembers);
+  if (ordinary && member) {
+    const uint32_t rank = static_cast<uint32_t>(__popcll(mask & ((1ull << lane) - 1ull)));
+    rec->m[rank] = TileMember{t, begin + lane, g - b, g + b};
+  }
+  if (lane == 0) {
+    rec->best_lower = L;
+    rec->flags = ordinary ? 0u : kTileRescoreAll;
+    rec->min_token = mt;
+    rec->min_pos = mp;
+    rec->begin = begin;
+    rec->count = n;
+    rec->n_members = ordinary ? total : 0u;
+  }
+}
+
+// Planned mode: the tile plan, then wave slot s of the grid's S slots walks
+// tiles [W s / S, W (s + 1) / S).
+template <int KC>
+__global__ __launch_bounds__(kThreads) void gather_mfma_kernel(GatherArgs a) {
+  __shared__ TilePlan<kThreads> plan;
+  const uint64_t W = plan_tiles<kThreads>(a.row_meta, a.rows, kGatherWaveTile, false, plan);
+  const uint64_t slots = static_cast<uint64_t>(gridDim.x) * kWaves;
+  const uint64_t me = static_cast<uint64_t>(blockIdx.x) * kWaves + threadIdx.x / kWave;
+  const uint32_t w0 = static_cast<uint32_t>(W * me / slots);
+  const uint32_t w1 = static_cast<uint32_t>(W * (me + 1) / slots);
+  if (w0 >= w1) return;
+  uint32_t r = plan_row_of<kThreads>(plan, a.rows, w0);
+  for (uint32_t w = w0; w < w1; ++w) {
+    while (plan.prefix[r + 1] <= w) ++r;
+    mfma_tile<KC>(a, r, w - plan.prefix[r], plan.begin[r], plan.count[r]);
+  }
+}
+
+// Grid mode (rows above the plan's capacity): one wave per (row, tile),
+// blockIdx.x = k * rows + r.
+template <int KC>
+__global__ __launch_bounds__(kWave) void gather_mfma_grid_kernel(GatherArgs a) {
+  const uint32_t r = blockIdx.x % a.rows;
+  const uint32_t k = blockIdx.x / a.rows;
+  const RowMeta meta = a.row_meta[r];
+  if (!row_gathered(meta, false) || k * kGatherWaveTile >= meta.count) return;
+  mfma_tile<KC>(a, r, k, meta.list_begin, meta.count);
+}
+
+template <int KC>
+hipError_t launch_variant(const GatherArgs& a, hipStream_t stream) {
+  if (a.rows <= kPlanRowsMax && a.groups > 0) {
+    static int resident = 0;
+    if (resident == 0) {
+      int n = 0;
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+              &n, reinterpret_cast<const void*>(gather_mfma_kernel<KC>), kThreads, 0) !=
+              hipSuccess ||
+          n <= 0) {
+        n = 2;
+      }
+      resident = n;
+    }
+    const uint32_t g = a.groups * static_cast<uint32_t>(resident);
+    hipLaunchKernelGGL((gather_mfma_kernel<KC>), dim3(g), dim3(kThreads), 0, stream, a);
+  } else {
+    const uint64_t slots = static_cast<uint64_t>(a.rows) * a.max_tiles;
+    if (slots > 0x7FFFFFFFull) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((gather_mfma_grid_kernel<KC>), dim3(static_cast<uint32_t>(slots)),
+                       dim3(kWave), 0, stream, a);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_gather_mfma(const GatherArgs& a, hipStream_t stream) {
+  if (a.H == 0 || a.H % kStep != 0 || a.tile != kGatherWaveTile || a.y_hi == nullptr ||
+      a.y_lo == nullptr || a.row_norm == nullptr) {
+    return hipErrorInvalidValue;
+  }
+  const uint32_t steps = a.H / kStep;
+  if (steps % 6 == 0) return launch_variant<6>(a, stream);
+  if (steps % 8 == 0) return launch_variant<8>(a, stream);
+  if (steps % 4 == 0) return launch_variant<4>(a, stream);
+  if (steps % 2 == 0) return launch_variant<2>(a, stream);
+  return launch_variant<1>(a, stream);
+}
+
+}  // namespace mf

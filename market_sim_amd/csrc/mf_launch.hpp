@@ -15,6 +15,7 @@ struct TileRecord;
 // Where a decode-tail gather workgroup reads candidate scores from.
 enum class ScoreSource : int {
   kDotF32 = 0,  // fast dot of FP32 normalized hidden with the FP16 table
+  kMfma = 1,    // MFMA dot of the FP16 hi/lo split of the hidden (H % 32 == 0)
   kLookup = 2,  // FP32 scores already computed by the MFMA projection
 };
 
@@ -68,6 +69,7 @@ hipError_t launch_fill_zero(void* address, uint64_t bytes, hipStream_t stream);
 
 constexpr uint32_t kGatherTileMax = 256;
 constexpr uint32_t kPlanRowsMax = 1024;  // rows the gather plans in LDS
+constexpr uint32_t kGatherWaveTile = 64;  // candidates per wave tile (MFMA gather)
 
 struct TailNormArgs {
   const float* x;          // [rows, H]
@@ -75,7 +77,7 @@ struct TailNormArgs {
   float epsilon;
   float* y;                // [rows, H] reference-order normalized hidden
   float* row_norm;         // [rows] upper bound of ||y||
-  uint16_t* y_hi;          // [rows, H] FP16 split of unrestricted rows (or null)
+  uint16_t* y_hi;          // [rows, H] FP16 split hi = rne(y), lo = rne(y - hi) (or null)
   uint16_t* y_lo;
   const uint32_t* row_state;
   const uint32_t* offsets;
@@ -93,9 +95,11 @@ struct TailNormArgs {
 
 struct GatherArgs {
   const float* y;          // [rows, H]
+  const uint16_t* y_hi;    // [rows, H] FP16 split (MFMA)
+  const uint16_t* y_lo;
   const uint16_t* emb;     // [V, H]
   const float* scores;     // [rows, V] (lookup)
-  const float* row_norm;   // (lookup)
+  const float* row_norm;   // (lookup, MFMA)
   const float* tok_norm;   // (lookup)
   const uint32_t* tokens;  // state lists
   const RowMeta* row_meta;
@@ -107,7 +111,7 @@ struct GatherArgs {
   uint32_t max_tiles;
   uint32_t groups;         // compute units for the planned mode (0 = grid mode)
   float coef;              // dot: b = coef * sum|y e| + slack
-  float coef2;             // lookup: b = ||e|| (coef ||y|| + coef2) + slack
+  float coef2;             // lookup, MFMA: b = ||e|| (coef ||y|| + coef2) + slack
   float slack;
 };
 
@@ -136,6 +140,7 @@ struct FinalizeArgs {
 
 hipError_t launch_tail_norm(const TailNormArgs& args, uint32_t rows, hipStream_t stream);
 hipError_t launch_gather(ScoreSource source, const GatherArgs& args, hipStream_t stream);
+hipError_t launch_gather_mfma(const GatherArgs& args, hipStream_t stream);  // mf_gather.hip
 hipError_t launch_finalize(const FinalizeArgs& args, hipStream_t stream);
 
 // ---- MFMA projection (mf_mfma.hip) ----------------------------------------

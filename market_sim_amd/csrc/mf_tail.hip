@@ -21,6 +21,7 @@
 
 #include "mf_device.hpp"
 #include "mf_launch.hpp"
+#include "mf_plan.hpp"
 
 namespace mf {
 namespace {
@@ -104,7 +105,7 @@ __global__ __launch_bounds__(kWave) void tail_norm_kernel(TailNormArgs a) {
   }
   __syncthreads();
   const float inverse = inverse_shared;
-  const bool split = a.y_hi != nullptr && a.row_state[r] == kStateUnrestricted;
+  const bool split = a.y_hi != nullptr;
   float norm_sq = 0.0f;
   for (uint32_t c = lane; c < H; c += kWave) {
     float v = xs[c];
@@ -327,10 +328,6 @@ __device__ void gather_tile(const GatherArgs& a, uint32_t r, uint32_t k, uint32_
   }
 }
 
-__device__ __forceinline__ bool gathered(const RowMeta& m, bool lookup) {
-  return (m.kind & kRowRestricted) || (lookup && (m.kind & kRowUnrestricted));
-}
-
 // Grid mode (any number of rows): blockIdx.x = k * rows + r.
 template <ScoreSource kSrc, int kH, int kG>
 __global__ __launch_bounds__(kThreads) void gather_kernel(GatherArgs a) {
@@ -339,78 +336,33 @@ __global__ __launch_bounds__(kThreads) void gather_kernel(GatherArgs a) {
   const uint32_t r = blockIdx.x % a.rows;
   const uint32_t k = blockIdx.x / a.rows;
   const RowMeta meta = a.row_meta[r];
-  if (!gathered(meta, kSrc == ScoreSource::kLookup) || k * a.tile >= meta.count) return;
+  if (!row_gathered(meta, kSrc == ScoreSource::kLookup) || k * a.tile >= meta.count) return;
   uint32_t staged = kInvalidToken;
   gather_tile<kSrc, kH, kG>(a, r, k, meta.list_begin, meta.count,
                             (meta.kind & kRowUnrestricted) != 0, ys, sh, staged);
 }
 
-// Planned mode (rows <= kPlanRowsMax): every workgroup reads all row
-// metadata, scans the tile counts in LDS (the same prefix in every
-// workgroup, so no workgroup waits on another) and walks its contiguous
-// range [W*b/G, W*(b+1)/G) of the W tiles -- no idle workgroups, and
-// consecutive tiles of one row reuse the staged hidden vector.
+// Planned mode (rows <= kPlanRowsMax): the tile plan (mf_plan.hpp), then
+// each workgroup walks its contiguous range [W*b/G, W*(b+1)/G) of the W
+// tiles -- no idle workgroups, and consecutive tiles of one row reuse the
+// staged hidden vector.
 template <ScoreSource kSrc, int kH, int kG>
 __global__ __launch_bounds__(kThreads) void gather_planned_kernel(GatherArgs a) {
   extern __shared__ float ys[];
   __shared__ GatherShared sh;
-  __shared__ uint32_t prefix[kPlanRowsMax + 1];
-  __shared__ uint32_t pbegin[kPlanRowsMax];
-  __shared__ uint32_t pcount[kPlanRowsMax];
-  __shared__ uint32_t pkind[kPlanRowsMax];
-  __shared__ uint32_t wave_total[kThreads / kWave];
-  constexpr bool lookup = kSrc == ScoreSource::kLookup;
-  const uint32_t rows = a.rows;
-  const uint32_t tid = threadIdx.x;
-  for (uint32_t r = tid; r < rows; r += kThreads) {
-    const RowMeta m = a.row_meta[r];
-    const bool use = gathered(m, lookup);
-    pbegin[r] = m.list_begin;
-    pcount[r] = use ? m.count : 0u;
-    pkind[r] = m.kind;
-    prefix[r + 1] = use ? (m.count + a.tile - 1) / a.tile : 0u;
-  }
-  __syncthreads();
-  // in-place inclusive scan of prefix[1..rows]: thread segments + block scan
-  const uint32_t seg = (rows + kThreads - 1) / kThreads;
-  const uint32_t s0 = tid * seg < rows ? tid * seg : rows;
-  const uint32_t s1 = s0 + seg < rows ? s0 + seg : rows;
-  uint32_t local = 0u;
-  for (uint32_t i = s0; i < s1; ++i) local += prefix[i + 1];
-  uint32_t incl = local;
-  const uint32_t lane = tid % kWave;
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    const uint32_t o = __shfl_up(incl, d);
-    if (static_cast<int>(lane) >= d) incl += o;
-  }
-  if (lane == kWave - 1) wave_total[tid / kWave] = incl;
-  __syncthreads();
-  uint32_t run = incl - local;
-  for (uint32_t w = 0; w < tid / kWave; ++w) run += wave_total[w];
-  for (uint32_t i = s0; i < s1; ++i) {
-    run += prefix[i + 1];
-    prefix[i + 1] = run;
-  }
-  if (tid == 0) prefix[0] = 0u;
-  __syncthreads();
-  const uint64_t W = prefix[rows];
+  __shared__ TilePlan<kThreads> plan;
+  const uint64_t W = plan_tiles<kThreads>(a.row_meta, a.rows, a.tile,
+                                          kSrc == ScoreSource::kLookup, plan);
   const uint64_t G = gridDim.x;
   const uint32_t w0 = static_cast<uint32_t>(W * blockIdx.x / G);
   const uint32_t w1 = static_cast<uint32_t>(W * (blockIdx.x + 1) / G);
   if (w0 >= w1) return;
-  // the row holding tile w0: largest r with prefix[r] <= w0 < prefix[r + 1]
-  uint32_t lo = 0u, hi = rows;
-  while (lo < hi) {
-    const uint32_t mid = (lo + hi) / 2;
-    if (prefix[mid + 1] <= w0) lo = mid + 1; else hi = mid;
-  }
-  uint32_t r = lo;
+  uint32_t r = plan_row_of<kThreads>(plan, a.rows, w0);
   uint32_t staged = kInvalidToken;
   for (uint32_t w = w0; w < w1; ++w) {
-    while (prefix[r + 1] <= w) ++r;
-    gather_tile<kSrc, kH, kG>(a, r, w - prefix[r], pbegin[r], pcount[r],
-                              (pkind[r] & kRowUnrestricted) != 0, ys, sh, staged);
+    while (plan.prefix[r + 1] <= w) ++r;
+    gather_tile<kSrc, kH, kG>(a, r, w - plan.prefix[r], plan.begin[r], plan.count[r],
+                              (plan.kind[r] & kRowUnrestricted) != 0, ys, sh, staged);
   }
 }
 
@@ -677,6 +629,7 @@ static void launch_gather_variant(const GatherArgs& a, hipStream_t stream) {
 
 hipError_t launch_gather(ScoreSource source, const GatherArgs& a, hipStream_t stream) {
   const bool aligned = (reinterpret_cast<uintptr_t>(a.emb) & 15u) == 0;
+  if (source == ScoreSource::kMfma) return launch_gather_mfma(a, stream);
   if (source == ScoreSource::kLookup) {
     launch_gather_variant<ScoreSource::kLookup, 0, 64>(a, stream);
   } else if (a.H == 576 && aligned) {
