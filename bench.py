@@ -1,6 +1,6 @@
 """Benchmark of the restricted decode tail on one MI355X.
 
-Workload ("cfg3"): a continuous-batching pack of
+Workload cfg3: a continuous-batching pack of
 B = 256 sequences over the 49152 x 576 FP16 tied embedding; allowed-set sizes
 log-uniform in [1, 4096]; 10% of rows unrestricted (MFMA fallback); hidden
 N(0, 1) through the final RMSNorm.  Synthetic data (seeded), inputs resident
@@ -40,17 +40,20 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
-    p.add_argument("--config", type=int, default=3, help="BASELINE configs[n-1]")
+    p.add_argument("--config", type=int, default=3, help="benchmark configuration cfgN")
     p.add_argument("--copies", type=int, default=8)
     p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="budget of the CPU oracle baseline sample")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-full", action="store_true")
+    p.add_argument("--calibration-copy-mib", type=int, default=0,
+                   help="after the timed loop, run 4 FP32 x1.0 copies of this many MiB "
+                        "(a known-traffic kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     return p.parse_args()
 
 
 def algorithmic_bytes(w) -> dict:
-    """Bytes one launch must move (SURVEY row d):
+    """Bytes one launch must move:
     gather  2 H U + 4 N + 4 H B_r + 4 (B_r + 1) + 12 B_r
     fallback 2 V H + 4 H B_u + 8 B_u, flops 2 B_u H V."""
     H, V = w.hidden, w.vocab
@@ -166,7 +169,7 @@ def main() -> int:
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; the path "
-                          "shards by rows with no exchange (see DESIGN.md)",
+                          "shards by rows with no exchange",
                           "n_gpus": args.gpus}))
         return 2
     import torch
@@ -176,11 +179,22 @@ def main() -> int:
     w = workloads.config(args.config, seed=0)
     alg = algorithmic_bytes(w)
     tail = DeviceTail(w, copies=args.copies)
-    total_ms, wall_ms, st = time_loop(tail, ["prepare", "restricted", "unrestricted", "finalize"],
-                                      args.steps, args.warmup, args.copies)
+    # the step as a caller runs it: one mf_decode_tail_f16 call
+    total_ms, wall_ms, _ = time_loop(tail, ["tail"], args.steps, args.warmup, args.copies)
+    # per-kernel times: the four stage entry points, HIP events between them
+    stages_ms, _, st = time_loop(tail, ["prepare", "restricted", "unrestricted", "finalize"],
+                                 args.steps, max(5, args.warmup // 2), args.copies)
     # correctness of what was timed: the last step's outputs vs the oracle on
     # a row sample is checked in tests; here record a token checksum
     tok, sc, nx = tail.results()
+    if args.calibration_copy_mib:
+        n = args.calibration_copy_mib * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(4):
+            torch.mul(src, 1.0, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
     gather_ms = st["restricted"][0]
     fb_ms = st["unrestricted"][0]
     achieved = alg["gather"] / (gather_ms * 1e-3) / 1e9
@@ -207,6 +221,7 @@ def main() -> int:
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "bytes_per_launch": alg["gather"], "avg_launch_us": round(gather_ms * 1e3, 2)},
         "stages_us": {k: round(v[0] * 1e3, 2) for k, v in st.items()},
+        "stages_serial_ms": round(stages_ms, 5),
         "effective_gather_GBs": round(alg["gather_logical"] / (gather_ms * 1e-3) / 1e9, 1),
         "fallback": {"kernel": "fallback_kernel (MFMA)", "rows": alg["B_u"],
                      "avg_launch_us": round(fb_ms * 1e3, 2),

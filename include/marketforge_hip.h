@@ -9,7 +9,7 @@
  * (StreamHandle, include/marketforge/cuda/cuda_stream.hpp:10-17).  No vendor
  * or torch type appears here.
  *
- * Conventions kept from the reference (SURVEY row b):
+ * Conventions kept from the reference:
  *   - ops borrow caller buffers: they never allocate and never synchronize;
  *   - work is asynchronous on the caller's stream;
  *   - validation happens before any launch, in the reference order: zero
@@ -59,8 +59,8 @@ enum mf_error_code {
 
 /* include/marketforge/cuda/greedy.hpp:11-12 */
 #define MF_INVALID_TOKEN 0xFFFFFFFFu
-/* Row states of the decode tail (no reference counterpart: BASELINE
- * north_star).  A state below the table's state count restricts the row to
+/* Row states of the decode tail (no reference counterpart: the
+ * packed decode tail).  A state below the table's state count restricts the row to
  * that state's list; MF_STATE_UNRESTRICTED scores the whole vocabulary (the
  * MFMA fallback); any other value makes the row invalid. */
 #define MF_STATE_UNRESTRICTED 0xFFFFFFFEu
@@ -165,7 +165,7 @@ mf_status mf_linear_f16(mf_buffer input, mf_buffer weight, mf_buffer output,
                         uint64_t rows, uint64_t input_features,
                         uint64_t output_features, uintptr_t stream);
 
-/* ---- the decode tail (no single reference call) ---- */
+/* ---- the packed decode tail (no single reference call) ------------------ */
 /* Per row r: y = RMSNorm(x[r]) (operators.cpp:523-535 order); score the
  * allowed ids of row_state[r] against the FP16 tied embedding in the chosen
  * reference order; select (greedy.cu rules); advance the DFA.  Restricted

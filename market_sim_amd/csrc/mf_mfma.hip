@@ -11,12 +11,12 @@
 // 128 x 64 FP16 slice of E and the 32 x 64 A slice in LDS (double-buffered,
 // rows padded to 144 bytes so b128 reads are bank-conflict free): eight
 // consecutive lanes load one token's 128 contiguous bytes, so every HBM line
-// is fetched once, and the next chunk's global loads are in flight while the
-// current chunk's MFMAs run.
+// is fetched once, and four chunks' global loads are in flight (in
+// registers) while the staged chunk's MFMAs run.
 //
 // FP32 hidden values enter as the FP16 pair hi = rne(y), lo = rne(y - hi)
-// (two MFMAs per step), so the fast score is accurate to ~2^-22 relative
-// before the reference-order rescore.
+// (two MFMAs per step into two accumulators, added at the end), so the fast
+// score is accurate to ~2^-22 relative before the reference-order rescore.
 #include <hip/hip_runtime.h>
 
 #include "mf_device.hpp"
@@ -59,6 +59,12 @@ struct AView {
   uint32_t H;
 };
 
+// Source row of A row m (row_index applied; 0xFFFFFFFF reads as zeros).
+__device__ __forceinline__ uint32_t a_source_row(const AView& A, uint32_t m) {
+  if (m >= A.m) return 0xFFFFFFFFu;
+  return A.row_index != nullptr ? A.row_index[m] : m;
+}
+
 // Per-thread registers holding one chunk in flight: 4 B pieces (16 B each)
 // and the A piece (hi and lo, 16 B each).
 struct ChunkRegs {
@@ -69,7 +75,7 @@ struct ChunkRegs {
 
 template <ASrc kA>
 __device__ __forceinline__ void load_chunk(const AView& A, const uint16_t* emb, uint32_t V,
-                                           uint32_t tok0, uint32_t m0, uint32_t c,
+                                           uint32_t tok0, uint32_t row, uint32_t c,
                                            ChunkRegs& r) {
   const uint32_t t = threadIdx.x;
   const uint32_t part = t % 8;
@@ -80,10 +86,8 @@ __device__ __forceinline__ void load_chunk(const AView& A, const uint16_t* emb, 
     r.b[j] = token < V ? *reinterpret_cast<const uint4*>(emb + static_cast<uint64_t>(token) * A.H + f)
                        : uint4{0u, 0u, 0u, 0u};
   }
-  // A: 32 rows x 8 pieces = 256 pieces, one per thread
-  const uint32_t i = t / 8;
-  const uint32_t row = m0 + i < A.m ? (A.row_index != nullptr ? A.row_index[m0 + i] : m0 + i)
-                                    : 0xFFFFFFFFu;
+  // A: 32 rows x 8 pieces = 256 pieces, one per thread (row resolved by
+  // the caller once per kernel)
   r.ahi = uint4{0u, 0u, 0u, 0u};
   r.alo = uint4{0u, 0u, 0u, 0u};
   if (row < A.rows) {
@@ -120,48 +124,82 @@ __device__ __forceinline__ void store_chunk(ProjShared& sh, int buf, const Chunk
   *reinterpret_cast<uint4*>(&sh.k.a[buf][1][t / 8][part * 8]) = r.alo;
 }
 
+// MFMAs of one staged chunk (LDS buffer buf): the hi and lo halves of A
+// accumulate separately (two independent MFMA chains) and are added once at
+// the end.
+template <ASrc kA>
+__device__ __forceinline__ void mma_chunk(const ProjShared& sh, int buf, floatx16& acc_hi,
+                                          floatx16& acc_lo, float& tok_sq) {
+  const int lane = threadIdx.x % 64;
+  const int wave = threadIdx.x / 64;
+  const int g = lane / 32;
+  const int i = lane % 32;
+#pragma unroll
+  for (int s = 0; s < kKC / 16; ++s) {
+    const half8_t b = *reinterpret_cast<const half8_t*>(&sh.k.b[buf][wave * 32 + i][s * 16 + g * 8]);
+    const half8_t ahi = *reinterpret_cast<const half8_t*>(&sh.k.a[buf][0][i][s * 16 + g * 8]);
+    acc_hi = __builtin_amdgcn_mfma_f32_32x32x16_f16(ahi, b, acc_hi, 0, 0, 0);
+    if constexpr (kA != ASrc::kF16) {
+      const half8_t alo = *reinterpret_cast<const half8_t*>(&sh.k.a[buf][1][i][s * 16 + g * 8]);
+      acc_lo = __builtin_amdgcn_mfma_f32_32x32x16_f16(alo, b, acc_lo, 0, 0, 0);
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float e = static_cast<float>(b[k]);
+      tok_sq = __builtin_fmaf(e, e, tok_sq);
+    }
+  }
+}
+
+// Step c of the pipeline (chunk k travels through register set k % 4): the
+// load of chunk c + 4 into the set chunk c left, the MFMAs of chunk c, then
+// chunk c + 1 into the other LDS buffer.  Four chunks are in flight from
+// HBM while one is multiplied.
+template <ASrc kA>
+__device__ __forceinline__ void pipeline_step(const AView& A, const uint16_t* emb, uint32_t V,
+                                              uint32_t tok0, uint32_t arow, uint32_t c,
+                                              uint32_t chunks, ChunkRegs& free_set,
+                                              const ChunkRegs& next_set, ProjShared& sh,
+                                              floatx16& acc_hi, floatx16& acc_lo,
+                                              float& tok_sq) {
+  if (c >= chunks) return;
+  if (c + 4 < chunks) load_chunk<kA>(A, emb, V, tok0, arow, c + 4, free_set);
+  mma_chunk<kA>(sh, c & 1, acc_hi, acc_lo, tok_sq);
+  if (c + 1 < chunks) store_chunk(sh, (c + 1) & 1, next_set);
+  __syncthreads();
+}
+
 // The wave's 32 x 32 block (rows m0.., tokens tok0 + 32 * wave ..).  Returns
 // the accumulator and the lane's sum of squares of its B values; combined
 // across the two lane groups that is ||e_token||^2 of token lane % 32.
 template <ASrc kA>
 __device__ floatx16 project_block(const AView& A, const uint16_t* emb, uint32_t V,
                                   uint32_t m0, uint32_t tok0, ProjShared& sh, float& tok_sq) {
-  const int lane = threadIdx.x % 64;
-  const int wave = threadIdx.x / 64;
-  const int g = lane / 32;
-  const int i = lane % 32;
-  floatx16 acc;
+  floatx16 acc_hi, acc_lo;
 #pragma unroll
-  for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
+  for (int v = 0; v < 16; ++v) {
+    acc_hi[v] = 0.0f;
+    acc_lo[v] = 0.0f;
+  }
   tok_sq = 0.0f;
   const uint32_t chunks = A.H / kKC;
-  ChunkRegs regs;
-  load_chunk<kA>(A, emb, V, tok0, m0, 0, regs);
-  store_chunk(sh, 0, regs);
+  const uint32_t arow = a_source_row(A, m0 + threadIdx.x / 8);
+  ChunkRegs r0, r1, r2, r3;
+  load_chunk<kA>(A, emb, V, tok0, arow, 0, r0);
+  if (chunks > 1) load_chunk<kA>(A, emb, V, tok0, arow, 1, r1);
+  if (chunks > 2) load_chunk<kA>(A, emb, V, tok0, arow, 2, r2);
+  if (chunks > 3) load_chunk<kA>(A, emb, V, tok0, arow, 3, r3);
+  store_chunk(sh, 0, r0);
   __syncthreads();
-  for (uint32_t c = 0; c < chunks; ++c) {
-    const int buf = c & 1;
-    if (c + 1 < chunks) load_chunk<kA>(A, emb, V, tok0, m0, c + 1, regs);
-#pragma unroll
-    for (int s = 0; s < kKC / 16; ++s) {
-      const half8_t b = *reinterpret_cast<const half8_t*>(&sh.k.b[buf][wave * 32 + i][s * 16 + g * 8]);
-      const half8_t ahi = *reinterpret_cast<const half8_t*>(&sh.k.a[buf][0][i][s * 16 + g * 8]);
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const float e = static_cast<float>(b[k]);
-        tok_sq = __builtin_fmaf(e, e, tok_sq);
-      }
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ahi, b, acc, 0, 0, 0);
-      if constexpr (kA != ASrc::kF16) {
-        const half8_t alo = *reinterpret_cast<const half8_t*>(&sh.k.a[buf][1][i][s * 16 + g * 8]);
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(alo, b, acc, 0, 0, 0);
-      }
-    }
-    if (c + 1 < chunks) store_chunk(sh, buf ^ 1, regs);
-    __syncthreads();
+  for (uint32_t c = 0; c < chunks; c += 4) {
+    pipeline_step<kA>(A, emb, V, tok0, arow, c, chunks, r0, r1, sh, acc_hi, acc_lo, tok_sq);
+    pipeline_step<kA>(A, emb, V, tok0, arow, c + 1, chunks, r1, r2, sh, acc_hi, acc_lo, tok_sq);
+    pipeline_step<kA>(A, emb, V, tok0, arow, c + 2, chunks, r2, r3, sh, acc_hi, acc_lo, tok_sq);
+    pipeline_step<kA>(A, emb, V, tok0, arow, c + 3, chunks, r3, r0, sh, acc_hi, acc_lo, tok_sq);
   }
   tok_sq += __shfl_xor(tok_sq, 32);
-  return acc;
+  if constexpr (kA == ASrc::kF16) return acc_hi;
+  return acc_hi + acc_lo;
 }
 
 // Accumulator element v of lane l holds D[row][col] with col = l % 32 and
@@ -210,6 +248,8 @@ __device__ __forceinline__ uint32_t group8_and(uint32_t v) {
 
 __global__ __launch_bounds__(kThreads) void fallback_kernel(FallbackArgs f) {
   __shared__ ProjShared sh;
+  __shared__ uint32_t src_row[kMTile];  // source row of A row i (>= rows: none)
+  __shared__ float src_norm[kMTile];    // its ||y|| bound
   const uint32_t tile = blockIdx.x;
   const uint32_t m0 = blockIdx.y * kMTile;
   const uint32_t tiles = gridDim.x;
@@ -217,24 +257,24 @@ __global__ __launch_bounds__(kThreads) void fallback_kernel(FallbackArgs f) {
   const int wave = threadIdx.x / 64;
   const uint32_t tok0 = tile * kTileTokens;
   const AView A{nullptr, f.y_hi, f.y_lo, f.row_index, f.m, f.rows, f.H};
+  // resolved before the main loop (its first barrier publishes them), so
+  // the epilogue waits on no global load
+  if (threadIdx.x < kMTile) {
+    const uint32_t row = a_source_row(A, m0 + threadIdx.x);
+    const bool ok = row < f.rows;
+    src_row[threadIdx.x] = ok ? row : 0xFFFFFFFFu;
+    src_norm[threadIdx.x] = ok ? f.row_norm[row] : 0.0f;
+    if (tile == 0 && ok) f.fb_map[row] = m0 + threadIdx.x;
+  }
   float tok_sq;
   const floatx16 acc = project_block<ASrc::kF16Pair>(A, f.emb, f.V, m0, tok0, sh, tok_sq);
-
-  if (tile == 0 && threadIdx.x < kMTile && m0 + threadIdx.x < f.m) {
-    const uint32_t row = f.row_index[m0 + threadIdx.x];
-    if (row < f.rows) f.fb_map[row] = m0 + threadIdx.x;
-  }
 
   // scores and bounds into LDS (the staging area is free after the loop)
   const float tok_norm = __fsqrt_rn(tok_sq) * (1.0f + 0x1p-7f);
 #pragma unroll
   for (int v = 0; v < 16; ++v) {
     const int i = acc_row(v, lane);
-    float yn = 0.0f;
-    if (m0 + i < f.m) {
-      const uint32_t src = f.row_index[m0 + i];
-      if (src < f.rows) yn = f.row_norm[src];
-    }
+    const float yn = src_norm[i];
     sh.epi.g[i][wave * 32 + (lane % 32)] = acc[v];
     sh.epi.b[i][wave * 32 + (lane % 32)] =
         __builtin_fmaf(tok_norm, __builtin_fmaf(f.coef, yn, f.coef2), f.slack);
@@ -265,7 +305,7 @@ __global__ __launch_bounds__(kThreads) void fallback_kernel(FallbackArgs f) {
     if (static_cast<int>(sub) >= d) incl += o;
   }
   const uint32_t total = __shfl(incl, 7, 8);
-  const bool row_ok = m0 + i < f.m && f.row_index[m0 + i] < f.rows;
+  const bool row_ok = src_row[i] != 0xFFFFFFFFu;
   if (!row_ok) return;
   TileRecord* rec = f.records + static_cast<uint64_t>(m0 + i) * tiles + tile;
   const bool ordinary = fin && total <= static_cast<uint32_t>(kTileMembers);

@@ -1,4 +1,4 @@
-"""Seeded synthetic workloads for the restricted head (the five BASELINE configs).
+"""Seeded synthetic workloads for the restricted head (the five benchmark configurations cfg1..cfg5).
 
 Generation is deterministic: numpy's PCG64 generator, one independent child
 stream per component (``SeedSequence(seed).spawn``), normals from
@@ -222,7 +222,7 @@ def single_sequence_f32(seed: int = 0, vocab: int = 49152, hidden: int = 576,
 
 def config(n: int, seed: int = 0, scale_vocab: Optional[int] = None,
            scale_rows: Optional[int] = None) -> Workload:
-    """BASELINE.json configs[n - 1].  ``scale_vocab``/``scale_rows`` shrink a
+    """Benchmark configuration cfg<n>.  ``scale_vocab``/``scale_rows`` shrink a
     config for quick CPU checks (same generator, smaller shape)."""
     if n == 1:
         return single_sequence_f32(seed, vocab=scale_vocab or 49152)
