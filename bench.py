@@ -112,6 +112,45 @@ def time_loop(tail, stages, steps, warmup, copies):
                             for k, v in per_stage.items()}
 
 
+def kernel_loop(tail, stage, launches, copies):
+    """Average duration of one stage's kernel: `launches` back-to-back launches
+    (rotating table copies) between two HIP events on the launch stream.  The
+    stage must be idempotent given the prepare stage's outputs (the restricted
+    gather is: it reads the normalized rows and writes tile records)."""
+    import torch
+    from market_sim_amd import abi, ops
+    fns = {"restricted": ops.decode_tail_restricted, "unrestricted": ops.decode_tail_unrestricted}
+    args = [tail.args(i % copies) for i in range(copies)]
+    s = tail.stream
+    h = s.cuda_stream
+    abi.check("prepare", ops.decode_tail_prepare(args[0], h))
+    for i in range(10):
+        abi.check(stage, fns[stage](args[i % copies], h))
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(s)
+    for i in range(launches):
+        abi.check(stage, fns[stage](args[i % copies], h))
+    stop.record(s)
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / launches
+
+
+def profiled_traffic(kernel: str):
+    """HBM-side bytes per launch of `kernel` from the committed rocprofv3 PMC
+    summary (FETCH_SIZE and WRITE_SIZE passes scaled by a copy kernel of known
+    size); None when the summary is absent."""
+    path = os.path.join(ROOT, "profiles", "decode_tail_cfg3_traffic.md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch") and kernel in line:
+                return int(line.split("=", 1)[1].split()[0])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(w, budget_s: float) -> dict:
     """The CPU oracle (a plain-C port of the reference loops) on a bounded
     sample of the same pack: whole batches, all host threads, until the time
@@ -195,9 +234,10 @@ def main() -> int:
             torch.mul(src, 1.0, out=dst)
         torch.cuda.synchronize()
         del src, dst
-    gather_ms = st["restricted"][0]
-    fb_ms = st["unrestricted"][0]
+    gather_ms = kernel_loop(tail, "restricted", args.steps, args.copies)
+    fb_ms = kernel_loop(tail, "unrestricted", args.steps, args.copies)
     achieved = alg["gather"] / (gather_ms * 1e-3) / 1e9
+    traffic = profiled_traffic("gather_mfma_kernel")
     result = {
         "metric": METRIC,
         "value": round(w.rows / (total_ms * 1e-3), 1),
@@ -216,10 +256,11 @@ def main() -> int:
                    "unrestricted_rows": alg["B_u"], "candidates": alg["N"],
                    "distinct_ids": alg["U"], "table_copies": args.copies,
                    "order": "fma chain (greedy.cu:171-176)"},
-        "roofline": {"kernel": "gather_kernel (CSR gather)", "bound": "hbm",
+        "roofline": {"kernel": "gather_mfma_kernel (CSR gather)", "bound": "hbm",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "bytes_per_launch": alg["gather"], "avg_launch_us": round(gather_ms * 1e3, 2)},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "bytes_per_launch": alg["gather"], "avg_launch_us": round(gather_ms * 1e3, 2),
+                     "traffic_source": "profiles/decode_tail_cfg3_traffic.md"},
         "stages_us": {k: round(v[0] * 1e3, 2) for k, v in st.items()},
         "stages_serial_ms": round(stages_ms, 5),
         "effective_gather_GBs": round(alg["gather_logical"] / (gather_ms * 1e-3) / 1e9, 1),
