@@ -219,7 +219,7 @@ mf_status mf_decode_tail_workspace_bytes(const mf_decode_tail_args* args,
 mf_status mf_workspace_init(mf_buffer workspace, uintptr_t stream);
 
 /* The restricted path: CSR gather for restricted rows + MFMA fallback.
- * Equivalent to the three stages below, in order, on one stream. */
+ * Equivalent to the four stages below, in order, on one stream. */
 mf_status mf_decode_tail_f16(const mf_decode_tail_args* args, uintptr_t stream);
 
 /* Stages of mf_decode_tail_f16 for callers that schedule them separately

@@ -2,8 +2,8 @@
 
   market_sim_amd/lib/libmarketforge_hip.so   gfx950 kernels + C ABI (hipcc)
 
-Run ``python -m market_sim_amd.build``.  Always recompiles what changed
-(make), so a call after editing a source rebuilds before tests or GPU runs.
+Run ``python -m market_sim_amd.build``.  Recompiles what changed (make), or
+everything with ``force`` (the driver's build check compiles every time).
 """
 import os
 import subprocess
@@ -12,9 +12,11 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 
 
-def build(jobs: int = 4) -> None:
-    subprocess.run(["make", "-s", "-j", str(jobs), "-C", os.path.join(HERE, "csrc")],
-                   check=True)
+def build(jobs: int = 4, force: bool = False) -> None:
+    cmd = ["make", "-s", "-j", str(jobs), "-C", os.path.join(HERE, "csrc")]
+    if force:
+        cmd.insert(1, "-B")
+    subprocess.run(cmd, check=True)
 
 
 if __name__ == "__main__":
