@@ -36,32 +36,38 @@ constexpr int kWaves = kThreads / kWave;
 constexpr uint32_t kBlock = 16;  // tokens per MFMA block
 constexpr uint32_t kStep = 32;   // features per MFMA step
 
-// One unit: KC steps of the A and B operands of one block.
+// One unit: KC steps of the B operand (16 table rows) of one block.
 template <int KC>
 struct Operands {
-  half8_t a[KC];
   half8_t b[KC];
 };
 
+// Loads of one unit: straight-line (no predication, no branches) so the
+// compiler can count the loads in flight and wait only for the unit about to
+// be multiplied.
 template <int KC>
-__device__ __forceinline__ void load_unit(const uint16_t* brow, const uint16_t* arow,
-                                          bool a_live, uint32_t f0, Operands<KC>& o) {
+__device__ __forceinline__ void load_unit(const uint16_t* brow, uint32_t f0, Operands<KC>& o) {
 #pragma unroll
   for (int s = 0; s < KC; ++s) {
     o.b[s] = *reinterpret_cast<const half8_t*>(brow + f0 + s * kStep);
   }
-#pragma unroll
-  for (int s = 0; s < KC; ++s) {
-    o.a[s] = a_live ? *reinterpret_cast<const half8_t*>(arow + f0 + s * kStep)
-                    : half8_t{0, 0, 0, 0, 0, 0, 0, 0};
-  }
 }
 
+// MFMAs of one unit.  A comes from the wave's LDS stage of the row's FP16
+// split: lanes of A row 0 read hi, all others lo; rows 2..15 are masked.
 template <int KC>
-__device__ __forceinline__ void mma_unit(const Operands<KC>& o, floatx4& sc, floatx4& gram) {
+__device__ __forceinline__ void mma_unit(const Operands<KC>& o, const uint16_t* a_lane,
+                                         uint32_t f0, uint32_t amask, floatx4& sc,
+                                         floatx4& gram) {
 #pragma unroll
   for (int s = 0; s < KC; ++s) {
-    sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.a[s], o.b[s], sc, 0, 0, 0);
+    uint4 q = *reinterpret_cast<const uint4*>(a_lane + f0 + s * kStep);
+    q.x &= amask;
+    q.y &= amask;
+    q.z &= amask;
+    q.w &= amask;
+    sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, q), o.b[s], sc, 0,
+                                                0, 0);
     gram = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.b[s], o.b[s], gram, 0, 0, 0);
   }
 }
@@ -87,14 +93,16 @@ __device__ __forceinline__ void finish_block(uint32_t j, uint32_t lane, floatx4&
 }
 
 // Tile k of row r: candidates [64 k, 64 k + n) of the row's list.
+// The wave's LDS stage holds row `staged`'s y_hi then y_lo (2 H halves).
 template <int KC>
 __device__ void mfma_tile(const GatherArgs& a, uint32_t r, uint32_t k, uint32_t list_begin,
-                          uint32_t count) {
+                          uint32_t count, uint16_t* stage, uint32_t& staged) {
   const uint32_t lane = threadIdx.x % kWave;
   const uint32_t begin = k * kGatherWaveTile;
   const uint32_t n = count - begin < kGatherWaveTile ? count - begin : kGatherWaveTile;
   const bool live = lane < n;
-  const uint32_t t = live ? a.tokens[list_begin + begin + lane] : 0u;
+  const uint32_t id = a.tokens[list_begin + begin + (live ? lane : n - 1)];
+  const uint32_t t = live ? id : 0u;
   const float yn = a.row_norm[r];
   TileRecord* rec = a.records + static_cast<uint64_t>(r) * a.max_tiles + k;
   if (__ballot(live && t >= a.V) != 0ull) {
@@ -117,12 +125,30 @@ __device__ void mfma_tile(const GatherArgs& a, uint32_t r, uint32_t k, uint32_t 
   const uint32_t units = nblocks * chunks;
   const uint32_t kb = lane / kBlock;   // k-block: features 8 kb .. 8 kb + 7 of a step
   const uint32_t col = lane % kBlock;  // B column (token) and A row of this lane
-  const bool a_live = col < 2u;        // A rows 0 (hi) and 1 (lo); the rest are zero
-  const uint16_t* arow = (col == 0u ? a.y_hi : a.y_lo) + static_cast<uint64_t>(r) * H + kb * 8u;
-  auto brow_of = [&](uint32_t j) {
+  if (staged != r) {
+    // the row's FP16 split into the wave's stage (16 bytes per copy)
+    const uint32_t per = H / 8;
+    for (uint32_t q = lane; q < 2u * per; q += kWave) {
+      const uint16_t* src = (q < per ? a.y_hi : a.y_lo) + static_cast<uint64_t>(r) * H;
+      *reinterpret_cast<uint4*>(stage + q * 8) =
+          *reinterpret_cast<const uint4*>(src + (q % per) * 8);
+    }
+    staged = r;
+    // LDS writes of this wave complete before any lane reads them
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+  // A rows 0 (hi) and 1 (lo); rows 2..15 read lo too and are masked
+  const uint32_t amask = col < 2u ? 0xFFFFFFFFu : 0u;
+  const uint16_t* a_lane = stage + (col == 0u ? 0u : H) + kb * 8u;
+  const uint32_t unit_f = kStep * KC;
+  // unit q = (block q / chunks, chunk q % chunks); the B column's token
+  auto load_q = [&](uint32_t q, Operands<KC>& o) {
+    const uint32_t j = q / chunks;
     const uint32_t bt = static_cast<uint32_t>(__shfl(static_cast<int>(t),
                                                      static_cast<int>(j * kBlock + col)));
-    return a.emb + static_cast<uint64_t>(bt) * H + kb * 8u;
+    load_unit<KC>(a.emb + static_cast<uint64_t>(bt) * H + kb * 8u, (q % chunks) * unit_f, o);
   };
 
   Operands<KC> o0, o1;
@@ -130,28 +156,33 @@ __device__ void mfma_tile(const GatherArgs& a, uint32_t r, uint32_t k, uint32_t 
   floatx4 gram = {0.0f, 0.0f, 0.0f, 0.0f};
   float g_mine = 0.0f;
   float sq_mine = 0.0f;
-  const uint32_t unit_f = kStep * KC;
-  const uint16_t* brow = brow_of(0);
-  load_unit<KC>(brow, arow, a_live, 0u, o0);
-  for (uint32_t q = 0; q < units; q += 2) {
-    if (q + 1 < units) {
-      const uint32_t c1 = (q + 1) % chunks;
-      if (c1 == 0u) brow = brow_of((q + 1) / chunks);
-      load_unit<KC>(brow, arow, a_live, c1 * unit_f, o1);
-    }
-    mma_unit<KC>(o0, sc, gram);
+  // two units in flight; sched_barrier(0) keeps each unit's loads issued
+  // before the previous unit's MFMAs, and no load sits under a branch in
+  // the steady-state loop.
+  auto mma_q = [&](uint32_t q, const Operands<KC>& o) {
+    mma_unit<KC>(o, a_lane, (q % chunks) * unit_f, amask, sc, gram);
     if (q % chunks == chunks - 1u) finish_block(q / chunks, lane, sc, gram, g_mine, sq_mine);
-    if (q + 2 < units) {
-      const uint32_t c2 = (q + 2) % chunks;
-      if (c2 == 0u) brow = brow_of((q + 2) / chunks);
-      load_unit<KC>(brow, arow, a_live, c2 * unit_f, o0);
-    }
-    if (q + 1 < units) {
-      mma_unit<KC>(o1, sc, gram);
-      if ((q + 1) % chunks == chunks - 1u) {
-        finish_block((q + 1) / chunks, lane, sc, gram, g_mine, sq_mine);
-      }
-    }
+  };
+  load_q(0, o0);
+  uint32_t q = 0;
+  for (; q + 2 < units; q += 2) {
+    load_q(q + 1, o1);
+    __builtin_amdgcn_sched_barrier(0);
+    mma_q(q, o0);
+    __builtin_amdgcn_sched_barrier(0);
+    load_q(q + 2, o0);
+    __builtin_amdgcn_sched_barrier(0);
+    mma_q(q + 1, o1);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // the last one or two units
+  if (q + 1 < units) {
+    load_q(q + 1, o1);
+    __builtin_amdgcn_sched_barrier(0);
+    mma_q(q, o0);
+    mma_q(q + 1, o1);
+  } else {
+    mma_q(q, o0);
   }
 
   // window summary of the tile (the candidate of lane l is list position
@@ -189,6 +220,9 @@ __device__ void mfma_tile(const GatherArgs& a, uint32_t r, uint32_t k, uint32_t 
 template <int KC>
 __global__ __launch_bounds__(kThreads) void gather_mfma_kernel(GatherArgs a) {
   __shared__ TilePlan<kThreads> plan;
+  extern __shared__ __align__(16) uint16_t stages[];  // [waves][2 H]
+  uint16_t* stage = stages + static_cast<size_t>(threadIdx.x / kWave) * 2u * a.H;
+  uint32_t staged = kInvalidToken;
   const uint64_t W = plan_tiles<kThreads>(a.row_meta, a.rows, kGatherWaveTile, false, plan);
   const uint64_t slots = static_cast<uint64_t>(gridDim.x) * kWaves;
   const uint64_t me = static_cast<uint64_t>(blockIdx.x) * kWaves + threadIdx.x / kWave;
@@ -198,7 +232,7 @@ __global__ __launch_bounds__(kThreads) void gather_mfma_kernel(GatherArgs a) {
   uint32_t r = plan_row_of<kThreads>(plan, a.rows, w0);
   for (uint32_t w = w0; w < w1; ++w) {
     while (plan.prefix[r + 1] <= w) ++r;
-    mfma_tile<KC>(a, r, w - plan.prefix[r], plan.begin[r], plan.count[r]);
+    mfma_tile<KC>(a, r, w - plan.prefix[r], plan.begin[r], plan.count[r], stage, staged);
   }
 }
 
@@ -208,9 +242,11 @@ template <int KC>
 __global__ __launch_bounds__(kWave) void gather_mfma_grid_kernel(GatherArgs a) {
   const uint32_t r = blockIdx.x % a.rows;
   const uint32_t k = blockIdx.x / a.rows;
+  extern __shared__ __align__(16) uint16_t stages[];  // [2 H]
   const RowMeta meta = a.row_meta[r];
   if (!row_gathered(meta, false) || k * kGatherWaveTile >= meta.count) return;
-  mfma_tile<KC>(a, r, k, meta.list_begin, meta.count);
+  uint32_t staged = kInvalidToken;
+  mfma_tile<KC>(a, r, k, meta.list_begin, meta.count, stages, staged);
 }
 
 template <int KC>
@@ -220,7 +256,8 @@ hipError_t launch_variant(const GatherArgs& a, hipStream_t stream) {
     if (resident == 0) {
       int n = 0;
       if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-              &n, reinterpret_cast<const void*>(gather_mfma_kernel<KC>), kThreads, 0) !=
+              &n, reinterpret_cast<const void*>(gather_mfma_kernel<KC>), kThreads,
+              kWaves * 4u * a.H) !=
               hipSuccess ||
           n <= 0) {
         n = 2;
@@ -228,12 +265,13 @@ hipError_t launch_variant(const GatherArgs& a, hipStream_t stream) {
       resident = n;
     }
     const uint32_t g = a.groups * static_cast<uint32_t>(resident);
-    hipLaunchKernelGGL((gather_mfma_kernel<KC>), dim3(g), dim3(kThreads), 0, stream, a);
+    hipLaunchKernelGGL((gather_mfma_kernel<KC>), dim3(g), dim3(kThreads), kWaves * 4u * a.H,
+                       stream, a);
   } else {
     const uint64_t slots = static_cast<uint64_t>(a.rows) * a.max_tiles;
     if (slots > 0x7FFFFFFFull) return hipErrorInvalidValue;
     hipLaunchKernelGGL((gather_mfma_grid_kernel<KC>), dim3(static_cast<uint32_t>(slots)),
-                       dim3(kWave), 0, stream, a);
+                       dim3(kWave), 4u * a.H, stream, a);
   }
   return hipGetLastError();
 }
@@ -246,8 +284,9 @@ hipError_t launch_gather_mfma(const GatherArgs& a, hipStream_t stream) {
     return hipErrorInvalidValue;
   }
   const uint32_t steps = a.H / kStep;
-  if (steps % 6 == 0) return launch_variant<6>(a, stream);
+  if (steps % 9 == 0) return launch_variant<9>(a, stream);
   if (steps % 8 == 0) return launch_variant<8>(a, stream);
+  if (steps % 6 == 0) return launch_variant<6>(a, stream);
   if (steps % 4 == 0) return launch_variant<4>(a, stream);
   if (steps % 2 == 0) return launch_variant<2>(a, stream);
   return launch_variant<1>(a, stream);

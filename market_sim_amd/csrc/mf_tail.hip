@@ -455,14 +455,18 @@ __global__ __launch_bounds__(kWave) void finalize_kernel(FinalizeArgs a) {
   __shared__ FinalizeShared sh;
   const uint32_t r = blockIdx.x;
   const uint32_t lane = threadIdx.x;
+  // the loads that need nothing else go first: the row's hidden vector, its
+  // metadata and its MFMA-head slot
+  for (uint32_t f = lane; f < a.H; f += kWave) ys[f] = a.y[static_cast<uint64_t>(r) * a.H + f];
   const RowMeta meta = a.row_meta[r];
+  const uint32_t fb_slot = a.fb_map != nullptr ? a.fb_map[r] : kInvalidToken;
   const TileRecord* recs;
   uint32_t ntiles;
   if (meta.kind & kRowRestricted) {
     recs = a.records + static_cast<uint64_t>(r) * a.max_tiles;
     ntiles = (meta.count + a.tile - 1) / a.tile;
   } else if ((meta.kind & kRowUnrestricted) && a.fb_records != nullptr) {
-    const uint32_t m = a.fb_map[r];
+    const uint32_t m = fb_slot;
     if (m == kInvalidToken) return;
     recs = a.fb_records + static_cast<uint64_t>(m) * a.fb_tiles;
     ntiles = a.fb_tiles;
@@ -473,8 +477,6 @@ __global__ __launch_bounds__(kWave) void finalize_kernel(FinalizeArgs a) {
     return;
   }
   const bool virtual_list = meta.kind & kRowUnrestricted;
-  for (uint32_t f = lane; f < a.H; f += kWave) ys[f] = a.y[static_cast<uint64_t>(r) * a.H + f];
-
   __syncthreads();
   // pass 1: validity, the best lower bound of ordinary tiles, lowest id
   uint32_t inv = 0u;
@@ -530,7 +532,36 @@ __global__ __launch_bounds__(kWave) void finalize_kernel(FinalizeArgs a) {
   }
 
   // ordinary tiles: members whose upper bound reaches lg (at most
-  // kTileMembers per tile); collected over all tiles, then rescored together
+  // kTileMembers per tile), collected over all tiles without a barrier per
+  // sweep (the record loads of every sweep are in flight together), then
+  // rescored together.  If the buffer would overflow, the collection is
+  // redone below in flushed sweeps.
+  if (lane == 0) sh.n_cand = 0u;
+  __syncthreads();
+  uint32_t overflow = 0u;
+  for (uint32_t t = lane; t < ntiles; t += kWave) {
+    const TileRecord& q = recs[t];
+    if (q.flags != 0u) continue;
+    const uint32_t nm = q.n_members < kTileMembers ? q.n_members : kTileMembers;
+    for (uint32_t j = 0; j < nm; ++j) {
+      const TileMember mm = q.m[j];
+      if (mm.upper >= lg) {
+        const uint32_t slot = atomicAdd(&sh.n_cand, 1u);
+        if (slot < kCandMax) {
+          sh.cand_token[slot] = mm.token;
+          sh.cand_pos[slot] = mm.pos;
+        } else {
+          overflow = 1u;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  if (wave_sum_u32(overflow) == 0u) {
+    const uint32_t nc = sh.n_cand;
+    if (nc > 0) best = best_of(best, rescore_candidates(a, ys, es, sh, nc));
+  } else {
+  __syncthreads();
   if (lane == 0) sh.n_cand = 0u;
   __syncthreads();
   for (uint32_t t0 = 0; t0 < ntiles; t0 += kWave) {
@@ -558,6 +589,7 @@ __global__ __launch_bounds__(kWave) void finalize_kernel(FinalizeArgs a) {
       if (lane == 0) sh.n_cand = 0u;
       __syncthreads();
     }
+  }
   }
 
   if (lane == 0) {
