@@ -403,6 +403,7 @@ __device__ float chain_lds(const float* ys, const uint16_t* row, uint32_t H) {
 }
 
 constexpr uint32_t kCandMax = 2 * kWave * kTileMembers;
+constexpr uint32_t kRecBlock = 4;  // tile records per lane loaded together
 
 struct FinalizeShared {
   uint32_t cand_token[kCandMax];
@@ -484,14 +485,27 @@ __global__ __launch_bounds__(kWave) void finalize_kernel(FinalizeArgs a) {
   float lg = -__builtin_huge_valf();
   uint32_t mt = kInvalidToken;
   uint32_t mp = 0u;
-  for (uint32_t t = lane; t < ntiles; t += kWave) {
-    const TileRecord& q = recs[t];
-    inv |= (q.flags & kTileInvalid) ? 1u : 0u;
-    any_all |= (q.flags & kTileRescoreAll) ? 1u : 0u;
-    if (q.flags == 0u) lg = __builtin_fmaxf(lg, q.best_lower);
-    if (q.min_token < mt) {
-      mt = q.min_token;
-      mp = q.min_pos;
+  // headers (the first 16 bytes: best_lower, flags, min_token, min_pos) of
+  // kRecBlock tiles per lane are loaded before any is used, so a row with
+  // many tiles (an MFMA-head row has V / 128) costs one round trip per block
+  for (uint32_t base = 0; base < ntiles; base += kWave * kRecBlock) {
+    uint4 h[kRecBlock];
+#pragma unroll
+    for (uint32_t u = 0; u < kRecBlock; ++u) {
+      const uint32_t t = base + u * kWave + lane;
+      h[u] = t < ntiles ? *reinterpret_cast<const uint4*>(&recs[t])
+                        : uint4{__float_as_uint(-__builtin_huge_valf()), 0u, kInvalidToken, 0u};
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < kRecBlock; ++u) {
+      const uint32_t flags = h[u].y;
+      inv |= (flags & kTileInvalid) ? 1u : 0u;
+      any_all |= (flags & kTileRescoreAll) ? 1u : 0u;
+      if (flags == 0u) lg = __builtin_fmaxf(lg, __uint_as_float(h[u].x));
+      if (h[u].z < mt) {
+        mt = h[u].z;
+        mp = h[u].w;
+      }
     }
   }
   const bool invalid = wave_sum_u32(inv) != 0u;
@@ -539,19 +553,35 @@ __global__ __launch_bounds__(kWave) void finalize_kernel(FinalizeArgs a) {
   if (lane == 0) sh.n_cand = 0u;
   __syncthreads();
   uint32_t overflow = 0u;
-  for (uint32_t t = lane; t < ntiles; t += kWave) {
-    const TileRecord& q = recs[t];
-    if (q.flags != 0u) continue;
-    const uint32_t nm = q.n_members < kTileMembers ? q.n_members : kTileMembers;
-    for (uint32_t j = 0; j < nm; ++j) {
-      const TileMember mm = q.m[j];
-      if (mm.upper >= lg) {
-        const uint32_t slot = atomicAdd(&sh.n_cand, 1u);
-        if (slot < kCandMax) {
-          sh.cand_token[slot] = mm.token;
-          sh.cand_pos[slot] = mm.pos;
-        } else {
-          overflow = 1u;
+  for (uint32_t base = 0; base < ntiles; base += kWave * kRecBlock) {
+    // flags / member counts and the first member of kRecBlock tiles per lane
+    // in one round trip; the (rare) further members are read afterwards
+    uint4 h[kRecBlock];
+    uint4 c[kRecBlock];
+    TileMember m0[kRecBlock];
+#pragma unroll
+    for (uint32_t u = 0; u < kRecBlock; ++u) {
+      const uint32_t t = base + u * kWave + lane;
+      const bool in = t < ntiles;
+      h[u] = in ? *reinterpret_cast<const uint4*>(&recs[t]) : uint4{0u, kTileInvalid, 0u, 0u};
+      c[u] = in ? *reinterpret_cast<const uint4*>(&recs[t].begin) : uint4{0u, 0u, 0u, 0u};
+      m0[u] = in ? recs[t].m[0] : TileMember{0u, 0u, 0.0f, -__builtin_huge_valf()};
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < kRecBlock; ++u) {
+      if (h[u].y != 0u) continue;
+      const uint32_t t = base + u * kWave + lane;
+      const uint32_t nm = c[u].z < kTileMembers ? c[u].z : kTileMembers;
+      for (uint32_t j = 0; j < nm; ++j) {
+        const TileMember mm = j == 0 ? m0[u] : recs[t].m[j];
+        if (mm.upper >= lg) {
+          const uint32_t slot = atomicAdd(&sh.n_cand, 1u);
+          if (slot < kCandMax) {
+            sh.cand_token[slot] = mm.token;
+            sh.cand_pos[slot] = mm.pos;
+          } else {
+            overflow = 1u;
+          }
         }
       }
     }
