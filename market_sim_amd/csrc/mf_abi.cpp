@@ -669,6 +669,7 @@ mf_status decode_tail_stage(const mf_decode_tail_args* args, uintptr_t stream, S
       f.fb_map = reinterpret_cast<uint32_t*>(ws + L.fb_map);
       mfma_bound_coefs(a->hidden, f.coef, f.coef2);
       f.slack = underflow_slack(a->hidden);
+      f.groups = device_cus();
       e = mf::launch_fallback(f, s);
       break;
     }

@@ -260,6 +260,28 @@ struct alignas(16) TileRecord {
   TileMember m[kTileMembers];
 };
 
+// Copies n 16-byte pieces from global memory to LDS with `lanes` threads
+// (this one is `tid`), kBatch loads per thread in flight before their stores:
+// a loop that stores each load before issuing the next pays a memory round
+// trip per iteration.
+template <uint32_t kBatch>
+__device__ __forceinline__ void copy16_to_lds(uint4* dst, const uint4* src, uint32_t n,
+                                              uint32_t tid, uint32_t lanes) {
+  for (uint32_t base = tid; base < n; base += lanes * kBatch) {
+    uint4 v[kBatch];
+#pragma unroll
+    for (uint32_t u = 0; u < kBatch; ++u) {
+      const uint32_t q = base + u * lanes;
+      v[u] = q < n ? src[q] : uint4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < kBatch; ++u) {
+      const uint32_t q = base + u * lanes;
+      if (q < n) dst[q] = v[u];
+    }
+  }
+}
+
 // Per-row metadata written by the decode-tail norm kernel.
 enum : uint32_t { kRowRestricted = 1u, kRowUnrestricted = 2u, kRowInvalid = 4u };
 struct alignas(16) RowMeta {

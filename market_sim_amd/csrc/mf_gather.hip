@@ -125,13 +125,36 @@ __device__ void mfma_tile(const GatherArgs& a, uint32_t r, uint32_t k, uint32_t 
   const uint32_t units = nblocks * chunks;
   const uint32_t kb = lane / kBlock;   // k-block: features 8 kb .. 8 kb + 7 of a step
   const uint32_t col = lane % kBlock;  // B column (token) and A row of this lane
+  const uint32_t unit_f = kStep * KC;
+  // unit q = (block q / chunks, chunk q % chunks); the B column's token
+  auto load_q = [&](uint32_t q, Operands<KC>& o) {
+    const uint32_t j = q / chunks;
+    const uint32_t bt = static_cast<uint32_t>(__shfl(static_cast<int>(t),
+                                                     static_cast<int>(j * kBlock + col)));
+    load_unit<KC>(a.emb + static_cast<uint64_t>(bt) * H + kb * 8u, (q % chunks) * unit_f, o);
+  };
+  Operands<KC> o0, o1;
+  // the first unit's table rows are in flight during the staging
+  load_q(0, o0);
   if (staged != r) {
-    // the row's FP16 split into the wave's stage (16 bytes per copy)
+    // the row's FP16 split into the wave's stage (16 bytes per copy), four
+    // loads per lane in flight before their stores
+    constexpr uint32_t kBatch = 4;
     const uint32_t per = H / 8;
-    for (uint32_t q = lane; q < 2u * per; q += kWave) {
-      const uint16_t* src = (q < per ? a.y_hi : a.y_lo) + static_cast<uint64_t>(r) * H;
-      *reinterpret_cast<uint4*>(stage + q * 8) =
-          *reinterpret_cast<const uint4*>(src + (q % per) * 8);
+    const uint32_t n = 2u * per;
+    for (uint32_t base = lane; base < n; base += kWave * kBatch) {
+      uint4 v[kBatch];
+#pragma unroll
+      for (uint32_t u = 0; u < kBatch; ++u) {
+        const uint32_t q = base + u * kWave;
+        const uint16_t* src = (q < per ? a.y_hi : a.y_lo) + static_cast<uint64_t>(r) * H;
+        v[u] = q < n ? *reinterpret_cast<const uint4*>(src + (q % per) * 8) : uint4{0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+      for (uint32_t u = 0; u < kBatch; ++u) {
+        const uint32_t q = base + u * kWave;
+        if (q < n) *reinterpret_cast<uint4*>(stage + q * 8) = v[u];
+      }
     }
     staged = r;
     // LDS writes of this wave complete before any lane reads them
@@ -142,16 +165,7 @@ __device__ void mfma_tile(const GatherArgs& a, uint32_t r, uint32_t k, uint32_t 
   // A rows 0 (hi) and 1 (lo); rows 2..15 read lo too and are masked
   const uint32_t amask = col < 2u ? 0xFFFFFFFFu : 0u;
   const uint16_t* a_lane = stage + (col == 0u ? 0u : H) + kb * 8u;
-  const uint32_t unit_f = kStep * KC;
-  // unit q = (block q / chunks, chunk q % chunks); the B column's token
-  auto load_q = [&](uint32_t q, Operands<KC>& o) {
-    const uint32_t j = q / chunks;
-    const uint32_t bt = static_cast<uint32_t>(__shfl(static_cast<int>(t),
-                                                     static_cast<int>(j * kBlock + col)));
-    load_unit<KC>(a.emb + static_cast<uint64_t>(bt) * H + kb * 8u, (q % chunks) * unit_f, o);
-  };
 
-  Operands<KC> o0, o1;
   floatx4 sc = {0.0f, 0.0f, 0.0f, 0.0f};
   floatx4 gram = {0.0f, 0.0f, 0.0f, 0.0f};
   float g_mine = 0.0f;
@@ -163,7 +177,6 @@ __device__ void mfma_tile(const GatherArgs& a, uint32_t r, uint32_t k, uint32_t 
     mma_unit<KC>(o, a_lane, (q % chunks) * unit_f, amask, sc, gram);
     if (q % chunks == chunks - 1u) finish_block(q / chunks, lane, sc, gram, g_mine, sq_mine);
   };
-  load_q(0, o0);
   uint32_t q = 0;
   for (; q + 2 < units; q += 2) {
     load_q(q + 1, o1);

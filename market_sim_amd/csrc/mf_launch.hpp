@@ -178,8 +178,10 @@ struct FallbackArgs {
   const uint16_t* emb;
   uint32_t H;
   uint32_t V;
-  TileRecord* records;      // [m, tiles]
+  TileRecord* records;      // [m, tiles] (fallback_tiles(V) tiles of 192 tokens)
   uint32_t* fb_map;         // [rows] written: row -> m
+  uint32_t groups;          // compute units: workgroups per M-tile
+  uint32_t tiles_per_group; // set by the launcher
   float coef;               // b = ||e|| * (coef * ||y|| + coef2) + slack
   float coef2;
   float slack;

@@ -246,135 +246,70 @@ __device__ __forceinline__ uint32_t group8_and(uint32_t v) {
   return v;
 }
 
-// Window records of one 128-token tile for the (up to) 32 rows of an
-// M-tile, from scores and bounds staged in LDS: per row, eight lanes cover
-// 16 tokens each.  Called by all 256 threads after a barrier.
-__device__ void write_fallback_records(const FallbackArgs& f, const float (*g_tile)[kTileTokens],
-                                       const float (*b_tile)[kTileTokens],
-                                       const uint32_t* src_row, uint32_t m0, uint32_t tile,
-                                       uint32_t tiles) {
-  const uint32_t tok0 = tile * kTileTokens;
-  // per row (8 lanes, 16 tokens each): the tile's window record
-  const uint32_t i = threadIdx.x / 8;
-  const uint32_t sub = threadIdx.x % 8;
-  const uint32_t nt = f.V - tok0 < kTileTokens ? f.V - tok0 : kTileTokens;
-  uint32_t fin = 1u;
-  float lo = -__builtin_huge_valf();
-  for (uint32_t c = sub; c < nt; c += 8) {
-    const float g = g_tile[i][c];
-    const float b = b_tile[i][c];
-    fin &= (__builtin_isfinite(g) && __builtin_isfinite(b) && b < 0x1p100f) ? 1u : 0u;
-    lo = __builtin_fmaxf(lo, g - b);
-  }
-  fin = group8_and(fin);
-  const float L = group8_max(lo);
-  uint32_t cnt = 0u;
-  for (uint32_t c = sub; c < nt; c += 8) cnt += (g_tile[i][c] + b_tile[i][c] >= L) ? 1u : 0u;
-  // exclusive prefix of the member counts across the row's 8 lanes
-  uint32_t incl = cnt;
-#pragma unroll
-  for (int d = 1; d < 8; d <<= 1) {
-    const uint32_t o = __shfl_up(incl, d, 8);
-    if (static_cast<int>(sub) >= d) incl += o;
-  }
-  const uint32_t total = __shfl(incl, 7, 8);
-  const bool row_ok = src_row[i] != 0xFFFFFFFFu;
-  if (!row_ok) return;
-  TileRecord* rec = f.records + static_cast<uint64_t>(m0 + i) * tiles + tile;
-  const bool ordinary = fin && total <= static_cast<uint32_t>(kTileMembers);
-  if (ordinary) {
-    uint32_t rank = incl - cnt;
-    for (uint32_t c = sub; c < nt; c += 8) {
-      const float g = g_tile[i][c];
-      const float b = b_tile[i][c];
-      if (g + b >= L) {
-        rec->m[rank] = TileMember{tok0 + c, tok0 + c, g - b, g + b};
-        ++rank;
-      }
-    }
-  }
-  if (sub == 0) {
-    rec->best_lower = L;
-    rec->flags = ordinary ? 0u : kTileRescoreAll;
-    rec->min_token = tok0;
-    rec->min_pos = tok0;
-    rec->begin = tok0;
-    rec->count = nt;
-    rec->n_members = ordinary ? total : 0u;
-  }
-}
-
-__global__ __launch_bounds__(kThreads) void fallback_kernel(FallbackArgs f) {
-  __shared__ ProjShared sh;
-  __shared__ uint32_t src_row[kMTile];  // source row of A row i (>= rows: none)
-  __shared__ float src_norm[kMTile];    // its ||y|| bound
-  const uint32_t tile = blockIdx.x;
-  const uint32_t m0 = blockIdx.y * kMTile;
-  const uint32_t tiles = gridDim.x;
-  const int lane = threadIdx.x % 64;
-  const int wave = threadIdx.x / 64;
-  const uint32_t tok0 = tile * kTileTokens;
-  const AView A{nullptr, f.y_hi, f.y_lo, f.row_index, f.m, f.rows, f.H};
-  // resolved before the main loop (its first barrier publishes them), so
-  // the epilogue waits on no global load
-  if (threadIdx.x < kMTile) {
-    const uint32_t row = a_source_row(A, m0 + threadIdx.x);
-    const bool ok = row < f.rows;
-    src_row[threadIdx.x] = ok ? row : 0xFFFFFFFFu;
-    src_norm[threadIdx.x] = ok ? f.row_norm[row] : 0.0f;
-    if (tile == 0 && ok) f.fb_map[row] = m0 + threadIdx.x;
-  }
-  float tok_sq;
-  const floatx16 acc = project_block<ASrc::kF16Pair>(A, f.emb, f.V, m0, tok0, sh, tok_sq);
-
-  // scores and bounds into LDS (the staging area is free after the loop)
-  const float tok_norm = __fsqrt_rn(tok_sq) * (1.0f + 0x1p-7f);
-#pragma unroll
-  for (int v = 0; v < 16; ++v) {
-    const int i = acc_row(v, lane);
-    const float yn = src_norm[i];
-    sh.epi.g[i][wave * 32 + (lane % 32)] = acc[v];
-    sh.epi.b[i][wave * 32 + (lane % 32)] =
-        __builtin_fmaf(tok_norm, __builtin_fmaf(f.coef, yn, f.coef2), f.slack);
-  }
-  __syncthreads();
-
-  write_fallback_records(f, sh.epi.g, sh.epi.b, src_row, m0, tile, tiles);
-}
-
-
-// ---- register-direct MFMA head ---------------------------------------------
+// ---- MFMA head of the unrestricted rows -----------------------------------
 //
-// The same tiles and records as fallback_kernel, with the operands loaded
-// straight from memory into the registers of v_mfma_f32_16x16x32_f16 (no
-// LDS staging, no barrier until the epilogue).  Each wave owns 32 tokens
-// (two 16-token blocks) of the workgroup's 128 and all 32 rows of the M-tile
-// as four 16-row blocks: A rows 2j and 2j + 1 of block rb are the hi and lo
-// halves of row 8 rb + j.  In the 16x16x32 layout lane l holds 8 consecutive
-// features of column / A row l % 16 at k-block l / 16, so the four lanes of
-// a token read 64 contiguous bytes per step.  A (the FP16 split of at most
-// 32 hidden rows) is read from L2; a second MFMA of each token block with
-// itself gives the squared token norms (Gram diagonal).
+// A workgroup owns the 32 rows of an M-tile and a contiguous run of 192-token
+// tiles (one window record per row and tile); the runs are sized so that
+// every compute unit gets the same number of tiles.  Each wave owns 48
+// tokens of a tile, three 16-token blocks of v_mfma_f32_16x16x32_f16, and
+// all 32 rows as four 16-row blocks: A rows 2j and 2j + 1 of block rb are
+// the hi and lo halves of row 8 rb + j.  In the 16x16x32 layout lane l holds
+// 8 consecutive features of column / A row l % 16 at k-block l / 16, so the
+// four lanes of a token read 64 contiguous bytes per step.  The table rows
+// go straight from memory into the MFMA registers, two units of KC steps in
+// flight; A comes from an LDS stage of the M-tile's FP16 split (while it
+// fits two 32-row stages... one per workgroup) or, for wide rows, from L2.
+// A second MFMA of each token block with itself gives the squared token
+// norms (Gram diagonal) for the error bound.
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
-constexpr int kDirectKC = 2;  // MFMA steps (32 features each) per unit
+constexpr uint32_t kHeadBlocks = 3;                                   // per wave
+constexpr uint32_t kHeadTileTokens = (kThreads / 64) * 16 * kHeadBlocks;  // 192
+constexpr uint32_t kAStagePad = 8;  // halves; spreads the 16 row-parts of a read over banks
+__host__ __device__ constexpr uint32_t a_stage_bytes(uint32_t H) {
+  return kMTile * 2u * (H + kAStagePad) * 2u;
+}
+constexpr uint32_t kAStageMaxBytes = 76u * 1024u;
 
-struct DirectUnit {
-  half8_t b[2][kDirectKC];
-  half8_t a[4][kDirectKC];
+// Per-wave partial results of the tile's window records.
+struct HeadEpi {
+  float lo[kThreads / 64][kMTile];
+  uint32_t fin[kThreads / 64][kMTile];
+  uint32_t cnt[kThreads / 64][kMTile];
 };
 
-// Straight-line loads (no predication, no branches): rows outside the M-tile
-// read a valid row and are zeroed by a mask applied just before the MFMA, so
-// the compiler can count the loads in flight and wait only for the unit about
-// to be multiplied.
-__device__ __forceinline__ void direct_load(const uint16_t* const (&bptr)[2],
-                                            const uint16_t* const (&aptr)[4], uint32_t f0,
-                                            DirectUnit& u) {
+// Units of KC steps: table rows only (A from LDS) or table rows and A (A
+// from L2).  All loads are straight-line: a load under a branch makes the
+// compiler wait for every load in flight before the next MFMA.
+template <int KC>
+struct BUnit {
+  half8_t b[kHeadBlocks][KC];
+};
+template <int KC>
+struct ABUnit {
+  half8_t b[kHeadBlocks][KC];
+  half8_t a[4][KC];
+};
+
+template <int KC>
+__device__ __forceinline__ void unit_load(const uint16_t* const (&bptr)[kHeadBlocks],
+                                          uint32_t f0, BUnit<KC>& u) {
 #pragma unroll
-  for (int s = 0; s < kDirectKC; ++s) {
+  for (int s = 0; s < KC; ++s) {
 #pragma unroll
-    for (int tb = 0; tb < 2; ++tb) {
+    for (uint32_t tb = 0; tb < kHeadBlocks; ++tb) {
+      u.b[tb][s] = *reinterpret_cast<const half8_t*>(bptr[tb] + f0 + s * 32);
+    }
+  }
+}
+template <int KC>
+__device__ __forceinline__ void unit_load(const uint16_t* const (&bptr)[kHeadBlocks],
+                                          const uint16_t* const (&aptr)[4], uint32_t f0,
+                                          ABUnit<KC>& u) {
+#pragma unroll
+  for (int s = 0; s < KC; ++s) {
+#pragma unroll
+    for (uint32_t tb = 0; tb < kHeadBlocks; ++tb) {
       u.b[tb][s] = *reinterpret_cast<const half8_t*>(bptr[tb] + f0 + s * 32);
     }
 #pragma unroll
@@ -393,234 +328,341 @@ __device__ __forceinline__ half8_t masked(const half8_t& v, uint32_t mask) {
   return __builtin_bit_cast(half8_t, q);
 }
 
-__device__ __forceinline__ void direct_mma(const DirectUnit& u, const uint32_t (&amask)[4],
-                                           floatx4 (&acc)[4][2], floatx4 (&gram)[2]) {
-#pragma unroll
-  for (int s = 0; s < kDirectKC; ++s) {
-#pragma unroll
-    for (int tb = 0; tb < 2; ++tb) {
-      gram[tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(u.b[tb][s], u.b[tb][s], gram[tb], 0, 0, 0);
-    }
-#pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
-      const half8_t a = masked(u.a[rb][s], amask[rb]);
-#pragma unroll
-      for (int tb = 0; tb < 2; ++tb) {
-        acc[rb][tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, u.b[tb][s], acc[rb][tb], 0, 0, 0);
-      }
-    }
-  }
-}
-
-// A staged in LDS: rows i of the M-tile as [i][hi|lo][H + 8] halves (the
-// 16-byte pad spreads the 16 row-parts of one MFMA read over distinct banks);
-// rows outside the M-tile are zero.  Used while it fits two workgroups per
-// CU; the scores of the epilogue reuse the same LDS.
-constexpr uint32_t kAStagePad = 8;
-__host__ __device__ constexpr uint32_t a_stage_bytes(uint32_t H) {
-  return kMTile * 2u * (H + kAStagePad) * 2u;
-}
-constexpr uint32_t kAStageMaxBytes = 76u * 1024u;
-
-template <int KC>
-struct BUnit {
-  half8_t b[2][KC];
+struct HeadAcc {
+  floatx4 acc[4][kHeadBlocks];
+  floatx4 gram[kHeadBlocks];
 };
 
+// MFMAs of one unit.  A from the LDS stage: a_lane points at the lane's
+// row-part of block 0 (rows outside the M-tile are zero in the stage).
 template <int KC>
-__device__ __forceinline__ void b_load(const uint16_t* const (&bptr)[2], uint32_t f0,
-                                       BUnit<KC>& u) {
+__device__ __forceinline__ void unit_mma(const BUnit<KC>& u, const uint16_t* a_lane,
+                                         uint32_t rb_stride, uint32_t f0, HeadAcc& h) {
 #pragma unroll
   for (int s = 0; s < KC; ++s) {
 #pragma unroll
-    for (int tb = 0; tb < 2; ++tb) {
-      u.b[tb][s] = *reinterpret_cast<const half8_t*>(bptr[tb] + f0 + s * 32);
-    }
-  }
-}
-
-template <int KC>
-__device__ __forceinline__ void lds_a_mma(const BUnit<KC>& u, const uint16_t* a_lane, uint32_t f0,
-                                          uint32_t rb_stride, floatx4 (&acc)[4][2],
-                                          floatx4 (&gram)[2]) {
-#pragma unroll
-  for (int s = 0; s < KC; ++s) {
-#pragma unroll
-    for (int tb = 0; tb < 2; ++tb) {
-      gram[tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(u.b[tb][s], u.b[tb][s], gram[tb], 0, 0, 0);
+    for (uint32_t tb = 0; tb < kHeadBlocks; ++tb) {
+      h.gram[tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(u.b[tb][s], u.b[tb][s], h.gram[tb], 0, 0, 0);
     }
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) {
       const half8_t a = *reinterpret_cast<const half8_t*>(a_lane + rb * rb_stride + f0 + s * 32);
 #pragma unroll
-      for (int tb = 0; tb < 2; ++tb) {
-        acc[rb][tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, u.b[tb][s], acc[rb][tb], 0, 0, 0);
+      for (uint32_t tb = 0; tb < kHeadBlocks; ++tb) {
+        h.acc[rb][tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, u.b[tb][s], h.acc[rb][tb], 0, 0, 0);
+      }
+    }
+  }
+}
+// A from L2, rows outside the M-tile masked
+template <int KC>
+__device__ __forceinline__ void unit_mma(const ABUnit<KC>& u, const uint32_t (&amask)[4],
+                                         HeadAcc& h) {
+#pragma unroll
+  for (int s = 0; s < KC; ++s) {
+#pragma unroll
+    for (uint32_t tb = 0; tb < kHeadBlocks; ++tb) {
+      h.gram[tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(u.b[tb][s], u.b[tb][s], h.gram[tb], 0, 0, 0);
+    }
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+      const half8_t a = masked(u.a[rb][s], amask[rb]);
+#pragma unroll
+      for (uint32_t tb = 0; tb < kHeadBlocks; ++tb) {
+        h.acc[rb][tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, u.b[tb][s], h.acc[rb][tb], 0, 0, 0);
       }
     }
   }
 }
 
-// kALds: A from the LDS stage (one VMEM instruction per token block and
-// step remains); otherwise A from L2 with B in the same units.  KC steps per
-// unit with the LDS stage: two units, 2 x KC x 2 KiB of table rows, are in
-// flight per wave (all of a 576-feature row at KC = 9).
+// kALds: A from the LDS stage; otherwise from L2 (wide rows).  KC steps per
+// unit, two units in flight; the steady-state loop has no branch around a
+// load, and sched_barrier(0) keeps each unit's loads issued before the
+// previous unit's MFMAs (the scheduler would otherwise sink them past the
+// MFMAs and every unit would wait a full round trip).
 template <bool kALds, int KC>
-__global__ __launch_bounds__(kThreads) void fallback_direct_kernel(FallbackArgs f) {
+__global__ __launch_bounds__(kThreads) void head_kernel(FallbackArgs f) {
   extern __shared__ __align__(16) unsigned char dyn[];
   __shared__ uint32_t src_row[kMTile];
   __shared__ float src_norm[kMTile];
-  float(*sh_g)[kTileTokens] = reinterpret_cast<float(*)[kTileTokens]>(dyn);
-  float(*sh_b)[kTileTokens] = reinterpret_cast<float(*)[kTileTokens]>(dyn + kMTile * kTileTokens * 4);
-  const uint32_t tile = blockIdx.x;
+  HeadEpi& epi = *reinterpret_cast<HeadEpi*>(dyn);
   const uint32_t m0 = blockIdx.y * kMTile;
-  const uint32_t tiles = gridDim.x;
+  const uint32_t tiles = (f.V + kHeadTileTokens - 1) / kHeadTileTokens;
+  const uint32_t t_begin = blockIdx.x * f.tiles_per_group;
+  const uint32_t t_end = t_begin + f.tiles_per_group < tiles ? t_begin + f.tiles_per_group : tiles;
   const uint32_t lane = threadIdx.x % 64;
   const uint32_t wave = threadIdx.x / 64;
-  const uint32_t tok0 = tile * kTileTokens;
   const uint32_t H = f.H;
   const uint32_t col = lane % 16;
   const uint32_t kb = lane / 16;
   const AView A{nullptr, f.y_hi, f.y_lo, f.row_index, f.m, f.rows, H};
-  const uint16_t* bptr[2];
-#pragma unroll
-  for (int tb = 0; tb < 2; ++tb) {
-    const uint32_t token = tok0 + wave * 32 + tb * 16 + col;
-    bptr[tb] = f.emb + static_cast<uint64_t>(token < f.V ? token : 0u) * H + kb * 8;
-  }
   if (threadIdx.x < kMTile) {
     const uint32_t row = a_source_row(A, m0 + threadIdx.x);
     const bool ok = row < f.rows;
     src_row[threadIdx.x] = ok ? row : 0xFFFFFFFFu;
     src_norm[threadIdx.x] = ok ? f.row_norm[row] : 0.0f;
-    if (tile == 0 && ok) f.fb_map[row] = m0 + threadIdx.x;
-  }
-
-  floatx4 acc[4][2];
-  floatx4 gram[2];
-#pragma unroll
-  for (int tb = 0; tb < 2; ++tb) {
-    gram[tb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int rb = 0; rb < 4; ++rb) acc[rb][tb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-  }
-  // units of KC steps, two in flight (H % 64 == 0).  The steady-state loop
-  // has no branch around a load (a load under a branch makes the compiler
-  // wait for every load in flight), and sched_barrier(0) keeps each unit's
-  // loads issued before the previous unit's MFMAs (the scheduler would
-  // otherwise sink them past the MFMAs and every unit would wait a full
-  // round trip).
-  if constexpr (kALds) {
-    const uint32_t units = H / (32 * KC);
-    constexpr uint32_t kUnitF = 32 * KC;
-    uint16_t* stage = reinterpret_cast<uint16_t*>(dyn);
-    const uint32_t row_halves = H + kAStagePad;
-    BUnit<KC> u0, u1;
-    b_load(bptr, 0, u0);  // in flight during the staging
-    __syncthreads();      // src_row
-    // stage A: 64 row-parts x H halves, 16 bytes per copy
-    const uint32_t per = H / 8;
-    for (uint32_t q = threadIdx.x; q < 64u * per; q += kThreads) {
-      const uint32_t p = q / per;
-      const uint32_t c = q % per;
-      const uint32_t row = src_row[p / 2];
-      uint4 v = uint4{0u, 0u, 0u, 0u};
-      if (row != 0xFFFFFFFFu) {
-        v = *reinterpret_cast<const uint4*>(((p & 1u) ? f.y_lo : f.y_hi) +
-                                           static_cast<uint64_t>(row) * H + c * 8);
-      }
-      *reinterpret_cast<uint4*>(stage + p * row_halves + c * 8) = v;
-    }
-    __syncthreads();
-    // lane's A row-part in block rb: row 8 rb + col / 2, part col & 1
-    const uint16_t* a_lane = stage + col * row_halves + kb * 8;
-    const uint32_t rb_stride = 16u * row_halves;
-    uint32_t q = 0;
-    for (; q + 2 < units; q += 2) {
-      b_load(bptr, (q + 1) * kUnitF, u1);
-      __builtin_amdgcn_sched_barrier(0);
-      lds_a_mma(u0, a_lane, q * kUnitF, rb_stride, acc, gram);
-      __builtin_amdgcn_sched_barrier(0);
-      b_load(bptr, (q + 2) * kUnitF, u0);
-      __builtin_amdgcn_sched_barrier(0);
-      lds_a_mma(u1, a_lane, (q + 1) * kUnitF, rb_stride, acc, gram);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    // the last one or two units
-    if (q + 1 < units) {
-      b_load(bptr, (q + 1) * kUnitF, u1);
-      __builtin_amdgcn_sched_barrier(0);
-      lds_a_mma(u0, a_lane, q * kUnitF, rb_stride, acc, gram);
-      lds_a_mma(u1, a_lane, (q + 1) * kUnitF, rb_stride, acc, gram);
-    } else {
-      lds_a_mma(u0, a_lane, q * kUnitF, rb_stride, acc, gram);
-    }
-    __syncthreads();  // every wave is done with the stage before the scores reuse it
-  } else {
-    const uint32_t units = H / (32 * kDirectKC);
-    const uint32_t last = units - 1;
-    constexpr uint32_t kUnitF = 32 * kDirectKC;
-    const uint16_t* aptr[4];
-    uint32_t amask[4];
-#pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
-      const uint32_t row = a_source_row(A, m0 + rb * 8 + col / 2);
-      const bool ok = row < f.rows;
-      aptr[rb] = ((col & 1u) ? f.y_lo : f.y_hi) + static_cast<uint64_t>(ok ? row : 0u) * H + kb * 8;
-      amask[rb] = ok ? 0xFFFFFFFFu : 0u;
-    }
-    DirectUnit u0, u1;
-    direct_load(bptr, aptr, 0, u0);
-    uint32_t q = 0;
-    for (; q + 1 < units; q += 2) {
-      direct_load(bptr, aptr, (q + 1) * kUnitF, u1);
-      __builtin_amdgcn_sched_barrier(0);
-      direct_mma(u0, amask, acc, gram);
-      __builtin_amdgcn_sched_barrier(0);
-      direct_load(bptr, aptr, (q + 2 < last ? q + 2 : last) * kUnitF, u0);
-      __builtin_amdgcn_sched_barrier(0);
-      direct_mma(u1, amask, acc, gram);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    if (q < units) direct_mma(u0, amask, acc, gram);  // odd unit count: the last unit
-    __syncthreads();  // src_row / src_norm
-  }
-
-  // scores and bounds into LDS.  Lane l holds D[4 (l / 16) + i][l % 16]:
-  // rows 2j, 2j + 1 (hi, lo of row 8 rb + j) for j = 2 kb and 2 kb + 1; the
-  // Gram diagonal of column c sits in lane c + 16 (c / 4), element c % 4.
-#pragma unroll
-  for (int tb = 0; tb < 2; ++tb) {
-    const uint32_t e = col % 4u;
-    const float d = e == 0u ? gram[tb][0]
-                            : (e == 1u ? gram[tb][1] : (e == 2u ? gram[tb][2] : gram[tb][3]));
-    const float tsq = __shfl(d, static_cast<int>(col + 16u * (col / 4u)));
-    const float tok_norm = __fsqrt_rn(tsq) * (1.0f + 0x1p-7f);
-    const uint32_t c = wave * 32 + tb * 16 + col;
-#pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
-      const uint32_t i0 = rb * 8 + 2 * kb;
-      const float g0 = acc[rb][tb][0] + acc[rb][tb][1];
-      const float g1 = acc[rb][tb][2] + acc[rb][tb][3];
-      sh_g[i0][c] = g0;
-      sh_g[i0 + 1][c] = g1;
-      sh_b[i0][c] = __builtin_fmaf(tok_norm, __builtin_fmaf(f.coef, src_norm[i0], f.coef2), f.slack);
-      sh_b[i0 + 1][c] =
-          __builtin_fmaf(tok_norm, __builtin_fmaf(f.coef, src_norm[i0 + 1], f.coef2), f.slack);
-    }
+    if (blockIdx.x == 0 && ok) f.fb_map[row] = m0 + threadIdx.x;
   }
   __syncthreads();
-  write_fallback_records(f, sh_g, sh_b, src_row, m0, tile, tiles);
+  const uint32_t row_halves = H + kAStagePad;
+  uint16_t* stage = reinterpret_cast<uint16_t*>(dyn + sizeof(HeadEpi));
+  const uint32_t units = H / (32 * KC);
+  constexpr uint32_t kUnitF = 32 * KC;
+  // table-row pointers of tile t for this lane
+  auto tile_rows = [&](uint32_t t, const uint16_t* (&bptr)[kHeadBlocks]) {
+#pragma unroll
+    for (uint32_t tb = 0; tb < kHeadBlocks; ++tb) {
+      const uint32_t token = t * kHeadTileTokens + wave * (16 * kHeadBlocks) + tb * 16 + col;
+      bptr[tb] = f.emb + static_cast<uint64_t>(token < f.V ? token : 0u) * H + kb * 8;
+    }
+  };
+  const uint16_t* bptr[kHeadBlocks];
+  tile_rows(t_begin, bptr);
+  // the first unit of the first tile is in flight during the A staging
+  BUnit<KC> b0;
+  if constexpr (kALds) unit_load<KC>(bptr, 0, b0);
+  if constexpr (kALds) {
+    // the M-tile's FP16 split, [row][hi|lo][H + pad], zero rows beyond it;
+    // kStageBatch loads per thread are in flight before their stores (a
+    // copy loop that stores each load before the next would pay one round
+    // trip per iteration)
+    constexpr uint32_t kStageBatch = 6;
+    const uint32_t per = H / 8;
+    const uint32_t n = 64u * per;
+    for (uint32_t base = threadIdx.x; base < n; base += kThreads * kStageBatch) {
+      uint4 v[kStageBatch];
+#pragma unroll
+      for (uint32_t u = 0; u < kStageBatch; ++u) {
+        const uint32_t q = base + u * kThreads;
+        const uint32_t p = q / per;
+        const uint32_t row = q < n ? src_row[p / 2] : 0xFFFFFFFFu;
+        v[u] = row != 0xFFFFFFFFu
+                   ? *reinterpret_cast<const uint4*>(((p & 1u) ? f.y_lo : f.y_hi) +
+                                                    static_cast<uint64_t>(row) * H + (q % per) * 8)
+                   : uint4{0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+      for (uint32_t u = 0; u < kStageBatch; ++u) {
+        const uint32_t q = base + u * kThreads;
+        if (q < n) *reinterpret_cast<uint4*>(stage + (q / per) * row_halves + (q % per) * 8) = v[u];
+      }
+    }
+    __syncthreads();
+  }
+  const uint16_t* a_lane = stage + col * row_halves + kb * 8;  // LDS variant
+  const uint32_t rb_stride = 16u * row_halves;
+  const uint16_t* aptr[4];                                     // L2 variant
+  uint32_t amask[4];
+#pragma unroll
+  for (int rb = 0; rb < 4; ++rb) {
+    const uint32_t row = src_row[rb * 8 + col / 2];
+    const bool ok = row != 0xFFFFFFFFu;
+    aptr[rb] = ((col & 1u) ? f.y_lo : f.y_hi) + static_cast<uint64_t>(ok ? row : 0u) * H + kb * 8;
+    amask[rb] = ok ? 0xFFFFFFFFu : 0u;
+  }
+
+  for (uint32_t tile = t_begin; tile < t_end; ++tile) {
+    if (tile != t_begin) tile_rows(tile, bptr);
+    HeadAcc h;
+#pragma unroll
+    for (uint32_t tb = 0; tb < kHeadBlocks; ++tb) {
+      h.gram[tb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb) h.acc[rb][tb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    if constexpr (kALds) {
+      BUnit<KC> u0, u1;
+      if (tile == t_begin) {
+        u0 = b0;
+      } else {
+        unit_load<KC>(bptr, 0, u0);
+      }
+      uint32_t q = 0;
+      for (; q + 2 < units; q += 2) {
+        unit_load<KC>(bptr, (q + 1) * kUnitF, u1);
+        __builtin_amdgcn_sched_barrier(0);
+        unit_mma<KC>(u0, a_lane, rb_stride, q * kUnitF, h);
+        __builtin_amdgcn_sched_barrier(0);
+        unit_load<KC>(bptr, (q + 2) * kUnitF, u0);
+        __builtin_amdgcn_sched_barrier(0);
+        unit_mma<KC>(u1, a_lane, rb_stride, (q + 1) * kUnitF, h);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (q + 1 < units) {  // the last two units
+        unit_load<KC>(bptr, (q + 1) * kUnitF, u1);
+        __builtin_amdgcn_sched_barrier(0);
+        unit_mma<KC>(u0, a_lane, rb_stride, q * kUnitF, h);
+        unit_mma<KC>(u1, a_lane, rb_stride, (q + 1) * kUnitF, h);
+      } else {
+        unit_mma<KC>(u0, a_lane, rb_stride, q * kUnitF, h);
+      }
+    } else {
+      ABUnit<KC> u0, u1;
+      unit_load<KC>(bptr, aptr, 0, u0);
+      uint32_t q = 0;
+      for (; q + 2 < units; q += 2) {
+        unit_load<KC>(bptr, aptr, (q + 1) * kUnitF, u1);
+        __builtin_amdgcn_sched_barrier(0);
+        unit_mma<KC>(u0, amask, h);
+        __builtin_amdgcn_sched_barrier(0);
+        unit_load<KC>(bptr, aptr, (q + 2) * kUnitF, u0);
+        __builtin_amdgcn_sched_barrier(0);
+        unit_mma<KC>(u1, amask, h);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (q + 1 < units) {
+        unit_load<KC>(bptr, aptr, (q + 1) * kUnitF, u1);
+        __builtin_amdgcn_sched_barrier(0);
+        unit_mma<KC>(u0, amask, h);
+        unit_mma<KC>(u1, amask, h);
+      } else {
+        unit_mma<KC>(u0, amask, h);
+      }
+    }
+
+    // The tile's window records, reduced in registers.  Lane l holds
+    // D[4 (l / 16) + i][l % 16] of each block: rows 2j, 2j + 1 (hi, lo of
+    // row 8 rb + j) for j = 2 kb and 2 kb + 1, so the scores of row
+    // 8 rb + 2 kb + jj (jj = 0, 1) are h.acc[rb][tb][2 jj] + [2 jj + 1] for
+    // the wave's tokens wave * 48 + 16 tb + col.  The Gram diagonal of
+    // column c sits in lane c + 16 (c / 4), element c % 4.
+    const uint32_t tok0 = tile * kHeadTileTokens;
+    const uint32_t nt = f.V - tok0 < kHeadTileTokens ? f.V - tok0 : kHeadTileTokens;
+    float g[4][2][kHeadBlocks];
+    float b[4][2][kHeadBlocks];
+    bool valid[kHeadBlocks];
+#pragma unroll
+    for (uint32_t tb = 0; tb < kHeadBlocks; ++tb) {
+      const uint32_t e = col % 4u;
+      const float d = e == 0u ? h.gram[tb][0]
+                              : (e == 1u ? h.gram[tb][1] : (e == 2u ? h.gram[tb][2] : h.gram[tb][3]));
+      const float tsq = __shfl(d, static_cast<int>(col + 16u * (col / 4u)));
+      const float tok_norm = __fsqrt_rn(tsq) * (1.0f + 0x1p-7f);
+      valid[tb] = wave * (16 * kHeadBlocks) + tb * 16 + col < nt;
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb) {
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+          const uint32_t i = rb * 8 + 2 * kb + jj;
+          g[rb][jj][tb] = h.acc[rb][tb][2 * jj] + h.acc[rb][tb][2 * jj + 1];
+          b[rb][jj][tb] =
+              __builtin_fmaf(tok_norm, __builtin_fmaf(f.coef, src_norm[i], f.coef2), f.slack);
+        }
+      }
+    }
+    // per row: the best lower bound g - b and finiteness, over the lane's
+    // tokens, then over the 16 lanes of the row, then over the 4 waves
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        float lo = -__builtin_huge_valf();
+        uint32_t fin = 1u;
+#pragma unroll
+        for (uint32_t tb = 0; tb < kHeadBlocks; ++tb) {
+          if (!valid[tb]) continue;
+          const float gv = g[rb][jj][tb];
+          const float bv = b[rb][jj][tb];
+          fin &= (__builtin_isfinite(gv) && __builtin_isfinite(bv) && bv < 0x1p100f) ? 1u : 0u;
+          lo = __builtin_fmaxf(lo, gv - bv);
+        }
+#pragma unroll
+        for (int m = 8; m > 0; m >>= 1) {
+          lo = __builtin_fmaxf(lo, __shfl_xor(lo, m, 16));
+          fin &= __shfl_xor(fin, m, 16);
+        }
+        if (col == 0u) {
+          epi.lo[wave][rb * 8 + 2 * kb + jj] = lo;
+          epi.fin[wave][rb * 8 + 2 * kb + jj] = fin;
+        }
+      }
+    }
+    __syncthreads();
+    // members (g + b >= L) per row: count per wave, rank across waves
+    float L[4][2];
+    uint32_t rowfin[4][2];
+    uint32_t below[4][2][kHeadBlocks];  // members of this row before (tb, col) in the wave
+    uint32_t mine[4][2];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        const uint32_t i = rb * 8 + 2 * kb + jj;
+        float l = epi.lo[0][i];
+        uint32_t fn = epi.fin[0][i];
+#pragma unroll
+        for (int w = 1; w < 4; ++w) {
+          l = __builtin_fmaxf(l, epi.lo[w][i]);
+          fn &= epi.fin[w][i];
+        }
+        L[rb][jj] = l;
+        rowfin[rb][jj] = fn;
+        uint32_t run = 0u;
+#pragma unroll
+        for (uint32_t tb = 0; tb < kHeadBlocks; ++tb) {
+          const bool member = valid[tb] && g[rb][jj][tb] + b[rb][jj][tb] >= l;
+          const uint64_t mask = __ballot(member);
+          const uint32_t group = static_cast<uint32_t>(mask >> (16u * kb)) & 0xFFFFu;
+          below[rb][jj][tb] = run + static_cast<uint32_t>(__popc(group & ((1u << col) - 1u)));
+          run += static_cast<uint32_t>(__popc(group));
+        }
+        mine[rb][jj] = run;
+        if (col == 0u) epi.cnt[wave][i] = run;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        const uint32_t i = rb * 8 + 2 * kb + jj;
+        if (src_row[i] == 0xFFFFFFFFu) continue;
+        uint32_t base = 0u;
+        uint32_t total = 0u;
+#pragma unroll
+        for (uint32_t w = 0; w < 4; ++w) {
+          const uint32_t c = epi.cnt[w][i];
+          base += w < wave ? c : 0u;
+          total += c;
+        }
+        const bool ordinary = rowfin[rb][jj] && total <= static_cast<uint32_t>(kTileMembers);
+        TileRecord* rec = f.records + static_cast<uint64_t>(m0 + i) * tiles + tile;
+        if (ordinary) {
+#pragma unroll
+          for (uint32_t tb = 0; tb < kHeadBlocks; ++tb) {
+            const float gv = g[rb][jj][tb];
+            const float bv = b[rb][jj][tb];
+            if (valid[tb] && gv + bv >= L[rb][jj]) {
+              const uint32_t token = tok0 + wave * (16 * kHeadBlocks) + tb * 16 + col;
+              rec->m[base + below[rb][jj][tb]] = TileMember{token, token, gv - bv, gv + bv};
+            }
+          }
+        }
+        if (wave == 0 && col == 0u) {
+          rec->best_lower = L[rb][jj];
+          rec->flags = ordinary ? 0u : kTileRescoreAll;
+          rec->min_token = tok0;
+          rec->min_pos = tok0;
+          rec->begin = tok0;
+          rec->count = nt;
+          rec->n_members = ordinary ? total : 0u;
+        }
+      }
+    }
+    (void)mine;
+    __syncthreads();  // the next tile rewrites the scores
+  }
 }
 
 } // namespace
 
 uint32_t fallback_tiles(uint32_t vocab) {
-  return (vocab + kTileTokens - 1) / kTileTokens;
+  return (vocab + kHeadTileTokens - 1) / kHeadTileTokens;
 }
 
 hipError_t launch_projection(const ProjArgs& args, hipStream_t stream) {
   if (args.H % kKC != 0) return hipErrorInvalidValue;
-  const dim3 grid(fallback_tiles(args.V), (args.m + kMTile - 1) / kMTile);
+  const dim3 grid((args.V + kTileTokens - 1) / kTileTokens, (args.m + kMTile - 1) / kMTile);
   if (args.a16 != nullptr) {
     hipLaunchKernelGGL((projection_kernel<ASrc::kF16>), grid, dim3(kThreads), 0, stream, args);
   } else {
@@ -629,29 +671,35 @@ hipError_t launch_projection(const ProjArgs& args, hipStream_t stream) {
   return hipGetLastError();
 }
 
+template <bool kALds, int KC>
+static void launch_head(const FallbackArgs& f, dim3 grid, uint32_t lds, hipStream_t stream) {
+  hipLaunchKernelGGL((head_kernel<kALds, KC>), grid, dim3(kThreads), lds, stream, f);
+}
+
 hipError_t launch_fallback(const FallbackArgs& args, hipStream_t stream) {
   if (args.m == 0) return hipSuccess;
-  if (args.H % kKC != 0) return hipErrorInvalidValue;
-  const dim3 grid(fallback_tiles(args.V), (args.m + kMTile - 1) / kMTile);
-  constexpr uint32_t kEpiBytes = 2u * kMTile * kTileTokens * 4u;
+  if (args.H % 64 != 0) return hipErrorInvalidValue;
+  // runs of tiles per workgroup: as many workgroups as compute units (or
+  // tiles), every run the same length
+  const uint32_t tiles = fallback_tiles(args.V);
+  const uint32_t groups = args.groups > 0 ? args.groups : 256u;
+  FallbackArgs f = args;
+  f.tiles_per_group = (tiles + groups - 1) / groups;
+  const dim3 grid((tiles + f.tiles_per_group - 1) / f.tiles_per_group,
+                  (args.m + kMTile - 1) / kMTile);
+  const uint32_t steps = args.H / 32;  // even
   const uint32_t stage = a_stage_bytes(args.H);
-  const uint32_t steps = args.H / 32;  // even (H % 64 == 0)
   if (stage <= kAStageMaxBytes) {
-    const uint32_t lds = stage > kEpiBytes ? stage : kEpiBytes;
-    if (steps % 9 == 0) {
-      hipLaunchKernelGGL((fallback_direct_kernel<true, 9>), grid, dim3(kThreads), lds, stream, args);
-    } else if (steps % 8 == 0) {
-      hipLaunchKernelGGL((fallback_direct_kernel<true, 8>), grid, dim3(kThreads), lds, stream, args);
-    } else if (steps % 6 == 0) {
-      hipLaunchKernelGGL((fallback_direct_kernel<true, 6>), grid, dim3(kThreads), lds, stream, args);
+    const uint32_t lds = static_cast<uint32_t>(sizeof(HeadEpi)) + stage;
+    if (steps % 6 == 0) {
+      launch_head<true, 6>(f, grid, lds, stream);
     } else if (steps % 4 == 0) {
-      hipLaunchKernelGGL((fallback_direct_kernel<true, 4>), grid, dim3(kThreads), lds, stream, args);
+      launch_head<true, 4>(f, grid, lds, stream);
     } else {
-      hipLaunchKernelGGL((fallback_direct_kernel<true, 2>), grid, dim3(kThreads), lds, stream, args);
+      launch_head<true, 2>(f, grid, lds, stream);
     }
   } else {
-    hipLaunchKernelGGL((fallback_direct_kernel<false, kDirectKC>), grid, dim3(kThreads),
-                       kEpiBytes, stream, args);
+    launch_head<false, 2>(f, grid, static_cast<uint32_t>(sizeof(HeadEpi)), stream);
   }
   return hipGetLastError();
 }

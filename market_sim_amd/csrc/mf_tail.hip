@@ -8,7 +8,7 @@
 //                            (a chunk of one row's list) and writes a tile
 //                            record: the candidates whose [g - b, g + b]
 //                            interval reaches the tile's best lower bound
-//   (K4 fallback_kernel, mf_mfma.hip, writes the same records for
+//   (K4 head_kernel, mf_mfma.hip, writes the same records for
 //    unrestricted rows)
 //   K3 finalize_kernel       per row: merges tile records, rescores the
 //                            surviving candidates in the reference order,
@@ -66,10 +66,34 @@ __global__ __launch_bounds__(kWave) void tail_norm_kernel(TailNormArgs a) {
   const uint64_t r = blockIdx.x;
   const uint32_t lane = threadIdx.x;
   const uint32_t H = a.H;
-  for (uint32_t c = lane; c < H; c += kWave) {
-    const float v = a.x[r * H + c];
-    xs[c] = v;
-    sq[c] = v * v;
+  if ((H & 3u) == 0) {
+    // four float4 loads per lane in flight before the LDS stores
+    constexpr uint32_t kBatch = 4;
+    const float4* x4 = reinterpret_cast<const float4*>(a.x + r * H);
+    const uint32_t n = H / 4;
+    for (uint32_t base = lane; base < n; base += kWave * kBatch) {
+      float4 v[kBatch];
+#pragma unroll
+      for (uint32_t u = 0; u < kBatch; ++u) {
+        const uint32_t q = base + u * kWave;
+        v[u] = q < n ? x4[q] : float4{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+#pragma unroll
+      for (uint32_t u = 0; u < kBatch; ++u) {
+        const uint32_t q = base + u * kWave;
+        if (q < n) {
+          reinterpret_cast<float4*>(xs)[q] = v[u];
+          reinterpret_cast<float4*>(sq)[q] =
+              float4{v[u].x * v[u].x, v[u].y * v[u].y, v[u].z * v[u].z, v[u].w * v[u].w};
+        }
+      }
+    }
+  } else {
+    for (uint32_t c = lane; c < H; c += kWave) {
+      const float v = a.x[r * H + c];
+      xs[c] = v;
+      sq[c] = v * v;
+    }
   }
   __syncthreads();
   RowMeta meta{0u, 0u, 0u, kRowInvalid};
@@ -426,12 +450,27 @@ __device__ Best rescore_candidates(const FinalizeArgs& a, const float* ys, uint1
     const uint32_t m = n - base < kStage ? n - base : kStage;
     __syncthreads();
     if ((H & 7u) == 0) {
+      // every row's pieces in flight before their stores (kStage rows of
+      // H / 8 pieces over 64 lanes)
+      constexpr uint32_t kBatch = 10;
       const uint32_t per = H / 8;
-      for (uint32_t q = lane; q < m * per; q += kWave) {
-        const uint32_t j = q / per;
-        const uint32_t i = q % per;
-        reinterpret_cast<uint4*>(es + j * H)[i] =
-            reinterpret_cast<const uint4*>(a.emb + static_cast<uint64_t>(sh.cand_token[base + j]) * H)[i];
+      const uint32_t total = m * per;
+      for (uint32_t q0 = lane; q0 < total; q0 += kWave * kBatch) {
+        uint4 v[kBatch];
+#pragma unroll
+        for (uint32_t u = 0; u < kBatch; ++u) {
+          const uint32_t q = q0 + u * kWave;
+          const uint32_t j = q / per;
+          v[u] = q < total
+                     ? reinterpret_cast<const uint4*>(
+                           a.emb + static_cast<uint64_t>(sh.cand_token[base + j]) * H)[q % per]
+                     : uint4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < kBatch; ++u) {
+          const uint32_t q = q0 + u * kWave;
+          if (q < total) reinterpret_cast<uint4*>(es + (q / per) * H)[q % per] = v[u];
+        }
       }
     } else {
       for (uint32_t q = lane; q < m * H; q += kWave) {
@@ -458,7 +497,13 @@ __global__ __launch_bounds__(kWave) void finalize_kernel(FinalizeArgs a) {
   const uint32_t lane = threadIdx.x;
   // the loads that need nothing else go first: the row's hidden vector, its
   // metadata and its MFMA-head slot
-  for (uint32_t f = lane; f < a.H; f += kWave) ys[f] = a.y[static_cast<uint64_t>(r) * a.H + f];
+  if ((a.H & 3u) == 0) {
+    copy16_to_lds<4>(reinterpret_cast<uint4*>(ys),
+                     reinterpret_cast<const uint4*>(a.y + static_cast<uint64_t>(r) * a.H), a.H / 4,
+                     lane, kWave);
+  } else {
+    for (uint32_t f = lane; f < a.H; f += kWave) ys[f] = a.y[static_cast<uint64_t>(r) * a.H + f];
+  }
   const RowMeta meta = a.row_meta[r];
   const uint32_t fb_slot = a.fb_map != nullptr ? a.fb_map[r] : kInvalidToken;
   const TileRecord* recs;
@@ -636,7 +681,13 @@ __global__ __launch_bounds__(kWave) void finalize_kernel(FinalizeArgs a) {
   float score = sh.score;
   if (sh.need_score) {
     const uint32_t H = a.H;
-    for (uint32_t q = lane; q < H; q += kWave) es[q] = a.emb[static_cast<uint64_t>(token) * H + q];
+    if ((H & 7u) == 0) {
+      copy16_to_lds<2>(reinterpret_cast<uint4*>(es),
+                       reinterpret_cast<const uint4*>(a.emb + static_cast<uint64_t>(token) * H),
+                       H / 8, lane, kWave);
+    } else {
+      for (uint32_t q = lane; q < H; q += kWave) es[q] = a.emb[static_cast<uint64_t>(token) * H + q];
+    }
     __syncthreads();
     score = a.order == 1 ? chain_lds<true>(ys, es, H) : chain_lds<false>(ys, es, H);
   }
