@@ -396,14 +396,6 @@ __global__ __launch_bounds__(kThreads) void head_kernel(FallbackArgs f) {
   const uint32_t col = lane % 16;
   const uint32_t kb = lane / 16;
   const AView A{nullptr, f.y_hi, f.y_lo, f.row_index, f.m, f.rows, H};
-  if (threadIdx.x < kMTile) {
-    const uint32_t row = a_source_row(A, m0 + threadIdx.x);
-    const bool ok = row < f.rows;
-    src_row[threadIdx.x] = ok ? row : 0xFFFFFFFFu;
-    src_norm[threadIdx.x] = ok ? f.row_norm[row] : 0.0f;
-    if (blockIdx.x == 0 && ok) f.fb_map[row] = m0 + threadIdx.x;
-  }
-  __syncthreads();
   const uint32_t row_halves = H + kAStagePad;
   uint16_t* stage = reinterpret_cast<uint16_t*>(dyn + sizeof(HeadEpi));
   const uint32_t units = H / (32 * KC);
@@ -418,9 +410,18 @@ __global__ __launch_bounds__(kThreads) void head_kernel(FallbackArgs f) {
   };
   const uint16_t* bptr[kHeadBlocks];
   tile_rows(t_begin, bptr);
-  // the first unit of the first tile is in flight during the A staging
+  // the first unit of the first tile is in flight during the row lookups
+  // and the A staging
   BUnit<KC> b0;
   if constexpr (kALds) unit_load<KC>(bptr, 0, b0);
+  if (threadIdx.x < kMTile) {
+    const uint32_t row = a_source_row(A, m0 + threadIdx.x);
+    const bool ok = row < f.rows;
+    src_row[threadIdx.x] = ok ? row : 0xFFFFFFFFu;
+    src_norm[threadIdx.x] = ok ? f.row_norm[row] : 0.0f;
+    if (blockIdx.x == 0 && ok) f.fb_map[row] = m0 + threadIdx.x;
+  }
+  __syncthreads();
   if constexpr (kALds) {
     // the M-tile's FP16 split, [row][hi|lo][H + pad], zero rows beyond it;
     // kStageBatch loads per thread are in flight before their stores (a
