@@ -264,7 +264,7 @@ def main() -> int:
         "stages_us": {k: round(v[0] * 1e3, 2) for k, v in st.items()},
         "stages_serial_ms": round(stages_ms, 5),
         "effective_gather_GBs": round(alg["gather_logical"] / (gather_ms * 1e-3) / 1e9, 1),
-        "fallback": {"kernel": "head_kernel (MFMA head, unrestricted rows)", "rows": alg["B_u"],
+        "fallback": {"kernel": "vocab_head_kernel (MFMA head, unrestricted rows)", "rows": alg["B_u"],
                      "avg_launch_us": round(fb_ms * 1e3, 2),
                      "hbm_GBs": round(alg["fallback_bytes"] / (fb_ms * 1e-3) / 1e9, 1),
                      "hbm_frac": round(alg["fallback_bytes"] / (fb_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),

@@ -381,7 +381,7 @@ __device__ __forceinline__ void unit_mma(const ABUnit<KC>& u, const uint32_t (&a
 // previous unit's MFMAs (the scheduler would otherwise sink them past the
 // MFMAs and every unit would wait a full round trip).
 template <bool kALds, int KC>
-__global__ __launch_bounds__(kThreads) void head_kernel(FallbackArgs f) {
+__global__ __launch_bounds__(kThreads) void vocab_head_kernel(FallbackArgs f) {
   extern __shared__ __align__(16) unsigned char dyn[];
   __shared__ uint32_t src_row[kMTile];
   __shared__ float src_norm[kMTile];
@@ -674,7 +674,7 @@ hipError_t launch_projection(const ProjArgs& args, hipStream_t stream) {
 
 template <bool kALds, int KC>
 static void launch_head(const FallbackArgs& f, dim3 grid, uint32_t lds, hipStream_t stream) {
-  hipLaunchKernelGGL((head_kernel<kALds, KC>), grid, dim3(kThreads), lds, stream, f);
+  hipLaunchKernelGGL((vocab_head_kernel<kALds, KC>), grid, dim3(kThreads), lds, stream, f);
 }
 
 hipError_t launch_fallback(const FallbackArgs& args, hipStream_t stream) {

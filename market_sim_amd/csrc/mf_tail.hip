@@ -8,7 +8,7 @@
 //                            (a chunk of one row's list) and writes a tile
 //                            record: the candidates whose [g - b, g + b]
 //                            interval reaches the tile's best lower bound
-//   (K4 head_kernel, mf_mfma.hip, writes the same records for
+//   (K4 vocab_head_kernel, mf_mfma.hip, writes the same records for
 //    unrestricted rows)
 //   K3 finalize_kernel       per row: merges tile records, rescores the
 //                            surviving candidates in the reference order,
