@@ -63,6 +63,8 @@ hipError_t launch_restricted_greedy(const void* logits, bool half,
                                     uint32_t rows, uint32_t vocab,
                                     uint32_t max_allowed, hipStream_t stream);
 
+hipError_t launch_token_norms(const uint16_t* emb, uint32_t V, uint32_t H, float* out,
+                              hipStream_t stream);
 hipError_t launch_fill_zero(void* address, uint64_t bytes, hipStream_t stream);
 
 // ---- decode tail (mf_tail.hip) ----------------------------------------------
@@ -182,6 +184,10 @@ struct FallbackArgs {
   uint32_t* fb_map;         // [rows] written: row -> m
   uint32_t groups;          // compute units: workgroups per M-tile
   uint32_t tiles_per_group; // set by the launcher
+  // scores mode (the full-vocabulary comparator; records unused): FP32
+  // scores [m, V] and, from M-tile 0, the token norm bounds [V]
+  float* scores;
+  float* tok_norm;
   float coef;               // b = ||e|| * (coef * ||y|| + coef2) + slack
   float coef2;
   float slack;
@@ -189,5 +195,7 @@ struct FallbackArgs {
 
 uint32_t fallback_tiles(uint32_t vocab);
 hipError_t launch_fallback(const FallbackArgs& args, hipStream_t stream);
+// The same kernel writing args.scores / args.tok_norm instead of records.
+hipError_t launch_vocab_scores(const FallbackArgs& args, hipStream_t stream);
 
 } // namespace mf

@@ -380,7 +380,7 @@ __device__ __forceinline__ void unit_mma(const ABUnit<KC>& u, const uint32_t (&a
 // load, and sched_barrier(0) keeps each unit's loads issued before the
 // previous unit's MFMAs (the scheduler would otherwise sink them past the
 // MFMAs and every unit would wait a full round trip).
-template <bool kALds, int KC>
+template <bool kALds, int KC, bool kScores>
 __global__ __launch_bounds__(kThreads) void vocab_head_kernel(FallbackArgs f) {
   extern __shared__ __align__(16) unsigned char dyn[];
   __shared__ uint32_t src_row[kMTile];
@@ -419,7 +419,7 @@ __global__ __launch_bounds__(kThreads) void vocab_head_kernel(FallbackArgs f) {
     const bool ok = row < f.rows;
     src_row[threadIdx.x] = ok ? row : 0xFFFFFFFFu;
     src_norm[threadIdx.x] = ok ? f.row_norm[row] : 0.0f;
-    if (blockIdx.x == 0 && ok) f.fb_map[row] = m0 + threadIdx.x;
+    if (blockIdx.x == 0 && ok && f.fb_map != nullptr) f.fb_map[row] = m0 + threadIdx.x;
   }
   __syncthreads();
   if constexpr (kALds) {
@@ -521,6 +521,34 @@ __global__ __launch_bounds__(kThreads) void vocab_head_kernel(FallbackArgs f) {
       }
     }
 
+    if constexpr (kScores) {
+      // the comparator: every score of the tile, and the token norms
+      const uint32_t tok0 = tile * kHeadTileTokens;
+#pragma unroll
+      for (uint32_t tb = 0; tb < kHeadBlocks; ++tb) {
+        const uint32_t token = tok0 + wave * (16 * kHeadBlocks) + tb * 16 + col;
+        const uint32_t e = col % 4u;
+        const float d = e == 0u ? h.gram[tb][0]
+                                : (e == 1u ? h.gram[tb][1] : (e == 2u ? h.gram[tb][2] : h.gram[tb][3]));
+        const float tsq = __shfl(d, static_cast<int>(col + 16u * (col / 4u)));
+        if (token >= f.V) continue;
+        if (blockIdx.y == 0 && kb == 0u && f.tok_norm != nullptr) {
+          f.tok_norm[token] = __fsqrt_rn(tsq) * (1.0f + 0x1p-7f);
+        }
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+#pragma unroll
+          for (int jj = 0; jj < 2; ++jj) {
+            const uint32_t i = rb * 8 + 2 * kb + jj;
+            if (m0 + i < f.m) {
+              f.scores[static_cast<uint64_t>(m0 + i) * f.V + token] =
+                  h.acc[rb][tb][2 * jj] + h.acc[rb][tb][2 * jj + 1];
+            }
+          }
+        }
+      }
+      continue;
+    }
     // The tile's window records, reduced in registers.  Lane l holds
     // D[4 (l / 16) + i][l % 16] of each block: rows 2j, 2j + 1 (hi, lo of
     // row 8 rb + j) for j = 2 kb and 2 kb + 1, so the scores of row
@@ -672,12 +700,13 @@ hipError_t launch_projection(const ProjArgs& args, hipStream_t stream) {
   return hipGetLastError();
 }
 
-template <bool kALds, int KC>
+template <bool kALds, int KC, bool kScores>
 static void launch_head(const FallbackArgs& f, dim3 grid, uint32_t lds, hipStream_t stream) {
-  hipLaunchKernelGGL((vocab_head_kernel<kALds, KC>), grid, dim3(kThreads), lds, stream, f);
+  hipLaunchKernelGGL((vocab_head_kernel<kALds, KC, kScores>), grid, dim3(kThreads), lds, stream, f);
 }
 
-hipError_t launch_fallback(const FallbackArgs& args, hipStream_t stream) {
+template <bool kScores>
+static hipError_t launch_vocab(const FallbackArgs& args, hipStream_t stream) {
   if (args.m == 0) return hipSuccess;
   if (args.H % 64 != 0) return hipErrorInvalidValue;
   // runs of tiles per workgroup: as many workgroups as compute units (or
@@ -693,16 +722,25 @@ hipError_t launch_fallback(const FallbackArgs& args, hipStream_t stream) {
   if (stage <= kAStageMaxBytes) {
     const uint32_t lds = static_cast<uint32_t>(sizeof(HeadEpi)) + stage;
     if (steps % 6 == 0) {
-      launch_head<true, 6>(f, grid, lds, stream);
+      launch_head<true, 6, kScores>(f, grid, lds, stream);
     } else if (steps % 4 == 0) {
-      launch_head<true, 4>(f, grid, lds, stream);
+      launch_head<true, 4, kScores>(f, grid, lds, stream);
     } else {
-      launch_head<true, 2>(f, grid, lds, stream);
+      launch_head<true, 2, kScores>(f, grid, lds, stream);
     }
   } else {
-    launch_head<false, 2>(f, grid, static_cast<uint32_t>(sizeof(HeadEpi)), stream);
+    launch_head<false, 2, kScores>(f, grid, static_cast<uint32_t>(sizeof(HeadEpi)), stream);
   }
   return hipGetLastError();
+}
+
+hipError_t launch_fallback(const FallbackArgs& args, hipStream_t stream) {
+  return launch_vocab<false>(args, stream);
+}
+
+hipError_t launch_vocab_scores(const FallbackArgs& args, hipStream_t stream) {
+  if (args.scores == nullptr) return hipErrorInvalidValue;
+  return launch_vocab<true>(args, stream);
 }
 
 } // namespace mf
