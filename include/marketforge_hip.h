@@ -10,7 +10,9 @@
  * or torch type appears here.
  *
  * Conventions kept from the reference:
- *   - ops borrow caller buffers: they never allocate and never synchronize;
+ *   - ops borrow caller buffers: they never allocate (the comparator
+ *     mf_decode_tail_full_f16 creates one rocBLAS handle per device) and
+ *     never synchronize;
  *   - work is asynchronous on the caller's stream;
  *   - validation happens before any launch, in the reference order: zero
  *     dimensions / bad epsilon / null stream -> MF_INVALID_ARGUMENT; limits ->
@@ -238,12 +240,15 @@ mf_status mf_decode_tail_unrestricted(const mf_decode_tail_args* args,
                                       uintptr_t stream);
 mf_status mf_decode_tail_finalize(const mf_decode_tail_args* args, uintptr_t stream);
 
-/* The full-output-projection comparator for the same contract: an MFMA
- * projection of every row over the whole vocabulary into FP32 scores, then
- * the restricted selection over those scores (the shape of the reference's
- * "full" path, src/tools/cuda_restricted_output_head_bench.cu:181-191).
- * Outputs are bit-identical to mf_decode_tail_f16.  Needs
- * mf_decode_tail_full_workspace_bytes of workspace. */
+/* The full-output-projection comparator for the same contract: a GEMM
+ * projection of every row over the whole vocabulary into FP32 scores (two
+ * rocBLAS FP16 GEMMs, the normalized row split into FP16 hi and lo parts,
+ * FP32 accumulation), then the restricted selection over those scores (the
+ * shape of the reference's "full" path,
+ * src/tools/cuda_restricted_output_head_bench.cu:181-191).  Outputs are
+ * bit-identical to mf_decode_tail_f16.  Needs
+ * mf_decode_tail_full_workspace_bytes of workspace.  The first call on a
+ * device creates that device's rocBLAS handle. */
 mf_status mf_decode_tail_full_workspace_bytes(const mf_decode_tail_args* args,
                                               uint64_t* bytes);
 mf_status mf_decode_tail_full_f16(const mf_decode_tail_args* args,
