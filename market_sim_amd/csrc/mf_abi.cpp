@@ -453,9 +453,9 @@ namespace {
 constexpr uint32_t kFullTile = 256;  // selection over projected scores
 
 struct TailLayout {
-  uint64_t y, row_norm, row_meta, y_hi, y_lo, fb_map, records, fb_records, scores, tok_norm,
-      total;
-  uint32_t tile, max_tiles, fb_tiles;
+  uint64_t y, row_norm, row_meta, y_hi, y_lo, fb_map, records, fb_records, fb_panel,
+      fb_slot_row, fb_slot_norm, scores, tok_norm, total;
+  uint32_t tile, max_tiles, fb_tiles, fb_rows;
 };
 
 bool buffer_is(const mf_buffer& b, uint64_t bytes) { return b.address != 0 && b.bytes == bytes; }
@@ -540,6 +540,7 @@ mf_status validate_tail(const mf_decode_tail_args* a, bool full, TailLayout& L) 
   }
   L.fb_tiles = mf::fallback_tiles(static_cast<uint32_t>(a->vocab));
   const uint64_t fb_rows = full ? 0 : a->unrestricted_count;
+  L.fb_rows = static_cast<uint32_t>(fb_rows);
   uint64_t off = 0;
   auto take = [&off](uint64_t bytes) {
     const uint64_t at = off;
@@ -549,12 +550,16 @@ mf_status validate_tail(const mf_decode_tail_args* a, bool full, TailLayout& L) 
   L.y = take(xe * 4u);
   L.row_norm = take(rows * 4u);
   L.row_meta = take(rows * sizeof(mf::RowMeta));
-  const bool split = fb_rows > 0 || full || mfma_gather(a->hidden);
+  const bool split = full || mfma_gather(a->hidden);
   L.y_hi = take(split ? xe * 2u : 0u);
   L.y_lo = take(split ? xe * 2u : 0u);
   L.fb_map = take(rows * 4u);
   L.records = take(rows * L.max_tiles * sizeof(mf::TileRecord));
   L.fb_records = take(fb_rows * L.fb_tiles * sizeof(mf::TileRecord));
+  L.fb_panel = take(mf::panel_tiles(static_cast<uint32_t>(fb_rows)) *
+                    mf::panel_tile_bytes(a->hidden));
+  L.fb_slot_row = take(fb_rows * 4u);
+  L.fb_slot_norm = take(fb_rows * 4u);
   L.scores = take(full ? rows * a->vocab * 4u : 0u);
   L.tok_norm = take(full ? a->vocab * 4u : 0u);
   L.total = off;
@@ -574,6 +579,7 @@ enum class Stage { kPrepare, kRestricted, kUnrestricted, kFinalize };
 mf::TailNormArgs norm_args(const mf_decode_tail_args* a, const TailLayout& L, char* ws,
                            bool split) {
   mf::TailNormArgs n{};
+  n.rows = static_cast<uint32_t>(a->rows);
   n.x = ptr<const float>(a->x.address);
   n.weight = ptr<const float>(a->norm_weight.address);
   n.epsilon = a->epsilon;
@@ -593,6 +599,13 @@ mf::TailNormArgs norm_args(const mf_decode_tail_args* a, const TailLayout& L, ch
   n.out_token = ptr<uint32_t>(a->out_token.address);
   n.out_score = ptr<float>(a->out_score.address);
   n.out_next = ptr<uint32_t>(a->out_next_state.address);
+  if (L.fb_rows > 0) {  // the MFMA head's panel
+    n.fb_rows = ptr<const uint32_t>(a->unrestricted_rows.address);
+    n.fb_m = static_cast<uint32_t>(a->unrestricted_count);
+    n.fb_panel = reinterpret_cast<uint16_t*>(ws + L.fb_panel);
+    n.fb_slot_row = reinterpret_cast<uint32_t*>(ws + L.fb_slot_row);
+    n.fb_slot_norm = reinterpret_cast<float*>(ws + L.fb_slot_norm);
+  }
   return n;
 }
 
@@ -655,9 +668,7 @@ mf_status decode_tail_stage(const mf_decode_tail_args* args, uintptr_t stream, S
   hipError_t e = hipSuccess;
   switch (stage) {
     case Stage::kPrepare:
-      e = mf::launch_tail_norm(norm_args(a, L, ws, a->unrestricted_count > 0 ||
-                                                       mfma_gather(a->hidden)),
-                               static_cast<uint32_t>(a->rows), s);
+      e = mf::launch_tail_norm(norm_args(a, L, ws, mfma_gather(a->hidden)), s);
       break;
     case Stage::kRestricted: {
       mf::GatherArgs g = gather_args(a, L, ws);
@@ -676,12 +687,10 @@ mf_status decode_tail_stage(const mf_decode_tail_args* args, uintptr_t stream, S
     case Stage::kUnrestricted: {
       if (a->unrestricted_count == 0) break;
       mf::FallbackArgs f{};
-      f.y_hi = reinterpret_cast<const uint16_t*>(ws + L.y_hi);
-      f.y_lo = reinterpret_cast<const uint16_t*>(ws + L.y_lo);
-      f.row_index = ptr<const uint32_t>(a->unrestricted_rows.address);
+      f.panel = reinterpret_cast<const uint16_t*>(ws + L.fb_panel);
+      f.slot_row = reinterpret_cast<const uint32_t*>(ws + L.fb_slot_row);
+      f.slot_norm = reinterpret_cast<const float*>(ws + L.fb_slot_norm);
       f.m = static_cast<uint32_t>(a->unrestricted_count);
-      f.rows = static_cast<uint32_t>(a->rows);
-      f.row_norm = reinterpret_cast<const float*>(ws + L.row_norm);
       f.emb = ptr<const uint16_t>(a->embedding.address);
       f.H = static_cast<uint32_t>(a->hidden);
       f.V = static_cast<uint32_t>(a->vocab);
@@ -766,8 +775,7 @@ mf_status mf_decode_tail_full_f16(const mf_decode_tail_args* args, uintptr_t str
   float* tok_norm = reinterpret_cast<float*>(ws + L.tok_norm);
 
   // 1. final RMSNorm (and its FP16 split for the MFMA projection)
-  hipError_t e = mf::launch_tail_norm(norm_args(a, L, ws, true),
-                                      static_cast<uint32_t>(a->rows), s);
+  hipError_t e = mf::launch_tail_norm(norm_args(a, L, ws, true), s);
   if (e != hipSuccess) return launch_status(e);
   // 2. full output projection of every row: FP32 scores [rows, V] as two
   // FP16 GEMMs of the hidden split (hi, then lo accumulated) on rocBLAS --

@@ -167,45 +167,101 @@ __device__ __forceinline__ Best best_leaf(float score, uint32_t token,
   return score != score ? best_identity() : Best{score, token, pos};
 }
 
-__device__ __forceinline__ Best wave_best(Best b) {
-#pragma unroll
-  for (int m = kWave / 2; m > 0; m >>= 1) {
-    Best o;
-    o.score = __shfl_xor(b.score, m);
-    o.token = __shfl_xor(b.token, m);
-    o.pos = __shfl_xor(b.pos, m);
-    b = best_of(b, o);
-  }
-  return b;
+// Cross-lane reductions without the LDS pipe (__shfl_xor compiles to
+// ds_bpermute, an LDS round trip per step).  Within a DPP row (lanes 16 r ..
+// 16 r + 15) rotations by 8, 4, 2 and 1 (row_ror) leave every lane of the
+// row with the row's result; the four row results are then read with
+// v_readlane.  The whole wave must be active, as for the shuffles.
+template <int kN>
+__device__ __forceinline__ uint32_t row_ror(uint32_t v, uint32_t identity) {
+  static_assert(kN > 0 && kN < 16, "row_ror:1..15");
+  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(
+      static_cast<int>(identity), static_cast<int>(v), 0x120 + kN, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float as_float(uint32_t v) { return __builtin_bit_cast(float, v); }
+__device__ __forceinline__ uint32_t as_u32(float v) { return __builtin_bit_cast(uint32_t, v); }
+__device__ __forceinline__ uint32_t lane_value(uint32_t v, int lane) {
+  return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), lane));
+}
+
+__device__ __forceinline__ float row16_max(float v) {
+  v = __builtin_fmaxf(v, as_float(row_ror<8>(as_u32(v), as_u32(v))));
+  v = __builtin_fmaxf(v, as_float(row_ror<4>(as_u32(v), as_u32(v))));
+  v = __builtin_fmaxf(v, as_float(row_ror<2>(as_u32(v), as_u32(v))));
+  v = __builtin_fmaxf(v, as_float(row_ror<1>(as_u32(v), as_u32(v))));
+  return v;
+}
+__device__ __forceinline__ uint32_t row16_and(uint32_t v) {
+  v &= row_ror<8>(v, v);
+  v &= row_ror<4>(v, v);
+  v &= row_ror<2>(v, v);
+  v &= row_ror<1>(v, v);
+  return v;
+}
+__device__ __forceinline__ uint32_t row16_min(uint32_t v) {
+  v = __builtin_elementwise_min(v, row_ror<8>(v, v));
+  v = __builtin_elementwise_min(v, row_ror<4>(v, v));
+  v = __builtin_elementwise_min(v, row_ror<2>(v, v));
+  v = __builtin_elementwise_min(v, row_ror<1>(v, v));
+  return v;
+}
+__device__ __forceinline__ uint32_t row16_sum(uint32_t v) {
+  v += row_ror<8>(v, 0u);
+  v += row_ror<4>(v, 0u);
+  v += row_ror<2>(v, 0u);
+  v += row_ror<1>(v, 0u);
+  return v;
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int m = kWave / 2; m > 0; m >>= 1) {
-    v = __builtin_fmaxf(v, __shfl_xor(v, m));
-  }
-  return v;
+  const uint32_t r = as_u32(row16_max(v));
+  return __builtin_fmaxf(__builtin_fmaxf(as_float(lane_value(r, 0)), as_float(lane_value(r, 16))),
+                         __builtin_fmaxf(as_float(lane_value(r, 32)), as_float(lane_value(r, 48))));
+}
+
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+  const uint32_t r = row16_min(v);
+  return __builtin_elementwise_min(
+      __builtin_elementwise_min(lane_value(r, 0), lane_value(r, 16)),
+      __builtin_elementwise_min(lane_value(r, 32), lane_value(r, 48)));
 }
 
 __device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
-#pragma unroll
-  for (int m = kWave / 2; m > 0; m >>= 1) {
-    v += __shfl_xor(v, m);
-  }
-  return v;
+  const uint32_t r = row16_sum(v);
+  return lane_value(r, 0) + lane_value(r, 16) + lane_value(r, 32) + lane_value(r, 48);
 }
 
-// (token, pos) with the lowest token; used for the all-NaN fallback rule.
+// The lowest token and, among its lanes, the lowest position (the first
+// occurrence in list order: the all-NaN fallback rule).
 __device__ __forceinline__ void wave_min_token(uint32_t& token, uint32_t& pos) {
-#pragma unroll
-  for (int m = kWave / 2; m > 0; m >>= 1) {
-    const uint32_t t = __shfl_xor(token, m);
-    const uint32_t p = __shfl_xor(pos, m);
-    if (t < token) {
-      token = t;
-      pos = p;
-    }
+  const uint32_t t = wave_min_u32(token);
+  pos = wave_min_u32(token == t ? pos : 0xFFFFFFFFu);
+  token = t;
+}
+
+__device__ __forceinline__ Best wave_best(Best b) {
+  // within rows: each step takes the three fields from the same lane
+#define MF_BEST_STEP(n)                                                   \
+  {                                                                       \
+    Best o;                                                               \
+    o.score = as_float(row_ror<n>(as_u32(b.score), as_u32(b.score)));     \
+    o.token = row_ror<n>(b.token, b.token);                               \
+    o.pos = row_ror<n>(b.pos, b.pos);                                     \
+    b = best_of(b, o);                                                    \
   }
+  MF_BEST_STEP(8)
+  MF_BEST_STEP(4)
+  MF_BEST_STEP(2)
+  MF_BEST_STEP(1)
+#undef MF_BEST_STEP
+  Best r{as_float(lane_value(as_u32(b.score), 0)), lane_value(b.token, 0), lane_value(b.pos, 0)};
+#pragma unroll
+  for (int row = 1; row < 4; ++row) {
+    const Best o{as_float(lane_value(as_u32(b.score), 16 * row)), lane_value(b.token, 16 * row),
+                 lane_value(b.pos, 16 * row)};
+    r = best_of(r, o);
+  }
+  return r;
 }
 
 // Summary of one block of candidates, produced by one workgroup pass and
@@ -280,6 +336,22 @@ __device__ __forceinline__ void copy16_to_lds(uint4* dst, const uint4* src, uint
       if (q < n) dst[q] = v[u];
     }
   }
+}
+
+// One 1 KiB burst from global memory straight into LDS (global_load_lds,
+// 16 bytes per lane): lane l reads src_lane (its own 16 bytes) and the data
+// lands at dst_wave + 16 l, without passing through registers.  The wave
+// must wait for its vector memory count before the data is read, and a
+// barrier must follow before other waves read it.
+__device__ __forceinline__ void burst_to_lds(const void* src_lane, void* dst_wave) {
+  __builtin_amdgcn_global_load_lds(
+      (__attribute__((address_space(1))) void*)(const_cast<void*>(src_lane)),
+      (__attribute__((address_space(3))) void*)(dst_wave), 16, 0, 0);
+}
+// Every vector memory operation of this wave has completed (loads landed,
+// LDS bursts written).
+__device__ __forceinline__ void wait_vector_memory() {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 // Per-row metadata written by the decode-tail norm kernel.

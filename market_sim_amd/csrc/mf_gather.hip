@@ -126,11 +126,17 @@ __device__ void mfma_tile(const GatherArgs& a, uint32_t r, uint32_t k, uint32_t 
   const uint32_t kb = lane / kBlock;   // k-block: features 8 kb .. 8 kb + 7 of a step
   const uint32_t col = lane % kBlock;  // B column (token) and A row of this lane
   const uint32_t unit_f = kStep * KC;
-  // unit q = (block q / chunks, chunk q % chunks); the B column's token
+  // the B column's token of each block (lane col of block j holds candidate
+  // 16 j + col), gathered once per tile
+  uint32_t btok[4];
+#pragma unroll
+  for (uint32_t j = 0; j < 4; ++j) {
+    btok[j] = static_cast<uint32_t>(__shfl(static_cast<int>(t), static_cast<int>(j * kBlock + col)));
+  }
+  // unit q = (block q / chunks, chunk q % chunks); j is wave-uniform
   auto load_q = [&](uint32_t q, Operands<KC>& o) {
     const uint32_t j = q / chunks;
-    const uint32_t bt = static_cast<uint32_t>(__shfl(static_cast<int>(t),
-                                                     static_cast<int>(j * kBlock + col)));
+    const uint32_t bt = j == 0u ? btok[0] : (j == 1u ? btok[1] : (j == 2u ? btok[2] : btok[3]));
     load_unit<KC>(a.emb + static_cast<uint64_t>(bt) * H + kb * 8u, (q % chunks) * unit_f, o);
   };
   Operands<KC> o0, o1;

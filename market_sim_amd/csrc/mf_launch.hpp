@@ -74,6 +74,7 @@ constexpr uint32_t kPlanRowsMax = 1024;  // rows the gather plans in LDS
 constexpr uint32_t kGatherWaveTile = 64;  // candidates per wave tile (MFMA gather)
 
 struct TailNormArgs {
+  uint32_t rows;
   const float* x;          // [rows, H]
   const float* weight;     // [H] or null (x already normalized)
   float epsilon;
@@ -93,7 +94,29 @@ struct TailNormArgs {
   uint32_t* out_token;
   float* out_score;
   uint32_t* out_next;
+  // The MFMA head's panel (fb_panel null: none).  Workgroup rows + j
+  // normalizes row fb_rows[j] again (the same arithmetic, so the same bits)
+  // and writes slot j: its FP16 split into the panel, its norm bound and its
+  // row (kInvalidToken when fb_rows[j] >= rows).
+  const uint32_t* fb_rows; // [fb_m]
+  uint32_t fb_m;
+  uint16_t* fb_panel;      // [panel_tiles(fb_m)] x panel_tile_bytes(H)
+  uint32_t* fb_slot_row;   // [fb_m]
+  float* fb_slot_norm;     // [fb_m]
 };
+
+// Panel of the MFMA head: per tile of kPanelRows slots, the slots' FP16
+// split [slot][hi | lo][H + kPanelPad] halves -- the head's LDS image of its
+// A operand, so the head copies it with plain 1 KiB global-to-LDS bursts.
+// The pad spreads the 16 A rows of one LDS read over the banks.
+constexpr uint32_t kPanelRows = 32;
+constexpr uint32_t kPanelPad = 8;
+__host__ __device__ constexpr uint64_t panel_tile_bytes(uint64_t H) {
+  return kPanelRows * 2u * (H + kPanelPad) * 2u;
+}
+__host__ __device__ constexpr uint32_t panel_tiles(uint32_t m) {
+  return (m + kPanelRows - 1) / kPanelRows;
+}
 
 struct GatherArgs {
   const float* y;          // [rows, H]
@@ -140,7 +163,7 @@ struct FinalizeArgs {
   int order;
 };
 
-hipError_t launch_tail_norm(const TailNormArgs& args, uint32_t rows, hipStream_t stream);
+hipError_t launch_tail_norm(const TailNormArgs& args, hipStream_t stream);
 hipError_t launch_gather(ScoreSource source, const GatherArgs& args, hipStream_t stream);
 hipError_t launch_gather_mfma(const GatherArgs& args, hipStream_t stream);  // mf_gather.hip
 hipError_t launch_finalize(const FinalizeArgs& args, hipStream_t stream);
@@ -171,23 +194,17 @@ hipError_t launch_projection(const ProjArgs& args, hipStream_t stream);
 // argmax epilogue, per-tile records and a last-arriver merge per row that
 // rescores the window in the reference order.
 struct FallbackArgs {
-  const uint16_t* y_hi;     // [rows, H] FP16 split of the normalized hidden
-  const uint16_t* y_lo;
-  const uint32_t* row_index;// [m] unrestricted rows (entries >= rows are skipped)
+  const uint16_t* panel;    // the norm kernel's panel of the m unrestricted rows
+  const uint32_t* slot_row; // [m] source row of each slot (kInvalidToken: none)
+  const float* slot_norm;   // [m] norm bound of each slot's row
   uint32_t m;
-  uint32_t rows;
-  const float* row_norm;    // [rows]
   const uint16_t* emb;
   uint32_t H;
   uint32_t V;
   TileRecord* records;      // [m, tiles] (fallback_tiles(V) tiles of 192 tokens)
-  uint32_t* fb_map;         // [rows] written: row -> m
+  uint32_t* fb_map;         // [rows] written: row -> slot
   uint32_t groups;          // compute units: workgroups per M-tile
   uint32_t tiles_per_group; // set by the launcher
-  // scores mode (the full-vocabulary comparator; records unused): FP32
-  // scores [m, V] and, from M-tile 0, the token norm bounds [V]
-  float* scores;
-  float* tok_norm;
   float coef;               // b = ||e|| * (coef * ||y|| + coef2) + slack
   float coef2;
   float slack;
@@ -195,7 +212,5 @@ struct FallbackArgs {
 
 uint32_t fallback_tiles(uint32_t vocab);
 hipError_t launch_fallback(const FallbackArgs& args, hipStream_t stream);
-// The same kernel writing args.scores / args.tok_norm instead of records.
-hipError_t launch_vocab_scores(const FallbackArgs& args, hipStream_t stream);
 
 } // namespace mf

@@ -1,22 +1,19 @@
-// gfx950 MFMA kernels: the dense full-vocabulary projection Y * E^T.
+// gfx950 MFMA kernels: dense products against the whole FP16 table.
 //
-// Used for (1) the fallback head of unrestricted rows (windowed-argmax
-// epilogue writing tile records; no logits written), (2) the
-// full-output-projection comparator (FP32 scores), and (3) linear_f16 (FP16
-// logits, the reference's cublasGemmEx call).
-//
-// Tiling: a 256-thread workgroup owns 32 A rows (hidden vectors) x 128
-// tokens; each wave computes one 32x32 block with v_mfma_f32_32x32x16_f16.
-// K runs in chunks of 64 features.  Per chunk the workgroup stages the
-// 128 x 64 FP16 slice of E and the 32 x 64 A slice in LDS (double-buffered,
-// rows padded to 144 bytes so b128 reads are bank-conflict free): eight
-// consecutive lanes load one token's 128 contiguous bytes, so every HBM line
-// is fetched once, and four chunks' global loads are in flight (in
-// registers) while the staged chunk's MFMAs run.
+// (1) The head of the unrestricted rows (vocab_head_*_kernel): every token's
+//     score against the rows' FP16 hi/lo split, reduced in a windowed-argmax
+//     epilogue to tile records (no logits written).
+// (2) linear_f16 (projection_kernel): FP16 logits, the reference's
+//     cublasGemmEx call.  Tiling: a 256-thread workgroup owns 32 A rows x 128
+//     tokens; each wave computes one 32x32 block with
+//     v_mfma_f32_32x32x16_f16.  K runs in chunks of 64 features; per chunk
+//     the workgroup stages the 128 x 64 FP16 slice of E and the 32 x 64 A
+//     slice in LDS (double-buffered, rows padded to 144 bytes so b128 reads
+//     are bank-conflict free), with four chunks' global loads in flight.
 //
 // FP32 hidden values enter as the FP16 pair hi = rne(y), lo = rne(y - hi)
-// (two MFMAs per step into two accumulators, added at the end), so the fast
-// score is accurate to ~2^-22 relative before the reference-order rescore.
+// (two MFMAs per step), so the fast score is accurate to ~2^-22 relative
+// before the reference-order rescore.
 #include <hip/hip_runtime.h>
 
 #include "mf_device.hpp"
@@ -248,68 +245,334 @@ __device__ __forceinline__ uint32_t group8_and(uint32_t v) {
 
 // ---- MFMA head of the unrestricted rows -----------------------------------
 //
-// A workgroup owns the 32 rows of an M-tile and a contiguous run of 192-token
-// tiles (one window record per row and tile); the runs are sized so that
-// every compute unit gets the same number of tiles.  Each wave owns 48
-// tokens of a tile, three 16-token blocks of v_mfma_f32_16x16x32_f16, and
-// all 32 rows as four 16-row blocks: A rows 2j and 2j + 1 of block rb are
-// the hi and lo halves of row 8 rb + j.  In the 16x16x32 layout lane l holds
-// 8 consecutive features of column / A row l % 16 at k-block l / 16, so the
-// four lanes of a token read 64 contiguous bytes per step.  The table rows
-// go straight from memory into the MFMA registers, two units of KC steps in
-// flight; A comes from an LDS stage of the M-tile's FP16 split (while it
-// fits two 32-row stages... one per workgroup) or, for wide rows, from L2.
-// A second MFMA of each token block with itself gives the squared token
-// norms (Gram diagonal) for the error bound.
+// A workgroup owns the 32 slots of one panel tile (an M-tile) and a run of
+// 192-token tiles (one window record per row and tile); the runs are sized
+// so that every compute unit gets the same number of tiles.  The tile's 12
+// blocks of 16 tokens are split over the waves, kBlocks per wave; each block
+// is one v_mfma_f32_16x16x32_f16 column block against the 32 slots as four
+// 16-row A blocks: A rows 2j and 2j + 1 of block rb are the hi and lo halves
+// of slot 8 rb + j.  In the 16x16x32 layout lane l holds 8 consecutive
+// features of column / A row l % 16 at k-block l / 16, so the four lanes of
+// a token read 64 contiguous bytes per step, and table rows go straight from
+// memory into the MFMA registers.  A second MFMA of each token block with
+// itself gives the squared token norms (Gram diagonal) for the error bound.
+//
+// Two variants:
+//   narrow rows (panel tile in LDS, H <= 576): at entry the workgroup copies
+//     its panel tile into LDS with 1 KiB global-to-LDS bursts and every wave
+//     issues the loads of its whole K range; one wait, one barrier, then the
+//     MFMAs.  Each tile costs one memory round trip.
+//   wide rows: A and B from memory (A from L2) in units of KC steps, two
+//     units in flight.
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
-constexpr uint32_t kHeadBlocks = 3;                                   // per wave
-constexpr uint32_t kHeadTileTokens = (kThreads / 64) * 16 * kHeadBlocks;  // 192
-constexpr uint32_t kAStagePad = 8;  // halves; spreads the 16 row-parts of a read over banks
-__host__ __device__ constexpr uint32_t a_stage_bytes(uint32_t H) {
-  return kMTile * 2u * (H + kAStagePad) * 2u;
-}
-constexpr uint32_t kAStageMaxBytes = 76u * 1024u;
+constexpr uint32_t kHeadTileTokens = 192;
+constexpr uint32_t kHeadTileBlocks = kHeadTileTokens / 16;
+constexpr uint32_t kPanelLdsMaxBytes = 76u * 1024u;
+// narrow-row variant: waves per workgroup (tile blocks per wave = 12 / waves)
+constexpr int kHeadLdsWaves = 4;
+// wide-row variant: 4 waves x 3 blocks
+constexpr int kWideWaves = 4;
+constexpr int kWideBlocks = 3;
 
-// Per-wave partial results of the tile's window records.
+// The tile's scores [slot][token] and token norm bounds, staged in LDS for
+// the epilogue (rows padded so the four slot rows one write instruction
+// touches fall on different banks).
+constexpr uint32_t kEpiStride = kHeadTileTokens + 8;
+constexpr int kEpiWaves = 4;  // both variants run four waves
 struct HeadEpi {
-  float lo[kThreads / 64][kMTile];
-  uint32_t fin[kThreads / 64][kMTile];
-  uint32_t cnt[kThreads / 64][kMTile];
+  float g[kMTile][kEpiStride];
+  float tn[kEpiWaves];             // per-wave token-norm maxima
+  uint32_t count[kEpiWaves][64];   // per-lane member counts
 };
 
-// Units of KC steps: table rows only (A from LDS) or table rows and A (A
-// from L2).  All loads are straight-line: a load under a branch makes the
-// compiler wait for every load in flight before the next MFMA.
-template <int KC>
-struct BUnit {
-  half8_t b[kHeadBlocks][KC];
+template <int kBlocks>
+struct HeadAcc {
+  floatx4 acc[4][kBlocks];
+  floatx4 gram[kBlocks];
 };
+
+// Slot metadata of the workgroup's panel tile: source row (kInvalidToken
+// for slots past m or without a row) and norm bound; block column 0 also
+// records row -> slot for the finalize kernel.  Straight-line loads.
+__device__ __forceinline__ void head_slots(const FallbackArgs& f, uint32_t m0,
+                                           uint32_t* src_row, float* src_norm) {
+  if (threadIdx.x < kMTile) {
+    const uint32_t i = m0 + threadIdx.x;
+    const uint32_t at = i < f.m ? i : f.m - 1u;
+    const uint32_t row = f.slot_row[at];
+    const float norm = f.slot_norm[at];
+    const uint32_t r = i < f.m ? row : kInvalidToken;
+    src_row[threadIdx.x] = r;
+    src_norm[threadIdx.x] = r != kInvalidToken ? norm : 0.0f;
+    if (blockIdx.x == 0 && r != kInvalidToken && f.fb_map != nullptr) f.fb_map[r] = i;
+  }
+}
+
+// 8-lane max (lanes 8 s .. 8 s + 7): quad_perm xor 1 and xor 2, then the
+// mirror inside the half row.  v_max_f32 with the DPP operand directly (the
+// compiler's form adds a canonicalizing max per step); s_nop 1 is the
+// VALU-write to DPP-read wait.
+__device__ __forceinline__ float lane8_max(float v) {
+  asm("s_nop 1\n\tv_max_f32_dpp %0, %0, %0 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf"
+      : "+v"(v));
+  asm("s_nop 1\n\tv_max_f32_dpp %0, %0, %0 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf"
+      : "+v"(v));
+  asm("s_nop 1\n\tv_max_f32_dpp %0, %0, %0 row_half_mirror row_mask:0xf bank_mask:0xf"
+      : "+v"(v));
+  return v;
+}
+
+// The tile's window records.  Lane l holds D[4 (l / 16) + i][l % 16] of
+// each block: A rows 2j, 2j + 1 (hi, lo of slot 8 rb + j) for j = 2 kb and
+// 2 kb + 1, so the score of slot 8 rb + 2 kb + jj (jj = 0, 1) and token
+// (wave kBlocks + tb) 16 + col of the tile is acc[rb][tb][2 jj] +
+// acc[rb][tb][2 jj + 1]; the Gram diagonal of column c sits in lane
+// c + 16 (c / 4), element c % 4.
+//
+// One bound per slot and tile: b = tn_max (coef ||y|| + coef2) + slack with
+// tn_max the largest token-norm bound of the tile, which is at least every
+// token's own bound.  Then the best lower bound is L = fl(max g - b) (the
+// rounding is monotone) and a token is a member when fl(g + b) >= L.  The
+// scores go through LDS; then lanes 8 s .. 8 s + 7 of wave w take slot
+// 8 w + s, 24 consecutive tokens each, so the eight slots of a wave share
+// every instruction; members come out in ascending token order.  Ends with
+// a barrier (LDS is reused by the next tile).
+template <int kWaves, int kBlocks>
+__device__ __forceinline__ void head_records(const FallbackArgs& f, const HeadAcc<kBlocks>& h,
+                                             HeadEpi& epi, const uint32_t* src_row,
+                                             const float* src_norm, uint32_t m0, uint32_t tile,
+                                             uint32_t tiles) {
+  static_assert(kWaves == kEpiWaves && kMTile == 8 * kWaves, "eight slots per wave");
+  const uint32_t lane = threadIdx.x % 64;
+  const uint32_t wave = threadIdx.x / 64;
+  const uint32_t col = lane % 16;
+  const uint32_t kb = lane / 16;
+  const uint32_t wtok = wave * (16u * kBlocks);
+  const uint32_t tok0 = tile * kHeadTileTokens;
+  const uint32_t nt = f.V - tok0 < kHeadTileTokens ? f.V - tok0 : kHeadTileTokens;
+  float tn_local = 0.0f;
+#pragma unroll
+  for (int tb = 0; tb < kBlocks; ++tb) {
+    const uint32_t t = wtok + tb * 16u + col;
+    const uint32_t e = col % 4u;
+    const float d = e == 0u ? h.gram[tb][0]
+                            : (e == 1u ? h.gram[tb][1] : (e == 2u ? h.gram[tb][2] : h.gram[tb][3]));
+    // lanes of the Gram diagonal, tokens of the vocabulary
+    if (col / 4u == kb && t < nt) tn_local = __builtin_fmaxf(tn_local, __fsqrt_rn(d) * (1.0f + 0x1p-7f));
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        epi.g[rb * 8 + 2 * kb + jj][t] = h.acc[rb][tb][2 * jj] + h.acc[rb][tb][2 * jj + 1];
+      }
+    }
+  }
+  // a NaN norm (a non-finite table row) propagates: the bound then fails the
+  // finiteness test and the tile is rescored in full
+  const bool any_nan = __ballot(tn_local != tn_local) != 0ull;
+  const float tn_wave = wave_max(tn_local);
+  if (lane == 0) epi.tn[wave] = any_nan ? __builtin_nanf("") : tn_wave;
+  __syncthreads();
+  float tn_max = epi.tn[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) {
+    const float v = epi.tn[w];
+    tn_max = (tn_max != tn_max || v != v) ? __builtin_nanf("") : __builtin_fmaxf(tn_max, v);
+  }
+
+  constexpr int kSeg = kHeadTileTokens / 8;  // tokens per lane
+  const uint32_t sl = lane / 8;              // slot of the wave
+  const uint32_t j8 = lane % 8;
+  const uint32_t i = wave * 8u + sl;
+  const uint32_t t0 = j8 * kSeg;
+  float gv[kSeg];
+  const float4* src = reinterpret_cast<const float4*>(&epi.g[i][t0]);
+#pragma unroll
+  for (int q = 0; q < kSeg / 4; ++q) {
+    const float4 v = src[q];
+    gv[4 * q] = v.x;
+    gv[4 * q + 1] = v.y;
+    gv[4 * q + 2] = v.z;
+    gv[4 * q + 3] = v.w;
+  }
+  // tokens past the vocabulary (last tile only) read as -inf / 0
+  if (nt < kHeadTileTokens) {
+#pragma unroll
+    for (int k = 0; k < kSeg; ++k) {
+      if (t0 + k >= nt) gv[k] = -__builtin_huge_valf();
+    }
+  }
+  float gm = gv[0];
+  float sum = 0.0f;
+#pragma unroll
+  for (int k = 0; k < kSeg; ++k) {
+    gm = __builtin_fmaxf(gm, gv[k]);
+    sum += (t0 + k < nt) ? gv[k] : 0.0f;
+  }
+  // every score of the lane finite (a sum that overflows counts as not
+  // finite: the tile is then rescored in full, which is exact too)
+  const uint64_t fin_lanes = __ballot(__builtin_isfinite(sum));
+  const bool slot_finite = ((fin_lanes >> (8u * sl)) & 0xFFull) == 0xFFull;
+  const float G = lane8_max(gm);
+  const float bs = __builtin_fmaf(tn_max, __builtin_fmaf(f.coef, src_norm[i], f.coef2), f.slack);
+  const float L = G - bs;
+  uint32_t members = 0u;  // bit k: token t0 + k
+#pragma unroll
+  for (int k = 0; k < kSeg; ++k) members |= (gv[k] + bs >= L) ? (1u << k) : 0u;
+  const uint32_t n = static_cast<uint32_t>(__popc(members));
+  epi.count[wave][lane] = n;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const uint4 c0 = *reinterpret_cast<const uint4*>(&epi.count[wave][8u * sl]);
+  const uint4 c1 = *reinterpret_cast<const uint4*>(&epi.count[wave][8u * sl + 4u]);
+  const uint32_t cs[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+  uint32_t before = 0u;
+  uint32_t total = 0u;
+#pragma unroll
+  for (uint32_t q = 0; q < 8; ++q) {
+    before += q < j8 ? cs[q] : 0u;
+    total += cs[q];
+  }
+  if (src_row[i] != kInvalidToken) {
+    const bool ordinary = slot_finite && bs < 0x1p100f && total <= static_cast<uint32_t>(kTileMembers);
+    TileRecord* rec = f.records + static_cast<uint64_t>(m0 + i) * tiles + tile;
+    if (ordinary) {
+      // the lane's members in ascending order, their scores read back
+      uint32_t r = before;
+      while (members != 0u) {
+        const uint32_t k = static_cast<uint32_t>(__builtin_ctz(members));
+        members &= members - 1u;
+        const float gk = epi.g[i][t0 + k];
+        const uint32_t token = tok0 + t0 + k;
+        rec->m[r] = TileMember{token, token, gk - bs, gk + bs};
+        ++r;
+      }
+    }
+    if (j8 == 0u) {
+      rec->best_lower = L;
+      rec->flags = ordinary ? 0u : kTileRescoreAll;
+      rec->min_token = tok0;
+      rec->min_pos = tok0;
+      rec->begin = tok0;
+      rec->count = nt;
+      rec->n_members = ordinary ? total : 0u;
+    }
+  }
+  __syncthreads();
+}
+
+// Narrow rows: H = 32 kSteps, the panel tile in LDS, the whole K range of
+// the wave's kBlocks token blocks in registers.
+template <int kWaves, int kBlocks, int kSteps>
+__global__ __launch_bounds__(kWaves * 64) void vocab_head_lds_kernel(FallbackArgs f) {
+  static_assert(kWaves * kBlocks == static_cast<int>(kHeadTileBlocks), "tile of 12 blocks");
+  constexpr uint32_t H = 32u * kSteps;
+  constexpr uint32_t kRowHalves = H + kPanelPad;
+  constexpr uint32_t kTileHalves = static_cast<uint32_t>(panel_tile_bytes(H) / 2u);
+  constexpr uint32_t kBursts = static_cast<uint32_t>(panel_tile_bytes(H) / 1024u);
+  static_assert(panel_tile_bytes(H) % 1024u == 0, "whole bursts");
+  extern __shared__ __align__(16) unsigned char dyn[];
+  __shared__ uint32_t src_row[kMTile];
+  __shared__ float src_norm[kMTile];
+  HeadEpi& epi = *reinterpret_cast<HeadEpi*>(dyn);
+  uint16_t* stage = reinterpret_cast<uint16_t*>(dyn + sizeof(HeadEpi));
+  const uint32_t m0 = blockIdx.y * kMTile;
+  const uint32_t tiles = (f.V + kHeadTileTokens - 1) / kHeadTileTokens;
+  const uint32_t t_begin = blockIdx.x * f.tiles_per_group;
+  const uint32_t t_end = t_begin + f.tiles_per_group < tiles ? t_begin + f.tiles_per_group : tiles;
+  const uint32_t lane = threadIdx.x % 64;
+  const uint32_t wave = threadIdx.x / 64;
+  const uint32_t col = lane % 16;
+  const uint32_t kb = lane / 16;
+  // the panel tile into LDS: wave w takes bursts w, w + kWaves, ...
+  const uint16_t* panel = f.panel + static_cast<uint64_t>(blockIdx.y) * kTileHalves;
+  for (uint32_t c = wave; c < kBursts; c += kWaves) {
+    burst_to_lds(panel + c * 512u + lane * 8u, stage + c * 512u);
+  }
+  half8_t bt[kBlocks][kSteps];
+  auto load_tile = [&](uint32_t t) {
+#pragma unroll
+    for (int tb = 0; tb < kBlocks; ++tb) {
+      const uint32_t token = t * kHeadTileTokens + (wave * kBlocks + tb) * 16u + col;
+      const uint16_t* p = f.emb + static_cast<uint64_t>(token < f.V ? token : 0u) * H + kb * 8u;
+#pragma unroll
+      for (int s = 0; s < kSteps; ++s) bt[tb][s] = *reinterpret_cast<const half8_t*>(p + s * 32);
+    }
+  };
+  load_tile(t_begin);
+  head_slots(f, m0, src_row, src_norm);
+  wait_vector_memory();
+  __syncthreads();
+  const uint16_t* a_lane = stage + col * kRowHalves + kb * 8u;
+  constexpr uint32_t kRbStride = 16u * kRowHalves;
+  for (uint32_t tile = t_begin; tile < t_end; ++tile) {
+    if (tile != t_begin) load_tile(tile);
+    HeadAcc<kBlocks> h;
+#pragma unroll
+    for (int tb = 0; tb < kBlocks; ++tb) {
+      h.gram[tb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb) h.acc[rb][tb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    // A fragments one step ahead: the LDS reads of step s + 1 are in flight
+    // during the MFMAs of step s
+    half8_t a_cur[4];
+    half8_t a_nxt[4];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+      a_cur[rb] = *reinterpret_cast<const half8_t*>(a_lane + rb * kRbStride);
+    }
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) {
+      if (s + 1 < kSteps) {
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+          a_nxt[rb] = *reinterpret_cast<const half8_t*>(a_lane + rb * kRbStride + (s + 1) * 32);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int tb = 0; tb < kBlocks; ++tb) {
+        h.gram[tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bt[tb][s], bt[tb][s], h.gram[tb], 0, 0, 0);
+      }
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb) {
+#pragma unroll
+        for (int tb = 0; tb < kBlocks; ++tb) {
+          h.acc[rb][tb] =
+              __builtin_amdgcn_mfma_f32_16x16x32_f16(a_cur[rb], bt[tb][s], h.acc[rb][tb], 0, 0, 0);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb) a_cur[rb] = a_nxt[rb];
+    }
+    head_records<kWaves, kBlocks>(f, h, epi, src_row, src_norm, m0, tile, tiles);
+  }
+}
+
+// Wide rows: units of KC steps of table rows and A (from the panel in L2),
+// two units in flight; the steady-state loop has no branch around a load,
+// and sched_barrier(0) keeps each unit's loads issued before the previous
+// unit's MFMAs (the scheduler would otherwise sink them past the MFMAs and
+// every unit would wait a full round trip).
+
 template <int KC>
 struct ABUnit {
-  half8_t b[kHeadBlocks][KC];
+  half8_t b[kWideBlocks][KC];
   half8_t a[4][KC];
 };
 
 template <int KC>
-__device__ __forceinline__ void unit_load(const uint16_t* const (&bptr)[kHeadBlocks],
-                                          uint32_t f0, BUnit<KC>& u) {
-#pragma unroll
-  for (int s = 0; s < KC; ++s) {
-#pragma unroll
-    for (uint32_t tb = 0; tb < kHeadBlocks; ++tb) {
-      u.b[tb][s] = *reinterpret_cast<const half8_t*>(bptr[tb] + f0 + s * 32);
-    }
-  }
-}
-template <int KC>
-__device__ __forceinline__ void unit_load(const uint16_t* const (&bptr)[kHeadBlocks],
+__device__ __forceinline__ void unit_load(const uint16_t* const (&bptr)[kWideBlocks],
                                           const uint16_t* const (&aptr)[4], uint32_t f0,
                                           ABUnit<KC>& u) {
 #pragma unroll
   for (int s = 0; s < KC; ++s) {
 #pragma unroll
-    for (uint32_t tb = 0; tb < kHeadBlocks; ++tb) {
+    for (int tb = 0; tb < kWideBlocks; ++tb) {
       u.b[tb][s] = *reinterpret_cast<const half8_t*>(bptr[tb] + f0 + s * 32);
     }
 #pragma unroll
@@ -328,60 +591,29 @@ __device__ __forceinline__ half8_t masked(const half8_t& v, uint32_t mask) {
   return __builtin_bit_cast(half8_t, q);
 }
 
-struct HeadAcc {
-  floatx4 acc[4][kHeadBlocks];
-  floatx4 gram[kHeadBlocks];
-};
-
-// MFMAs of one unit.  A from the LDS stage: a_lane points at the lane's
-// row-part of block 0 (rows outside the M-tile are zero in the stage).
-template <int KC>
-__device__ __forceinline__ void unit_mma(const BUnit<KC>& u, const uint16_t* a_lane,
-                                         uint32_t rb_stride, uint32_t f0, HeadAcc& h) {
-#pragma unroll
-  for (int s = 0; s < KC; ++s) {
-#pragma unroll
-    for (uint32_t tb = 0; tb < kHeadBlocks; ++tb) {
-      h.gram[tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(u.b[tb][s], u.b[tb][s], h.gram[tb], 0, 0, 0);
-    }
-#pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
-      const half8_t a = *reinterpret_cast<const half8_t*>(a_lane + rb * rb_stride + f0 + s * 32);
-#pragma unroll
-      for (uint32_t tb = 0; tb < kHeadBlocks; ++tb) {
-        h.acc[rb][tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, u.b[tb][s], h.acc[rb][tb], 0, 0, 0);
-      }
-    }
-  }
-}
-// A from L2, rows outside the M-tile masked
+// slots without a row are masked to zero (their panel rows are not written)
 template <int KC>
 __device__ __forceinline__ void unit_mma(const ABUnit<KC>& u, const uint32_t (&amask)[4],
-                                         HeadAcc& h) {
+                                         HeadAcc<kWideBlocks>& h) {
 #pragma unroll
   for (int s = 0; s < KC; ++s) {
 #pragma unroll
-    for (uint32_t tb = 0; tb < kHeadBlocks; ++tb) {
+    for (int tb = 0; tb < kWideBlocks; ++tb) {
       h.gram[tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(u.b[tb][s], u.b[tb][s], h.gram[tb], 0, 0, 0);
     }
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) {
       const half8_t a = masked(u.a[rb][s], amask[rb]);
 #pragma unroll
-      for (uint32_t tb = 0; tb < kHeadBlocks; ++tb) {
+      for (int tb = 0; tb < kWideBlocks; ++tb) {
         h.acc[rb][tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, u.b[tb][s], h.acc[rb][tb], 0, 0, 0);
       }
     }
   }
 }
 
-// kALds: A from the LDS stage; otherwise from L2 (wide rows).  KC steps per
-// unit, two units in flight; the steady-state loop has no branch around a
-// load, and sched_barrier(0) keeps each unit's loads issued before the
-// previous unit's MFMAs (the scheduler would otherwise sink them past the
-// MFMAs and every unit would wait a full round trip).
-template <bool kALds, int KC, bool kScores>
-__global__ __launch_bounds__(kThreads) void vocab_head_kernel(FallbackArgs f) {
+template <int KC>
+__global__ __launch_bounds__(kWideWaves * 64) void vocab_head_wide_kernel(FallbackArgs f) {
   extern __shared__ __align__(16) unsigned char dyn[];
   __shared__ uint32_t src_row[kMTile];
   __shared__ float src_norm[kMTile];
@@ -395,291 +627,55 @@ __global__ __launch_bounds__(kThreads) void vocab_head_kernel(FallbackArgs f) {
   const uint32_t H = f.H;
   const uint32_t col = lane % 16;
   const uint32_t kb = lane / 16;
-  const AView A{nullptr, f.y_hi, f.y_lo, f.row_index, f.m, f.rows, H};
-  const uint32_t row_halves = H + kAStagePad;
-  uint16_t* stage = reinterpret_cast<uint16_t*>(dyn + sizeof(HeadEpi));
+  const uint32_t row_halves = H + kPanelPad;
+  const uint16_t* panel = f.panel + static_cast<uint64_t>(blockIdx.y) * (panel_tile_bytes(H) / 2u);
   const uint32_t units = H / (32 * KC);
   constexpr uint32_t kUnitF = 32 * KC;
-  // table-row pointers of tile t for this lane
-  auto tile_rows = [&](uint32_t t, const uint16_t* (&bptr)[kHeadBlocks]) {
-#pragma unroll
-    for (uint32_t tb = 0; tb < kHeadBlocks; ++tb) {
-      const uint32_t token = t * kHeadTileTokens + wave * (16 * kHeadBlocks) + tb * 16 + col;
-      bptr[tb] = f.emb + static_cast<uint64_t>(token < f.V ? token : 0u) * H + kb * 8;
-    }
-  };
-  const uint16_t* bptr[kHeadBlocks];
-  tile_rows(t_begin, bptr);
-  // the first unit of the first tile is in flight during the row lookups
-  // and the A staging
-  BUnit<KC> b0;
-  if constexpr (kALds) unit_load<KC>(bptr, 0, b0);
-  if (threadIdx.x < kMTile) {
-    const uint32_t row = a_source_row(A, m0 + threadIdx.x);
-    const bool ok = row < f.rows;
-    src_row[threadIdx.x] = ok ? row : 0xFFFFFFFFu;
-    src_norm[threadIdx.x] = ok ? f.row_norm[row] : 0.0f;
-    if (blockIdx.x == 0 && ok && f.fb_map != nullptr) f.fb_map[row] = m0 + threadIdx.x;
-  }
+  head_slots(f, m0, src_row, src_norm);
   __syncthreads();
-  if constexpr (kALds) {
-    // the M-tile's FP16 split, [row][hi|lo][H + pad], zero rows beyond it;
-    // kStageBatch loads per thread are in flight before their stores (a
-    // copy loop that stores each load before the next would pay one round
-    // trip per iteration)
-    constexpr uint32_t kStageBatch = 6;
-    const uint32_t per = H / 8;
-    const uint32_t n = 64u * per;
-    for (uint32_t base = threadIdx.x; base < n; base += kThreads * kStageBatch) {
-      uint4 v[kStageBatch];
-#pragma unroll
-      for (uint32_t u = 0; u < kStageBatch; ++u) {
-        const uint32_t q = base + u * kThreads;
-        const uint32_t p = q / per;
-        const uint32_t row = q < n ? src_row[p / 2] : 0xFFFFFFFFu;
-        v[u] = row != 0xFFFFFFFFu
-                   ? *reinterpret_cast<const uint4*>(((p & 1u) ? f.y_lo : f.y_hi) +
-                                                    static_cast<uint64_t>(row) * H + (q % per) * 8)
-                   : uint4{0u, 0u, 0u, 0u};
-      }
-#pragma unroll
-      for (uint32_t u = 0; u < kStageBatch; ++u) {
-        const uint32_t q = base + u * kThreads;
-        if (q < n) *reinterpret_cast<uint4*>(stage + (q / per) * row_halves + (q % per) * 8) = v[u];
-      }
-    }
-    __syncthreads();
-  }
-  const uint16_t* a_lane = stage + col * row_halves + kb * 8;  // LDS variant
-  const uint32_t rb_stride = 16u * row_halves;
-  const uint16_t* aptr[4];                                     // L2 variant
+  const uint16_t* aptr[4];
   uint32_t amask[4];
 #pragma unroll
   for (int rb = 0; rb < 4; ++rb) {
-    const uint32_t row = src_row[rb * 8 + col / 2];
-    const bool ok = row != 0xFFFFFFFFu;
-    aptr[rb] = ((col & 1u) ? f.y_lo : f.y_hi) + static_cast<uint64_t>(ok ? row : 0u) * H + kb * 8;
-    amask[rb] = ok ? 0xFFFFFFFFu : 0u;
+    aptr[rb] = panel + (16u * rb + col) * row_halves + kb * 8u;
+    amask[rb] = src_row[rb * 8 + col / 2] != kInvalidToken ? 0xFFFFFFFFu : 0u;
   }
-
+  const uint16_t* bptr[kWideBlocks];
   for (uint32_t tile = t_begin; tile < t_end; ++tile) {
-    if (tile != t_begin) tile_rows(tile, bptr);
-    HeadAcc h;
 #pragma unroll
-    for (uint32_t tb = 0; tb < kHeadBlocks; ++tb) {
+    for (int tb = 0; tb < kWideBlocks; ++tb) {
+      const uint32_t token = tile * kHeadTileTokens + (wave * kWideBlocks + tb) * 16u + col;
+      bptr[tb] = f.emb + static_cast<uint64_t>(token < f.V ? token : 0u) * H + kb * 8u;
+    }
+    HeadAcc<kWideBlocks> h;
+#pragma unroll
+    for (int tb = 0; tb < kWideBlocks; ++tb) {
       h.gram[tb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int rb = 0; rb < 4; ++rb) h.acc[rb][tb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     }
-    if constexpr (kALds) {
-      BUnit<KC> u0, u1;
-      if (tile == t_begin) {
-        u0 = b0;
-      } else {
-        unit_load<KC>(bptr, 0, u0);
-      }
-      uint32_t q = 0;
-      for (; q + 2 < units; q += 2) {
-        unit_load<KC>(bptr, (q + 1) * kUnitF, u1);
-        __builtin_amdgcn_sched_barrier(0);
-        unit_mma<KC>(u0, a_lane, rb_stride, q * kUnitF, h);
-        __builtin_amdgcn_sched_barrier(0);
-        unit_load<KC>(bptr, (q + 2) * kUnitF, u0);
-        __builtin_amdgcn_sched_barrier(0);
-        unit_mma<KC>(u1, a_lane, rb_stride, (q + 1) * kUnitF, h);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      if (q + 1 < units) {  // the last two units
-        unit_load<KC>(bptr, (q + 1) * kUnitF, u1);
-        __builtin_amdgcn_sched_barrier(0);
-        unit_mma<KC>(u0, a_lane, rb_stride, q * kUnitF, h);
-        unit_mma<KC>(u1, a_lane, rb_stride, (q + 1) * kUnitF, h);
-      } else {
-        unit_mma<KC>(u0, a_lane, rb_stride, q * kUnitF, h);
-      }
+    ABUnit<KC> u0, u1;
+    unit_load<KC>(bptr, aptr, 0, u0);
+    uint32_t q = 0;
+    for (; q + 2 < units; q += 2) {
+      unit_load<KC>(bptr, aptr, (q + 1) * kUnitF, u1);
+      __builtin_amdgcn_sched_barrier(0);
+      unit_mma<KC>(u0, amask, h);
+      __builtin_amdgcn_sched_barrier(0);
+      unit_load<KC>(bptr, aptr, (q + 2) * kUnitF, u0);
+      __builtin_amdgcn_sched_barrier(0);
+      unit_mma<KC>(u1, amask, h);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (q + 1 < units) {
+      unit_load<KC>(bptr, aptr, (q + 1) * kUnitF, u1);
+      __builtin_amdgcn_sched_barrier(0);
+      unit_mma<KC>(u0, amask, h);
+      unit_mma<KC>(u1, amask, h);
     } else {
-      ABUnit<KC> u0, u1;
-      unit_load<KC>(bptr, aptr, 0, u0);
-      uint32_t q = 0;
-      for (; q + 2 < units; q += 2) {
-        unit_load<KC>(bptr, aptr, (q + 1) * kUnitF, u1);
-        __builtin_amdgcn_sched_barrier(0);
-        unit_mma<KC>(u0, amask, h);
-        __builtin_amdgcn_sched_barrier(0);
-        unit_load<KC>(bptr, aptr, (q + 2) * kUnitF, u0);
-        __builtin_amdgcn_sched_barrier(0);
-        unit_mma<KC>(u1, amask, h);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      if (q + 1 < units) {
-        unit_load<KC>(bptr, aptr, (q + 1) * kUnitF, u1);
-        __builtin_amdgcn_sched_barrier(0);
-        unit_mma<KC>(u0, amask, h);
-        unit_mma<KC>(u1, amask, h);
-      } else {
-        unit_mma<KC>(u0, amask, h);
-      }
+      unit_mma<KC>(u0, amask, h);
     }
-
-    if constexpr (kScores) {
-      // the comparator: every score of the tile, and the token norms
-      const uint32_t tok0 = tile * kHeadTileTokens;
-#pragma unroll
-      for (uint32_t tb = 0; tb < kHeadBlocks; ++tb) {
-        const uint32_t token = tok0 + wave * (16 * kHeadBlocks) + tb * 16 + col;
-        const uint32_t e = col % 4u;
-        const float d = e == 0u ? h.gram[tb][0]
-                                : (e == 1u ? h.gram[tb][1] : (e == 2u ? h.gram[tb][2] : h.gram[tb][3]));
-        const float tsq = __shfl(d, static_cast<int>(col + 16u * (col / 4u)));
-        if (token >= f.V) continue;
-        if (blockIdx.y == 0 && kb == 0u && f.tok_norm != nullptr) {
-          f.tok_norm[token] = __fsqrt_rn(tsq) * (1.0f + 0x1p-7f);
-        }
-#pragma unroll
-        for (int rb = 0; rb < 4; ++rb) {
-#pragma unroll
-          for (int jj = 0; jj < 2; ++jj) {
-            const uint32_t i = rb * 8 + 2 * kb + jj;
-            if (m0 + i < f.m) {
-              f.scores[static_cast<uint64_t>(m0 + i) * f.V + token] =
-                  h.acc[rb][tb][2 * jj] + h.acc[rb][tb][2 * jj + 1];
-            }
-          }
-        }
-      }
-      continue;
-    }
-    // The tile's window records, reduced in registers.  Lane l holds
-    // D[4 (l / 16) + i][l % 16] of each block: rows 2j, 2j + 1 (hi, lo of
-    // row 8 rb + j) for j = 2 kb and 2 kb + 1, so the scores of row
-    // 8 rb + 2 kb + jj (jj = 0, 1) are h.acc[rb][tb][2 jj] + [2 jj + 1] for
-    // the wave's tokens wave * 48 + 16 tb + col.  The Gram diagonal of
-    // column c sits in lane c + 16 (c / 4), element c % 4.
-    const uint32_t tok0 = tile * kHeadTileTokens;
-    const uint32_t nt = f.V - tok0 < kHeadTileTokens ? f.V - tok0 : kHeadTileTokens;
-    float g[4][2][kHeadBlocks];
-    float b[4][2][kHeadBlocks];
-    bool valid[kHeadBlocks];
-#pragma unroll
-    for (uint32_t tb = 0; tb < kHeadBlocks; ++tb) {
-      const uint32_t e = col % 4u;
-      const float d = e == 0u ? h.gram[tb][0]
-                              : (e == 1u ? h.gram[tb][1] : (e == 2u ? h.gram[tb][2] : h.gram[tb][3]));
-      const float tsq = __shfl(d, static_cast<int>(col + 16u * (col / 4u)));
-      const float tok_norm = __fsqrt_rn(tsq) * (1.0f + 0x1p-7f);
-      valid[tb] = wave * (16 * kHeadBlocks) + tb * 16 + col < nt;
-#pragma unroll
-      for (int rb = 0; rb < 4; ++rb) {
-#pragma unroll
-        for (int jj = 0; jj < 2; ++jj) {
-          const uint32_t i = rb * 8 + 2 * kb + jj;
-          g[rb][jj][tb] = h.acc[rb][tb][2 * jj] + h.acc[rb][tb][2 * jj + 1];
-          b[rb][jj][tb] =
-              __builtin_fmaf(tok_norm, __builtin_fmaf(f.coef, src_norm[i], f.coef2), f.slack);
-        }
-      }
-    }
-    // per row: the best lower bound g - b and finiteness, over the lane's
-    // tokens, then over the 16 lanes of the row, then over the 4 waves
-#pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
-#pragma unroll
-      for (int jj = 0; jj < 2; ++jj) {
-        float lo = -__builtin_huge_valf();
-        uint32_t fin = 1u;
-#pragma unroll
-        for (uint32_t tb = 0; tb < kHeadBlocks; ++tb) {
-          if (!valid[tb]) continue;
-          const float gv = g[rb][jj][tb];
-          const float bv = b[rb][jj][tb];
-          fin &= (__builtin_isfinite(gv) && __builtin_isfinite(bv) && bv < 0x1p100f) ? 1u : 0u;
-          lo = __builtin_fmaxf(lo, gv - bv);
-        }
-#pragma unroll
-        for (int m = 8; m > 0; m >>= 1) {
-          lo = __builtin_fmaxf(lo, __shfl_xor(lo, m, 16));
-          fin &= __shfl_xor(fin, m, 16);
-        }
-        if (col == 0u) {
-          epi.lo[wave][rb * 8 + 2 * kb + jj] = lo;
-          epi.fin[wave][rb * 8 + 2 * kb + jj] = fin;
-        }
-      }
-    }
-    __syncthreads();
-    // members (g + b >= L) per row: count per wave, rank across waves
-    float L[4][2];
-    uint32_t rowfin[4][2];
-    uint32_t below[4][2][kHeadBlocks];  // members of this row before (tb, col) in the wave
-    uint32_t mine[4][2];
-#pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
-#pragma unroll
-      for (int jj = 0; jj < 2; ++jj) {
-        const uint32_t i = rb * 8 + 2 * kb + jj;
-        float l = epi.lo[0][i];
-        uint32_t fn = epi.fin[0][i];
-#pragma unroll
-        for (int w = 1; w < 4; ++w) {
-          l = __builtin_fmaxf(l, epi.lo[w][i]);
-          fn &= epi.fin[w][i];
-        }
-        L[rb][jj] = l;
-        rowfin[rb][jj] = fn;
-        uint32_t run = 0u;
-#pragma unroll
-        for (uint32_t tb = 0; tb < kHeadBlocks; ++tb) {
-          const bool member = valid[tb] && g[rb][jj][tb] + b[rb][jj][tb] >= l;
-          const uint64_t mask = __ballot(member);
-          const uint32_t group = static_cast<uint32_t>(mask >> (16u * kb)) & 0xFFFFu;
-          below[rb][jj][tb] = run + static_cast<uint32_t>(__popc(group & ((1u << col) - 1u)));
-          run += static_cast<uint32_t>(__popc(group));
-        }
-        mine[rb][jj] = run;
-        if (col == 0u) epi.cnt[wave][i] = run;
-      }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
-#pragma unroll
-      for (int jj = 0; jj < 2; ++jj) {
-        const uint32_t i = rb * 8 + 2 * kb + jj;
-        if (src_row[i] == 0xFFFFFFFFu) continue;
-        uint32_t base = 0u;
-        uint32_t total = 0u;
-#pragma unroll
-        for (uint32_t w = 0; w < 4; ++w) {
-          const uint32_t c = epi.cnt[w][i];
-          base += w < wave ? c : 0u;
-          total += c;
-        }
-        const bool ordinary = rowfin[rb][jj] && total <= static_cast<uint32_t>(kTileMembers);
-        TileRecord* rec = f.records + static_cast<uint64_t>(m0 + i) * tiles + tile;
-        if (ordinary) {
-#pragma unroll
-          for (uint32_t tb = 0; tb < kHeadBlocks; ++tb) {
-            const float gv = g[rb][jj][tb];
-            const float bv = b[rb][jj][tb];
-            if (valid[tb] && gv + bv >= L[rb][jj]) {
-              const uint32_t token = tok0 + wave * (16 * kHeadBlocks) + tb * 16 + col;
-              rec->m[base + below[rb][jj][tb]] = TileMember{token, token, gv - bv, gv + bv};
-            }
-          }
-        }
-        if (wave == 0 && col == 0u) {
-          rec->best_lower = L[rb][jj];
-          rec->flags = ordinary ? 0u : kTileRescoreAll;
-          rec->min_token = tok0;
-          rec->min_pos = tok0;
-          rec->begin = tok0;
-          rec->count = nt;
-          rec->n_members = ordinary ? total : 0u;
-        }
-      }
-    }
-    (void)mine;
-    __syncthreads();  // the next tile rewrites the scores
+    head_records<kWideWaves, kWideBlocks>(f, h, epi, src_row, src_norm, m0, tile, tiles);
   }
 }
 
@@ -700,47 +696,48 @@ hipError_t launch_projection(const ProjArgs& args, hipStream_t stream) {
   return hipGetLastError();
 }
 
-template <bool kALds, int KC, bool kScores>
-static void launch_head(const FallbackArgs& f, dim3 grid, uint32_t lds, hipStream_t stream) {
-  hipLaunchKernelGGL((vocab_head_kernel<kALds, KC, kScores>), grid, dim3(kThreads), lds, stream, f);
+// Narrow-row variant per H = 32 kSteps (H % 64 == 0, panel tile <= 76 KiB).
+template <int kSteps>
+static void launch_head_lds(const FallbackArgs& f, dim3 grid, hipStream_t stream) {
+  constexpr int kWaves = kHeadLdsWaves;
+  constexpr int kBlocks = static_cast<int>(kHeadTileBlocks) / kWaves;
+  const uint32_t lds = static_cast<uint32_t>(sizeof(HeadEpi) + panel_tile_bytes(32u * kSteps));
+  hipLaunchKernelGGL((vocab_head_lds_kernel<kWaves, kBlocks, kSteps>), grid, dim3(kWaves * 64), lds,
+                     stream, f);
 }
 
-template <bool kScores>
-static hipError_t launch_vocab(const FallbackArgs& args, hipStream_t stream) {
+hipError_t launch_fallback(const FallbackArgs& args, hipStream_t stream) {
   if (args.m == 0) return hipSuccess;
-  if (args.H % 64 != 0) return hipErrorInvalidValue;
+  if (args.H % 64 != 0 || args.panel == nullptr) return hipErrorInvalidValue;
   // runs of tiles per workgroup: as many workgroups as compute units (or
   // tiles), every run the same length
   const uint32_t tiles = fallback_tiles(args.V);
   const uint32_t groups = args.groups > 0 ? args.groups : 256u;
   FallbackArgs f = args;
   f.tiles_per_group = (tiles + groups - 1) / groups;
-  const dim3 grid((tiles + f.tiles_per_group - 1) / f.tiles_per_group,
-                  (args.m + kMTile - 1) / kMTile);
+  const dim3 grid((tiles + f.tiles_per_group - 1) / f.tiles_per_group, panel_tiles(args.m));
   const uint32_t steps = args.H / 32;  // even
-  const uint32_t stage = a_stage_bytes(args.H);
-  if (stage <= kAStageMaxBytes) {
-    const uint32_t lds = static_cast<uint32_t>(sizeof(HeadEpi)) + stage;
-    if (steps % 6 == 0) {
-      launch_head<true, 6, kScores>(f, grid, lds, stream);
-    } else if (steps % 4 == 0) {
-      launch_head<true, 4, kScores>(f, grid, lds, stream);
-    } else {
-      launch_head<true, 2, kScores>(f, grid, lds, stream);
+  if (panel_tile_bytes(args.H) <= kPanelLdsMaxBytes) {
+    switch (steps) {
+      case 2: launch_head_lds<2>(f, grid, stream); break;
+      case 4: launch_head_lds<4>(f, grid, stream); break;
+      case 6: launch_head_lds<6>(f, grid, stream); break;
+      case 8: launch_head_lds<8>(f, grid, stream); break;
+      case 10: launch_head_lds<10>(f, grid, stream); break;
+      case 12: launch_head_lds<12>(f, grid, stream); break;
+      case 14: launch_head_lds<14>(f, grid, stream); break;
+      case 16: launch_head_lds<16>(f, grid, stream); break;
+      case 18: launch_head_lds<18>(f, grid, stream); break;
+      default: return hipErrorInvalidValue;
     }
   } else {
-    launch_head<false, 2, kScores>(f, grid, static_cast<uint32_t>(sizeof(HeadEpi)), stream);
+    const uint32_t lds = static_cast<uint32_t>(sizeof(HeadEpi));
+    const dim3 block(kWideWaves * 64);
+    // units of two steps: wider units spill (A and B of a unit share the
+    // registers)
+    hipLaunchKernelGGL((vocab_head_wide_kernel<2>), grid, block, lds, stream, f);
   }
   return hipGetLastError();
-}
-
-hipError_t launch_fallback(const FallbackArgs& args, hipStream_t stream) {
-  return launch_vocab<false>(args, stream);
-}
-
-hipError_t launch_vocab_scores(const FallbackArgs& args, hipStream_t stream) {
-  if (args.scores == nullptr) return hipErrorInvalidValue;
-  return launch_vocab<true>(args, stream);
 }
 
 } // namespace mf

@@ -1,8 +1,9 @@
 // The decode tail on gfx950 (mf_decode_tail_f16):
 //
 //   K1 tail_norm_kernel      final RMSNorm in the reference order, per-row
-//                            metadata (list, kind), FP16 hi/lo split of the
-//                            unrestricted rows for the MFMA head; presets the
+//                            metadata (list, kind), FP16 hi/lo split (all
+//                            rows for the MFMA gather; the unrestricted rows
+//                            again as the MFMA head's panel); presets the
 //                            outputs of invalid and unrestricted rows
 //   K2 gather_kernel         streams the allowed embedding rows of one tile
 //                            (a chunk of one row's list) and writes a tile
@@ -58,14 +59,29 @@ __device__ float sequential_sum(const float* sq, uint32_t H) {
   return s;
 }
 
+// Workgroup r < rows normalizes row r; workgroup rows + j normalizes row
+// fb_rows[j] again for slot j of the MFMA head's panel (the same code on the
+// same data, so the same bits) and writes only the slot.
 __global__ __launch_bounds__(kWave) void tail_norm_kernel(TailNormArgs a) {
   extern __shared__ float lds[];
   float* xs = lds;
   float* sq = lds + a.H;
   __shared__ float inverse_shared;
-  const uint64_t r = blockIdx.x;
+  const bool slot = blockIdx.x >= a.rows;
+  const uint32_t j = blockIdx.x - a.rows;  // the slot (slot workgroups)
+  uint64_t r = blockIdx.x;
   const uint32_t lane = threadIdx.x;
   const uint32_t H = a.H;
+  if (slot) {
+    r = a.fb_rows[j];
+    if (r >= a.rows) {
+      if (lane == 0) {
+        a.fb_slot_row[j] = kInvalidToken;
+        a.fb_slot_norm[j] = 0.0f;
+      }
+      return;
+    }
+  }
   if ((H & 3u) == 0) {
     // four float4 loads per lane in flight before the LDS stores
     constexpr uint32_t kBatch = 4;
@@ -99,37 +115,47 @@ __global__ __launch_bounds__(kWave) void tail_norm_kernel(TailNormArgs a) {
   RowMeta meta{0u, 0u, 0u, kRowInvalid};
   if (lane == 0) {
     // metadata loads first: they resolve while the serial sum runs
-    const uint32_t s = a.row_state[r];
-    uint32_t b = 0u, e = 0u;
-    if (s < a.states) {
-      b = a.offsets[s];
-      e = a.offsets[s + 1];
+    uint32_t s = 0u, b = 0u, e = 0u;
+    if (!slot) {
+      s = a.row_state[r];
+      if (s < a.states) {
+        b = a.offsets[s];
+        e = a.offsets[s + 1];
+      }
     }
     if (a.weight != nullptr) {
       const float sum_squares = sequential_sum(sq, H);
       const float mean = div_rn(sum_squares, static_cast<float>(H));
       inverse_shared = div_rn(1.0f, sqrt_rn(mean + a.epsilon));
     }
-    meta.state = s;
-    if (s == kStateUnrestricted) {
-      meta.kind = kRowUnrestricted;
-      meta.count = a.V;
-    } else if (s < a.states && e > b && e <= a.nnz && e - b <= a.max_count) {
-      meta = RowMeta{b, e - b, s, kRowRestricted};
+    if (!slot) {
+      meta.state = s;
+      if (s == kStateUnrestricted) {
+        meta.kind = kRowUnrestricted;
+        meta.count = a.V;
+      } else if (s < a.states && e > b && e <= a.nnz && e - b <= a.max_count) {
+        meta = RowMeta{b, e - b, s, kRowRestricted};
+      }
+      a.row_meta[r] = meta;
+      if (meta.kind != kRowRestricted) {
+        // invalid rows keep these; unrestricted rows are overwritten by the
+        // finalize kernel when the MFMA head was given them
+        a.out_token[r] = kInvalidToken;
+        if (a.out_score != nullptr) a.out_score[r] = __builtin_nanf("");
+        if (a.out_next != nullptr) a.out_next[r] = kInvalidToken;
+      }
+      if (a.fb_map != nullptr) a.fb_map[r] = kInvalidToken;
     }
-    a.row_meta[r] = meta;
-    if (meta.kind != kRowRestricted) {
-      // invalid rows keep these; unrestricted rows are overwritten by the
-      // finalize kernel when the MFMA head was given them
-      a.out_token[r] = kInvalidToken;
-      if (a.out_score != nullptr) a.out_score[r] = __builtin_nanf("");
-      if (a.out_next != nullptr) a.out_next[r] = kInvalidToken;
-    }
-    if (a.fb_map != nullptr) a.fb_map[r] = kInvalidToken;
   }
   __syncthreads();
   const float inverse = inverse_shared;
   const bool split = a.y_hi != nullptr;
+  // slot workgroups: the slot's [hi | lo] rows of the panel
+  uint16_t* panel_hi = nullptr;
+  if (slot) {
+    panel_hi = a.fb_panel + static_cast<uint64_t>(j / kPanelRows) * (panel_tile_bytes(H) / 2u) +
+               static_cast<uint64_t>(j % kPanelRows) * 2u * (H + kPanelPad);
+  }
   float norm_sq = 0.0f;
   for (uint32_t c = lane; c < H; c += kWave) {
     float v = xs[c];
@@ -137,12 +163,18 @@ __global__ __launch_bounds__(kWave) void tail_norm_kernel(TailNormArgs a) {
       const float scaled = v * inverse;
       v = scaled * a.weight[c];
     }
-    a.y[r * H + c] = v;
     norm_sq = __builtin_fmaf(v, v, norm_sq);
-    if (split) {
-      const _Float16 hi = static_cast<_Float16>(v);
-      a.y_hi[r * H + c] = __builtin_bit_cast(uint16_t, hi);
-      a.y_lo[r * H + c] = float_to_half_rne(v - static_cast<float>(hi));
+    const _Float16 hi = static_cast<_Float16>(v);
+    const uint16_t lo = float_to_half_rne(v - static_cast<float>(hi));
+    if (slot) {
+      panel_hi[c] = __builtin_bit_cast(uint16_t, hi);
+      panel_hi[H + kPanelPad + c] = lo;
+    } else {
+      a.y[r * H + c] = v;
+      if (split) {
+        a.y_hi[r * H + c] = __builtin_bit_cast(uint16_t, hi);
+        a.y_lo[r * H + c] = lo;
+      }
     }
   }
 #pragma unroll
@@ -150,7 +182,13 @@ __global__ __launch_bounds__(kWave) void tail_norm_kernel(TailNormArgs a) {
   if (lane == 0) {
     // FP32 sum of H squares is within a relative H 2^-24 of the exact value;
     // the factor covers that and the sqrt for any H <= 2^16
-    a.row_norm[r] = __fsqrt_rn(norm_sq) * (1.0f + 0x1p-7f);
+    const float bound = __fsqrt_rn(norm_sq) * (1.0f + 0x1p-7f);
+    if (slot) {
+      a.fb_slot_norm[j] = bound;
+      a.fb_slot_row[j] = static_cast<uint32_t>(r);
+    } else {
+      a.row_norm[r] = bound;
+    }
   }
 }
 
@@ -708,9 +746,10 @@ __global__ __launch_bounds__(kWave) void finalize_kernel(FinalizeArgs a) {
 
 } // namespace
 
-hipError_t launch_tail_norm(const TailNormArgs& args, uint32_t rows, hipStream_t stream) {
+hipError_t launch_tail_norm(const TailNormArgs& args, hipStream_t stream) {
   const size_t lds = 2u * static_cast<size_t>(args.H) * sizeof(float);
-  hipLaunchKernelGGL(tail_norm_kernel, dim3(rows), dim3(kWave), lds, stream, args);
+  const uint32_t slots = args.fb_panel != nullptr ? args.fb_m : 0u;
+  hipLaunchKernelGGL(tail_norm_kernel, dim3(args.rows + slots), dim3(kWave), lds, stream, args);
   return hipGetLastError();
 }
 
