@@ -226,6 +226,18 @@ __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
       __builtin_elementwise_min(lane_value(r, 32), lane_value(r, 48)));
 }
 
+// A sum over the wave in an unspecified order (for bounds, not reference
+// arithmetic).
+__device__ __forceinline__ float wave_sum_f32(float v) {
+  v += as_float(row_ror<8>(as_u32(v), 0u));
+  v += as_float(row_ror<4>(as_u32(v), 0u));
+  v += as_float(row_ror<2>(as_u32(v), 0u));
+  v += as_float(row_ror<1>(as_u32(v), 0u));
+  const uint32_t r = as_u32(v);
+  return (as_float(lane_value(r, 0)) + as_float(lane_value(r, 16))) +
+         (as_float(lane_value(r, 32)) + as_float(lane_value(r, 48)));
+}
+
 __device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
   const uint32_t r = row16_sum(v);
   return lane_value(r, 0) + lane_value(r, 16) + lane_value(r, 32) + lane_value(r, 48);

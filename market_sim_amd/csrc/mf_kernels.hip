@@ -28,7 +28,7 @@ template <bool kHalfIn, bool kHalfW, bool kHalfOut>
 __global__ __launch_bounds__(kWave) void rms_norm_kernel(
     const void* __restrict__ input, const void* __restrict__ weight,
     void* output, float* __restrict__ row_norm, uint32_t H, float epsilon) {
-  extern __shared__ float xs[];
+  extern __shared__ __align__(16) float xs[];
   __shared__ float inverse_shared;
   const uint64_t r = blockIdx.x;
   const uint32_t lane = threadIdx.x;
@@ -447,7 +447,7 @@ __device__ bool load_block_ids(const HeadArgs& a, const RowList& rl,
 // block summarized into a record in LDS, then merged (finalize_row).
 template <int kH, int kG>
 __global__ __launch_bounds__(kThreads) void head_kernel(HeadArgs a) {
-  extern __shared__ float ys[];
+  extern __shared__ __align__(16) float ys[];
   __shared__ HeadShared sh;
   const uint32_t r = blockIdx.x;
   const RowList rl = resolve_row(a, r);

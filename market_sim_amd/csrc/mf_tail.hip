@@ -31,27 +31,41 @@ constexpr int kThreads = 256;
 
 // Sum of squares in the reference order (operators.cpp:527-531): every square
 // rounded (lanes compute them in parallel into sq[]), then added in column
-// order by one lane, with the LDS reads of the next four values issued ahead
-// of the dependent adds.
+// order by one lane.  Blocks of 16 values alternate between two register
+// sets: the LDS reads of block i + 1 are issued before the adds of block i
+// (sched_barrier keeps the scheduler from sinking them to their use, which
+// would pay an LDS round trip per block).
+__device__ __forceinline__ void load16(const float4* q, uint32_t i, float4 (&v)[4]) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) v[k] = q[4 * i + k];
+}
+__device__ __forceinline__ float add16(float s, const float4 (&v)[4]) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    s = s + v[k].x;
+    s = s + v[k].y;
+    s = s + v[k].z;
+    s = s + v[k].w;
+  }
+  return s;
+}
 __device__ float sequential_sum(const float* sq, uint32_t H) {
   float s = 0.0f;
   uint32_t c = 0;
-  if ((H & 15u) == 0) {
-    // 16 values per step; the next 16 are read while these are added
+  if ((H & 31u) == 0) {
     const float4* q = reinterpret_cast<const float4*>(sq);
-    const uint32_t n16 = H / 16;
-    float4 c0 = q[0], c1 = q[1], c2 = q[2], c3 = q[3];
-    for (uint32_t i = 0; i < n16; ++i) {
-      const uint32_t j = (i + 1 < n16 ? i + 1 : i) * 4;
-      const float4 n0 = q[j], n1 = q[j + 1], n2 = q[j + 2], n3 = q[j + 3];
-      const float v[16] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w,
-                           c2.x, c2.y, c2.z, c2.w, c3.x, c3.y, c3.z, c3.w};
-#pragma unroll
-      for (int k = 0; k < 16; ++k) s = s + v[k];
-      c0 = n0;
-      c1 = n1;
-      c2 = n2;
-      c3 = n3;
+    const uint32_t n16 = H / 16;  // even
+    float4 a[4], b[4];
+    load16(q, 0, a);
+    for (uint32_t i = 0; i < n16; i += 2) {
+      load16(q, i + 1, b);
+      __builtin_amdgcn_sched_barrier(0);
+      s = add16(s, a);
+      __builtin_amdgcn_sched_barrier(0);
+      load16(q, i + 2 < n16 ? i + 2 : i, a);
+      __builtin_amdgcn_sched_barrier(0);
+      s = add16(s, b);
+      __builtin_amdgcn_sched_barrier(0);
     }
     c = H;
   }
@@ -63,7 +77,7 @@ __device__ float sequential_sum(const float* sq, uint32_t H) {
 // fb_rows[j] again for slot j of the MFMA head's panel (the same code on the
 // same data, so the same bits) and writes only the slot.
 __global__ __launch_bounds__(kWave) void tail_norm_kernel(TailNormArgs a) {
-  extern __shared__ float lds[];
+  extern __shared__ __align__(16) float lds[];
   float* xs = lds;
   float* sq = lds + a.H;
   __shared__ float inverse_shared;
@@ -82,17 +96,26 @@ __global__ __launch_bounds__(kWave) void tail_norm_kernel(TailNormArgs a) {
       return;
     }
   }
+  // the row's state first: its list offsets depend on it
+  uint32_t s = 0u;
+  if (!slot && lane == 0) s = a.row_state[r];
+  float* ws = lds + 2u * H;  // weight (when given)
+  const bool weighted = a.weight != nullptr;
   if ((H & 3u) == 0) {
-    // four float4 loads per lane in flight before the LDS stores
+    // x and the weight: four float4 loads of each per lane in flight before
+    // the LDS stores
     constexpr uint32_t kBatch = 4;
     const float4* x4 = reinterpret_cast<const float4*>(a.x + r * H);
+    const float4* w4 = reinterpret_cast<const float4*>(a.weight);
     const uint32_t n = H / 4;
     for (uint32_t base = lane; base < n; base += kWave * kBatch) {
       float4 v[kBatch];
+      float4 wv[kBatch];
 #pragma unroll
       for (uint32_t u = 0; u < kBatch; ++u) {
         const uint32_t q = base + u * kWave;
         v[u] = q < n ? x4[q] : float4{0.0f, 0.0f, 0.0f, 0.0f};
+        wv[u] = (weighted && q < n) ? w4[q] : float4{0.0f, 0.0f, 0.0f, 0.0f};
       }
 #pragma unroll
       for (uint32_t u = 0; u < kBatch; ++u) {
@@ -101,6 +124,7 @@ __global__ __launch_bounds__(kWave) void tail_norm_kernel(TailNormArgs a) {
           reinterpret_cast<float4*>(xs)[q] = v[u];
           reinterpret_cast<float4*>(sq)[q] =
               float4{v[u].x * v[u].x, v[u].y * v[u].y, v[u].z * v[u].z, v[u].w * v[u].w};
+          if (weighted) reinterpret_cast<float4*>(ws)[q] = wv[u];
         }
       }
     }
@@ -109,21 +133,19 @@ __global__ __launch_bounds__(kWave) void tail_norm_kernel(TailNormArgs a) {
       const float v = a.x[r * H + c];
       xs[c] = v;
       sq[c] = v * v;
+      if (weighted) ws[c] = a.weight[c];
     }
   }
   __syncthreads();
   RowMeta meta{0u, 0u, 0u, kRowInvalid};
   if (lane == 0) {
-    // metadata loads first: they resolve while the serial sum runs
-    uint32_t s = 0u, b = 0u, e = 0u;
-    if (!slot) {
-      s = a.row_state[r];
-      if (s < a.states) {
-        b = a.offsets[s];
-        e = a.offsets[s + 1];
-      }
+    // the offsets loads are in flight during the serial sum
+    uint32_t b = 0u, e = 0u;
+    if (!slot && s < a.states) {
+      b = a.offsets[s];
+      e = a.offsets[s + 1];
     }
-    if (a.weight != nullptr) {
+    if (weighted) {
       const float sum_squares = sequential_sum(sq, H);
       const float mean = div_rn(sum_squares, static_cast<float>(H));
       inverse_shared = div_rn(1.0f, sqrt_rn(mean + a.epsilon));
@@ -159,9 +181,9 @@ __global__ __launch_bounds__(kWave) void tail_norm_kernel(TailNormArgs a) {
   float norm_sq = 0.0f;
   for (uint32_t c = lane; c < H; c += kWave) {
     float v = xs[c];
-    if (a.weight != nullptr) {
+    if (weighted) {
       const float scaled = v * inverse;
-      v = scaled * a.weight[c];
+      v = scaled * ws[c];
     }
     norm_sq = __builtin_fmaf(v, v, norm_sq);
     const _Float16 hi = static_cast<_Float16>(v);
@@ -177,8 +199,7 @@ __global__ __launch_bounds__(kWave) void tail_norm_kernel(TailNormArgs a) {
       }
     }
   }
-#pragma unroll
-  for (int m = kWave / 2; m > 0; m >>= 1) norm_sq += __shfl_xor(norm_sq, m);
+  norm_sq = wave_sum_f32(norm_sq);
   if (lane == 0) {
     // FP32 sum of H squares is within a relative H 2^-24 of the exact value;
     // the factor covers that and the sqrt for any H <= 2^16
@@ -393,7 +414,7 @@ __device__ void gather_tile(const GatherArgs& a, uint32_t r, uint32_t k, uint32_
 // Grid mode (any number of rows): blockIdx.x = k * rows + r.
 template <ScoreSource kSrc, int kH, int kG>
 __global__ __launch_bounds__(kThreads) void gather_kernel(GatherArgs a) {
-  extern __shared__ float ys[];
+  extern __shared__ __align__(16) float ys[];
   __shared__ GatherShared sh;
   const uint32_t r = blockIdx.x % a.rows;
   const uint32_t k = blockIdx.x / a.rows;
@@ -410,7 +431,7 @@ __global__ __launch_bounds__(kThreads) void gather_kernel(GatherArgs a) {
 // staged hidden vector.
 template <ScoreSource kSrc, int kH, int kG>
 __global__ __launch_bounds__(kThreads) void gather_planned_kernel(GatherArgs a) {
-  extern __shared__ float ys[];
+  extern __shared__ __align__(16) float ys[];
   __shared__ GatherShared sh;
   __shared__ TilePlan<kThreads> plan;
   const uint64_t W = plan_tiles<kThreads>(a.row_meta, a.rows, a.tile,
@@ -437,26 +458,46 @@ constexpr int kStage = 8;  // embedding rows staged in LDS per rescore pass
 // Reference-order chain over LDS-resident FP32 y and FP16 row (see
 // canonical_dot): same arithmetic, LDS reads issued a vector ahead.
 template <bool kMulAdd>
+__device__ __forceinline__ void chain_load(const uint4* e, const float4* y, uint32_t i,
+                                           uint4 (&ev)[2], float4 (&yv)[4]) {
+  ev[0] = e[2 * i];
+  ev[1] = e[2 * i + 1];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) yv[k] = y[4 * i + k];
+}
+template <bool kMulAdd>
+__device__ __forceinline__ float chain16(float s, const uint4 (&ev)[2], const float4 (&yv)[4]) {
+  const float yf[16] = {yv[0].x, yv[0].y, yv[0].z, yv[0].w, yv[1].x, yv[1].y, yv[1].z, yv[1].w,
+                        yv[2].x, yv[2].y, yv[2].z, yv[2].w, yv[3].x, yv[3].y, yv[3].z, yv[3].w};
+  const uint16_t* h = reinterpret_cast<const uint16_t*>(&ev[0]);
+#pragma unroll
+  for (int k = 0; k < 16; ++k) s = order_step<kMulAdd>(s, yf[k], half_to_float(h[k]));
+  return s;
+}
+
+// One candidate's score in a reference order from LDS (the same arithmetic
+// as canonical_dot).  Blocks of 16 features alternate between two register
+// sets so that block i + 1's LDS reads are in flight during block i's chain.
+template <bool kMulAdd>
 __device__ float chain_lds(const float* ys, const uint16_t* row, uint32_t H) {
   float s = 0.0f;
   uint32_t f = 0;
-  if ((H & 7u) == 0) {
+  if ((H & 31u) == 0 && (reinterpret_cast<uintptr_t>(row) & 15u) == 0) {
     const uint4* e = reinterpret_cast<const uint4*>(row);
     const float4* y = reinterpret_cast<const float4*>(ys);
-    const uint32_t n8 = H / 8;
-    uint4 ce = e[0];
-    float4 cy0 = y[0], cy1 = y[1];
-    for (uint32_t i = 0; i < n8; ++i) {
-      const uint32_t j = i + 1 < n8 ? i + 1 : i;
-      const uint4 ne = e[j];
-      const float4 ny0 = y[2 * j], ny1 = y[2 * j + 1];
-      const float yv[8] = {cy0.x, cy0.y, cy0.z, cy0.w, cy1.x, cy1.y, cy1.z, cy1.w};
-      const uint16_t* h = reinterpret_cast<const uint16_t*>(&ce);
-#pragma unroll
-      for (int k = 0; k < 8; ++k) s = order_step<kMulAdd>(s, yv[k], half_to_float(h[k]));
-      ce = ne;
-      cy0 = ny0;
-      cy1 = ny1;
+    const uint32_t n16 = H / 16;  // even
+    uint4 ea[2], eb[2];
+    float4 ya[4], yb[4];
+    chain_load<kMulAdd>(e, y, 0, ea, ya);
+    for (uint32_t i = 0; i < n16; i += 2) {
+      chain_load<kMulAdd>(e, y, i + 1, eb, yb);
+      __builtin_amdgcn_sched_barrier(0);
+      s = chain16<kMulAdd>(s, ea, ya);
+      __builtin_amdgcn_sched_barrier(0);
+      chain_load<kMulAdd>(e, y, i + 2 < n16 ? i + 2 : i, ea, ya);
+      __builtin_amdgcn_sched_barrier(0);
+      s = chain16<kMulAdd>(s, eb, yb);
+      __builtin_amdgcn_sched_barrier(0);
     }
     f = H;
   }
@@ -527,7 +568,7 @@ __device__ Best rescore_candidates(const FinalizeArgs& a, const float* ys, uint1
 }
 
 __global__ __launch_bounds__(kWave) void finalize_kernel(FinalizeArgs a) {
-  extern __shared__ float lds[];
+  extern __shared__ __align__(16) float lds[];
   float* ys = lds;                                            // H floats
   uint16_t* es = reinterpret_cast<uint16_t*>(lds + a.H);      // kStage rows
   __shared__ FinalizeShared sh;
@@ -568,16 +609,27 @@ __global__ __launch_bounds__(kWave) void finalize_kernel(FinalizeArgs a) {
   float lg = -__builtin_huge_valf();
   uint32_t mt = kInvalidToken;
   uint32_t mp = 0u;
-  // headers (the first 16 bytes: best_lower, flags, min_token, min_pos) of
-  // kRecBlock tiles per lane are loaded before any is used, so a row with
-  // many tiles (an MFMA-head row has V / 128) costs one round trip per block
+  // Per tile the header (best_lower, flags, min_token, min_pos), the counts
+  // (begin, count, n_members) and the first member, kRecBlock tiles per lane
+  // loaded before any is used: one round trip per block.  A row of at most
+  // kWave kRecBlock tiles (every gather row up to 16384 candidates, every
+  // MFMA-head row up to 49152 tokens) keeps them in registers for the
+  // member collection below.
+  const bool resident = ntiles <= kWave * kRecBlock;
+  uint4 h[kRecBlock];
+  uint4 c[kRecBlock];
+  TileMember m0[kRecBlock];
   for (uint32_t base = 0; base < ntiles; base += kWave * kRecBlock) {
-    uint4 h[kRecBlock];
 #pragma unroll
     for (uint32_t u = 0; u < kRecBlock; ++u) {
       const uint32_t t = base + u * kWave + lane;
-      h[u] = t < ntiles ? *reinterpret_cast<const uint4*>(&recs[t])
-                        : uint4{__float_as_uint(-__builtin_huge_valf()), 0u, kInvalidToken, 0u};
+      const bool in = t < ntiles;
+      // past the row's tiles: an empty ordinary tile (no members, lowest
+      // bound, no token)
+      h[u] = in ? *reinterpret_cast<const uint4*>(&recs[t])
+                : uint4{__float_as_uint(-__builtin_huge_valf()), 0u, kInvalidToken, 0u};
+      c[u] = in ? *reinterpret_cast<const uint4*>(&recs[t].begin) : uint4{0u, 0u, 0u, 0u};
+      m0[u] = in ? recs[t].m[0] : TileMember{0u, 0u, 0.0f, -__builtin_huge_valf()};
     }
 #pragma unroll
     for (uint32_t u = 0; u < kRecBlock; ++u) {
@@ -637,23 +689,23 @@ __global__ __launch_bounds__(kWave) void finalize_kernel(FinalizeArgs a) {
   __syncthreads();
   uint32_t overflow = 0u;
   for (uint32_t base = 0; base < ntiles; base += kWave * kRecBlock) {
-    // flags / member counts and the first member of kRecBlock tiles per lane
-    // in one round trip; the (rare) further members are read afterwards
-    uint4 h[kRecBlock];
-    uint4 c[kRecBlock];
-    TileMember m0[kRecBlock];
+    // a row with more blocks reloads each block's flags, member counts and
+    // first member (one round trip); the (rare) further members are read
+    // afterwards
+    if (!resident) {
 #pragma unroll
-    for (uint32_t u = 0; u < kRecBlock; ++u) {
-      const uint32_t t = base + u * kWave + lane;
-      const bool in = t < ntiles;
-      h[u] = in ? *reinterpret_cast<const uint4*>(&recs[t]) : uint4{0u, kTileInvalid, 0u, 0u};
-      c[u] = in ? *reinterpret_cast<const uint4*>(&recs[t].begin) : uint4{0u, 0u, 0u, 0u};
-      m0[u] = in ? recs[t].m[0] : TileMember{0u, 0u, 0.0f, -__builtin_huge_valf()};
+      for (uint32_t u = 0; u < kRecBlock; ++u) {
+        const uint32_t t = base + u * kWave + lane;
+        const bool in = t < ntiles;
+        h[u] = in ? *reinterpret_cast<const uint4*>(&recs[t]) : uint4{0u, kTileInvalid, 0u, 0u};
+        c[u] = in ? *reinterpret_cast<const uint4*>(&recs[t].begin) : uint4{0u, 0u, 0u, 0u};
+        m0[u] = in ? recs[t].m[0] : TileMember{0u, 0u, 0.0f, -__builtin_huge_valf()};
+      }
     }
 #pragma unroll
     for (uint32_t u = 0; u < kRecBlock; ++u) {
-      if (h[u].y != 0u) continue;
       const uint32_t t = base + u * kWave + lane;
+      if (h[u].y != 0u || t >= ntiles) continue;
       const uint32_t nm = c[u].z < kTileMembers ? c[u].z : kTileMembers;
       for (uint32_t j = 0; j < nm; ++j) {
         const TileMember mm = j == 0 ? m0[u] : recs[t].m[j];
@@ -747,7 +799,7 @@ __global__ __launch_bounds__(kWave) void finalize_kernel(FinalizeArgs a) {
 } // namespace
 
 hipError_t launch_tail_norm(const TailNormArgs& args, hipStream_t stream) {
-  const size_t lds = 2u * static_cast<size_t>(args.H) * sizeof(float);
+  const size_t lds = (args.weight != nullptr ? 3u : 2u) * static_cast<size_t>(args.H) * sizeof(float);
   const uint32_t slots = args.fb_panel != nullptr ? args.fb_m : 0u;
   hipLaunchKernelGGL(tail_norm_kernel, dim3(args.rows + slots), dim3(kWave), lds, stream, args);
   return hipGetLastError();
