@@ -72,7 +72,12 @@ def algorithmic_bytes(w) -> dict:
 
 def time_loop(tail, stages, steps, warmup, copies):
     """Runs `steps` steps (after `warmup`), bracketed by synchronization.
-    Returns wall ms per step and, per stage, the summed HIP-event time."""
+    Returns the HIP-event ms per step (two events around the whole loop),
+    the wall ms per step and, with more than one stage, each stage's mean
+    and median ms from events recorded between the stages (those per-stage
+    events are only recorded for multi-stage loops: an event record costs
+    a few microseconds of stream time, which would inflate a one-stage
+    step)."""
     import torch
     from market_sim_amd import abi, ops
 
@@ -87,8 +92,9 @@ def time_loop(tail, stages, steps, warmup, copies):
         for st in stages:
             abi.check(st, fns[st](args[i % copies], handle))
     torch.cuda.synchronize()
+    staged = len(stages) > 1
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(stages) + 1)]
-          for _ in range(steps)]
+          for _ in range(steps)] if staged else None
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -96,14 +102,18 @@ def time_loop(tail, stages, steps, warmup, copies):
     start.record(s)
     for i in range(steps):
         a = args[i % copies]
-        ev[i][0].record(s)
+        if staged:
+            ev[i][0].record(s)
         for j, st in enumerate(stages):
             abi.check(st, fns[st](a, handle))
-            ev[i][j + 1].record(s)
+            if staged:
+                ev[i][j + 1].record(s)
     stop.record(s)
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) * 1e3 / steps
     total_ms = start.elapsed_time(stop) / steps
+    if not staged:
+        return total_ms, wall, {}
     per_stage = {st: [] for st in stages}
     for i in range(steps):
         for j, st in enumerate(stages):
@@ -115,8 +125,8 @@ def time_loop(tail, stages, steps, warmup, copies):
 def kernel_loop(tail, stage, launches, copies):
     """Average duration of one stage's kernel: `launches` back-to-back launches
     (rotating table copies) between two HIP events on the launch stream.  The
-    stage must be idempotent given the prepare stage's outputs (the restricted
-    gather is: it reads the normalized rows and writes tile records)."""
+    stage must be idempotent given the prepare stage's outputs (both heads
+    are: they read the normalized rows and write tile records)."""
     import torch
     from market_sim_amd import abi, ops
     fns = {"restricted": ops.decode_tail_restricted, "unrestricted": ops.decode_tail_unrestricted}

@@ -677,7 +677,7 @@ mf_status decode_tail_stage(const mf_decode_tail_args* args, uintptr_t stream, S
         g.y_lo = reinterpret_cast<const uint16_t*>(ws + L.y_lo);
         g.row_norm = reinterpret_cast<const float*>(ws + L.row_norm);
         mfma_bound_coefs(a->hidden, g.coef, g.coef2);
-        e = mf::launch_gather(ScoreSource::kMfma, g, s);
+        e = mf::launch_gather_mfma(g, s);
       } else {
         g.coef = dot_bound_coef(a->hidden);
         e = mf::launch_gather(ScoreSource::kDotF32, g, s);

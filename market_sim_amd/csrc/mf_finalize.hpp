@@ -1,0 +1,374 @@
+// Per-row finalize of the decode tail, run by ONE wave: merges the row's
+// tile records, rescores the window survivors in the reference order,
+// selects with the reference rule (greedy.cu:84-100, 177-211) and advances
+// the DFA.  Every synchronization inside is a wave barrier, so the same code
+// serves the one-wave finalize kernel and any wave of a larger workgroup (the
+// restricted gather finalizes a row in the wave that writes its last tile
+// record).  LDS scratch comes in through FinalizeLds.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "mf_device.hpp"
+#include "mf_launch.hpp"
+
+namespace mf {
+
+// LDS writes of this wave are visible to every lane of the wave afterwards.
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+struct FinalizeWords {
+  uint32_t n_cand;
+  uint32_t token;
+  uint32_t pos;
+  float score;
+  uint32_t need_score;
+};
+
+// One wave's finalize scratch.  cand_max must be a multiple of
+// 2 kTileMembers; stage_rows >= 1.
+struct FinalizeLds {
+  float* ys;            // [H] the row's normalized hidden vector
+  uint16_t* es;         // [stage_rows][H] embedding rows being rescored
+  uint32_t stage_rows;
+  uint32_t* cand_token; // [cand_max]
+  uint32_t* cand_pos;   // [cand_max]
+  uint32_t cand_max;
+  FinalizeWords* w;
+};
+
+// Reference-order chain over LDS-resident FP32 y and FP16 row (the same
+// arithmetic as canonical_dot), LDS reads issued a vector ahead.
+template <bool kMulAdd>
+__device__ __forceinline__ void chain_load(const uint4* e, const float4* y, uint32_t i,
+                                           uint4 (&ev)[2], float4 (&yv)[4]) {
+  ev[0] = e[2 * i];
+  ev[1] = e[2 * i + 1];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) yv[k] = y[4 * i + k];
+}
+template <bool kMulAdd>
+__device__ __forceinline__ float chain16(float s, const uint4 (&ev)[2], const float4 (&yv)[4]) {
+  const float yf[16] = {yv[0].x, yv[0].y, yv[0].z, yv[0].w, yv[1].x, yv[1].y, yv[1].z, yv[1].w,
+                        yv[2].x, yv[2].y, yv[2].z, yv[2].w, yv[3].x, yv[3].y, yv[3].z, yv[3].w};
+  const uint16_t* h = reinterpret_cast<const uint16_t*>(&ev[0]);
+#pragma unroll
+  for (int k = 0; k < 16; ++k) s = order_step<kMulAdd>(s, yf[k], half_to_float(h[k]));
+  return s;
+}
+
+// One candidate's score in a reference order from LDS.  Blocks of 16
+// features alternate between two register sets so that block i + 1's LDS
+// reads are in flight during block i's chain.
+template <bool kMulAdd>
+__device__ float chain_lds(const float* ys, const uint16_t* row, uint32_t H) {
+  float s = 0.0f;
+  uint32_t f = 0;
+  if ((H & 31u) == 0 && (reinterpret_cast<uintptr_t>(row) & 15u) == 0 &&
+      (reinterpret_cast<uintptr_t>(ys) & 15u) == 0) {
+    const uint4* e = reinterpret_cast<const uint4*>(row);
+    const float4* y = reinterpret_cast<const float4*>(ys);
+    const uint32_t n16 = H / 16;  // even
+    uint4 ea[2], eb[2];
+    float4 ya[4], yb[4];
+    chain_load<kMulAdd>(e, y, 0, ea, ya);
+    for (uint32_t i = 0; i < n16; i += 2) {
+      chain_load<kMulAdd>(e, y, i + 1, eb, yb);
+      __builtin_amdgcn_sched_barrier(0);
+      s = chain16<kMulAdd>(s, ea, ya);
+      __builtin_amdgcn_sched_barrier(0);
+      chain_load<kMulAdd>(e, y, i + 2 < n16 ? i + 2 : i, ea, ya);
+      __builtin_amdgcn_sched_barrier(0);
+      s = chain16<kMulAdd>(s, eb, yb);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    f = H;
+  }
+  for (; f < H; ++f) s = order_step<kMulAdd>(s, ys[f], half_to_float(row[f]));
+  return s;
+}
+
+// Rescores candidates cand_token[0..n) of one row in the reference order,
+// stage_rows rows at a time staged in LDS; returns the wave's best.
+__device__ inline Best rescore_candidates(const FinalizeArgs& a, const FinalizeLds& L,
+                                          uint32_t n) {
+  const uint32_t lane = threadIdx.x % kWave;
+  const uint32_t H = a.H;
+  Best best = best_identity();
+  for (uint32_t base = 0; base < n; base += L.stage_rows) {
+    const uint32_t m = n - base < L.stage_rows ? n - base : L.stage_rows;
+    wave_sync();
+    if ((H & 7u) == 0) {
+      // every row's pieces in flight before their stores
+      constexpr uint32_t kBatch = 10;
+      const uint32_t per = H / 8;
+      const uint32_t total = m * per;
+      for (uint32_t q0 = lane; q0 < total; q0 += kWave * kBatch) {
+        uint4 v[kBatch];
+#pragma unroll
+        for (uint32_t u = 0; u < kBatch; ++u) {
+          const uint32_t q = q0 + u * kWave;
+          const uint32_t j = q / per;
+          v[u] = q < total
+                     ? reinterpret_cast<const uint4*>(
+                           a.emb + static_cast<uint64_t>(L.cand_token[base + j]) * H)[q % per]
+                     : uint4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < kBatch; ++u) {
+          const uint32_t q = q0 + u * kWave;
+          if (q < total) reinterpret_cast<uint4*>(L.es + (q / per) * H)[q % per] = v[u];
+        }
+      }
+    } else {
+      for (uint32_t q = lane; q < m * H; q += kWave) {
+        const uint32_t j = q / H;
+        L.es[q] = a.emb[static_cast<uint64_t>(L.cand_token[base + j]) * H + (q % H)];
+      }
+    }
+    wave_sync();
+    if (lane < m) {
+      const float s = a.order == 1 ? chain_lds<true>(L.ys, L.es + lane * H, H)
+                                   : chain_lds<false>(L.ys, L.es + lane * H, H);
+      best = best_of(best, best_leaf(s, L.cand_token[base + lane], L.cand_pos[base + lane]));
+    }
+  }
+  return wave_best(best);
+}
+
+// Adds the members of ordinary tile t (upper >= lg) to the candidate buffer.
+// Returns 1 if the buffer had no room for one of them.
+__device__ __forceinline__ uint32_t collect_members(const TileRecord* recs, uint32_t t,
+                                                    uint32_t n_members, const TileMember& first,
+                                                    float lg, const FinalizeLds& L) {
+  uint32_t overflow = 0u;
+  const uint32_t nm = n_members < kTileMembers ? n_members : kTileMembers;
+  for (uint32_t j = 0; j < nm; ++j) {
+    const TileMember mm = j == 0 ? first : recs[t].m[j];
+    if (mm.upper >= lg) {
+      const uint32_t slot = atomicAdd(&L.w->n_cand, 1u);
+      if (slot < L.cand_max) {
+        L.cand_token[slot] = mm.token;
+        L.cand_pos[slot] = mm.pos;
+      } else {
+        overflow = 1u;
+      }
+    }
+  }
+  return overflow;
+}
+
+// Finalizes row r (meta = its metadata) with one wave.  ys_ready: L.ys
+// already holds the row's normalized hidden vector (otherwise it is loaded
+// from a.y).  Writes token, score and next state of the row; rows that are
+// neither gathered nor served by the MFMA head are left alone (their outputs
+// were preset by the norm kernel).
+__device__ inline void finalize_row(const FinalizeArgs& a, uint32_t r, const RowMeta& meta,
+                                    const FinalizeLds& L, bool ys_ready) {
+  const uint32_t lane = threadIdx.x % kWave;
+  const TileRecord* recs;
+  uint32_t ntiles;
+  if (meta.kind & kRowRestricted) {
+    recs = a.records + static_cast<uint64_t>(r) * a.max_tiles;
+    ntiles = (meta.count + a.tile - 1) / a.tile;
+  } else if ((meta.kind & kRowUnrestricted) && a.fb_records != nullptr) {
+    const uint32_t m = a.fb_map[r];
+    if (m == kInvalidToken) return;
+    recs = a.fb_records + static_cast<uint64_t>(m) * a.fb_tiles;
+    ntiles = a.fb_tiles;
+  } else if ((meta.kind & kRowUnrestricted) && a.lookup_unrestricted) {
+    recs = a.records + static_cast<uint64_t>(r) * a.max_tiles;
+    ntiles = (meta.count + a.tile - 1) / a.tile;
+  } else {
+    return;
+  }
+  if (!ys_ready) {
+    if ((a.H & 3u) == 0) {
+      copy16_to_lds<4>(reinterpret_cast<uint4*>(L.ys),
+                       reinterpret_cast<const uint4*>(a.y + static_cast<uint64_t>(r) * a.H),
+                       a.H / 4, lane, kWave);
+    } else {
+      for (uint32_t f = lane; f < a.H; f += kWave) L.ys[f] = a.y[static_cast<uint64_t>(r) * a.H + f];
+    }
+  }
+  const bool virtual_list = meta.kind & kRowUnrestricted;
+  wave_sync();
+  // pass 1: validity, the best lower bound of ordinary tiles, lowest id.
+  // Per tile the header (best_lower, flags, min_token, min_pos), the counts
+  // (begin, count, n_members) and the first member, kRecBlock tiles per lane
+  // loaded before any is used: one round trip per block.  A row of at most
+  // kWave kRecBlock tiles keeps them in registers for the member collection.
+  constexpr uint32_t kRecBlock = 4;
+  uint32_t inv = 0u;
+  uint32_t any_all = 0u;
+  float lg = -__builtin_huge_valf();
+  uint32_t mt = kInvalidToken;
+  uint32_t mp = 0u;
+  const bool resident = ntiles <= kWave * kRecBlock;
+  uint4 h[kRecBlock];
+  uint4 c[kRecBlock];
+  TileMember m0[kRecBlock];
+  for (uint32_t base = 0; base < ntiles; base += kWave * kRecBlock) {
+#pragma unroll
+    for (uint32_t u = 0; u < kRecBlock; ++u) {
+      const uint32_t t = base + u * kWave + lane;
+      const bool in = t < ntiles;
+      // past the row's tiles: an empty ordinary tile (no members, lowest
+      // bound, no token)
+      h[u] = in ? *reinterpret_cast<const uint4*>(&recs[t])
+                : uint4{__float_as_uint(-__builtin_huge_valf()), 0u, kInvalidToken, 0u};
+      c[u] = in ? *reinterpret_cast<const uint4*>(&recs[t].begin) : uint4{0u, 0u, 0u, 0u};
+      m0[u] = in ? recs[t].m[0] : TileMember{0u, 0u, 0.0f, -__builtin_huge_valf()};
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < kRecBlock; ++u) {
+      const uint32_t flags = h[u].y;
+      inv |= (flags & kTileInvalid) ? 1u : 0u;
+      any_all |= (flags & kTileRescoreAll) ? 1u : 0u;
+      if (flags == 0u) lg = __builtin_fmaxf(lg, __uint_as_float(h[u].x));
+      if (h[u].z < mt) {
+        mt = h[u].z;
+        mp = h[u].w;
+      }
+    }
+  }
+  const bool invalid = wave_sum_u32(inv) != 0u;
+  if (invalid) {
+    // an id outside the vocabulary makes the row invalid (greedy.cu:163-166)
+    if (lane == 0) {
+      a.out_token[r] = kInvalidToken;
+      if (a.out_score != nullptr) a.out_score[r] = __builtin_nanf("");
+      if (a.out_next != nullptr) a.out_next[r] = kInvalidToken;
+    }
+    return;
+  }
+  const bool has_all = wave_sum_u32(any_all) != 0u;
+  lg = wave_max(lg);
+  wave_min_token(mt, mp);
+
+  // tiles that need every candidate rescored (non-finite values, crowded
+  // windows): exact scores, which then also bound the window
+  Best best = best_identity();
+  if (has_all) {
+    for (uint32_t t = 0; t < ntiles; ++t) {
+      const TileRecord& q = recs[t];
+      if (!(q.flags & kTileRescoreAll)) continue;
+      const uint32_t chunk = L.cand_max < kWave ? L.cand_max : kWave;
+      for (uint32_t c0 = 0; c0 < q.count; c0 += chunk) {
+        const uint32_t n = q.count - c0 < chunk ? q.count - c0 : chunk;
+        wave_sync();
+        if (lane < n) {
+          const uint32_t p = q.begin + c0 + lane;
+          L.cand_token[lane] = virtual_list ? p : a.tokens[meta.list_begin + p];
+          L.cand_pos[lane] = p;
+        }
+        best = best_of(best, rescore_candidates(a, L, n));
+      }
+    }
+    if (best.token != kInvalidToken) lg = __builtin_fmaxf(lg, best.score);
+  }
+
+  // ordinary tiles: members whose upper bound reaches lg (at most
+  // kTileMembers per tile), collected over all tiles without a barrier per
+  // sweep, then rescored together.  If the buffer would overflow, the
+  // collection is redone below in flushed sweeps.
+  wave_sync();
+  if (lane == 0) L.w->n_cand = 0u;
+  wave_sync();
+  uint32_t overflow = 0u;
+  for (uint32_t base = 0; base < ntiles; base += kWave * kRecBlock) {
+    // a row with more blocks reloads each block's flags, member counts and
+    // first member (one round trip); the (rare) further members are read
+    // afterwards
+    if (!resident) {
+#pragma unroll
+      for (uint32_t u = 0; u < kRecBlock; ++u) {
+        const uint32_t t = base + u * kWave + lane;
+        const bool in = t < ntiles;
+        h[u] = in ? *reinterpret_cast<const uint4*>(&recs[t]) : uint4{0u, kTileInvalid, 0u, 0u};
+        c[u] = in ? *reinterpret_cast<const uint4*>(&recs[t].begin) : uint4{0u, 0u, 0u, 0u};
+        m0[u] = in ? recs[t].m[0] : TileMember{0u, 0u, 0.0f, -__builtin_huge_valf()};
+      }
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < kRecBlock; ++u) {
+      const uint32_t t = base + u * kWave + lane;
+      if (h[u].y != 0u || t >= ntiles) continue;
+      overflow |= collect_members(recs, t, c[u].z, m0[u], lg, L);
+    }
+  }
+  wave_sync();
+  if (wave_sum_u32(overflow) == 0u) {
+    const uint32_t nc = L.w->n_cand;
+    if (nc > 0) best = best_of(best, rescore_candidates(a, L, nc));
+  } else {
+    // flushed sweeps: a sweep of sw tiles adds at most sw kTileMembers =
+    // cand_max / 2 candidates, so flushing above half keeps the buffer
+    // within its size
+    const uint32_t sw = L.cand_max / (2u * kTileMembers);
+    wave_sync();
+    if (lane == 0) L.w->n_cand = 0u;
+    wave_sync();
+    for (uint32_t t0 = 0; t0 < ntiles; t0 += sw) {
+      const uint32_t t = t0 + lane;
+      if (lane < sw && t < ntiles) {
+        const TileRecord& q = recs[t];
+        if (q.flags == 0u) collect_members(recs, t, q.n_members, q.m[0], lg, L);
+      }
+      wave_sync();
+      const uint32_t nc = L.w->n_cand;
+      // flush when the next sweep could overflow the buffer, and at the end
+      if (nc > 0 && (nc > L.cand_max / 2u || t0 + sw >= ntiles)) {
+        best = best_of(best, rescore_candidates(a, L, nc));
+        wave_sync();
+        if (lane == 0) L.w->n_cand = 0u;
+        wave_sync();
+      }
+    }
+  }
+
+  if (lane == 0) {
+    L.w->need_score = best.token == kInvalidToken ? 1u : 0u;
+    L.w->token = L.w->need_score ? mt : best.token;
+    L.w->pos = L.w->need_score ? mp : best.pos;
+    L.w->score = best.score;
+  }
+  wave_sync();
+  // a row whose scores are all NaN selects its lowest id (greedy.cu:206-211)
+  // and reports that id's reference-order score
+  const uint32_t token = L.w->token;
+  const uint32_t pos = L.w->pos;
+  float score = L.w->score;
+  if (L.w->need_score) {
+    const uint32_t H = a.H;
+    if ((H & 7u) == 0) {
+      copy16_to_lds<2>(reinterpret_cast<uint4*>(L.es),
+                       reinterpret_cast<const uint4*>(a.emb + static_cast<uint64_t>(token) * H),
+                       H / 8, lane, kWave);
+    } else {
+      for (uint32_t q = lane; q < H; q += kWave) L.es[q] = a.emb[static_cast<uint64_t>(token) * H + q];
+    }
+    wave_sync();
+    score = a.order == 1 ? chain_lds<true>(L.ys, L.es, H) : chain_lds<false>(L.ys, L.es, H);
+  }
+  if (lane == 0) {
+    uint32_t next = kInvalidToken;
+    if (virtual_list) {
+      next = kStateUnrestricted;
+    } else if (a.state_next != nullptr) {
+      next = a.state_next[meta.list_begin + pos];
+    } else if (a.next_table != nullptr) {
+      next = static_cast<uint32_t>(a.next_table[static_cast<uint64_t>(meta.state) * a.V + token]);
+    }
+    a.out_token[r] = token;
+    if (a.out_score != nullptr) a.out_score[r] = score;
+    if (a.out_next != nullptr) a.out_next[r] = next;
+  }
+  wave_sync();
+}
+
+}  // namespace mf

@@ -271,12 +271,12 @@ __global__ __launch_bounds__(kWave) void gather_mfma_grid_kernel(GatherArgs a) {
 template <int KC>
 hipError_t launch_variant(const GatherArgs& a, hipStream_t stream) {
   if (a.rows <= kPlanRowsMax && a.groups > 0) {
+    const uint32_t lds = kWaves * 4u * a.H;
     static int resident = 0;
     if (resident == 0) {
       int n = 0;
       if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-              &n, reinterpret_cast<const void*>(gather_mfma_kernel<KC>), kThreads,
-              kWaves * 4u * a.H) !=
+              &n, reinterpret_cast<const void*>(gather_mfma_kernel<KC>), kThreads, lds) !=
               hipSuccess ||
           n <= 0) {
         n = 2;
@@ -284,14 +284,13 @@ hipError_t launch_variant(const GatherArgs& a, hipStream_t stream) {
       resident = n;
     }
     const uint32_t g = a.groups * static_cast<uint32_t>(resident);
-    hipLaunchKernelGGL((gather_mfma_kernel<KC>), dim3(g), dim3(kThreads), kWaves * 4u * a.H,
-                       stream, a);
-  } else {
-    const uint64_t slots = static_cast<uint64_t>(a.rows) * a.max_tiles;
-    if (slots > 0x7FFFFFFFull) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((gather_mfma_grid_kernel<KC>), dim3(static_cast<uint32_t>(slots)),
-                       dim3(kWave), 4u * a.H, stream, a);
+    hipLaunchKernelGGL((gather_mfma_kernel<KC>), dim3(g), dim3(kThreads), lds, stream, a);
+    return hipGetLastError();
   }
+  const uint64_t slots = static_cast<uint64_t>(a.rows) * a.max_tiles;
+  if (slots > 0x7FFFFFFFull) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((gather_mfma_grid_kernel<KC>), dim3(static_cast<uint32_t>(slots)),
+                     dim3(kWave), 4u * a.H, stream, a);
   return hipGetLastError();
 }
 

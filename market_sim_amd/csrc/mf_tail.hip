@@ -22,6 +22,7 @@
 
 #include "mf_device.hpp"
 #include "mf_launch.hpp"
+#include "mf_finalize.hpp"
 #include "mf_plan.hpp"
 
 namespace mf {
@@ -450,350 +451,33 @@ __global__ __launch_bounds__(kThreads) void gather_planned_kernel(GatherArgs a) 
 }
 
 // ---------------------------------------------------------------------------
-// K3: finalize
+// K3: finalize (one wave per row; the per-row work is finalize_row in
+// mf_finalize.hpp)
 // ---------------------------------------------------------------------------
 
-constexpr int kStage = 8;  // embedding rows staged in LDS per rescore pass
-
-// Reference-order chain over LDS-resident FP32 y and FP16 row (see
-// canonical_dot): same arithmetic, LDS reads issued a vector ahead.
-template <bool kMulAdd>
-__device__ __forceinline__ void chain_load(const uint4* e, const float4* y, uint32_t i,
-                                           uint4 (&ev)[2], float4 (&yv)[4]) {
-  ev[0] = e[2 * i];
-  ev[1] = e[2 * i + 1];
-#pragma unroll
-  for (int k = 0; k < 4; ++k) yv[k] = y[4 * i + k];
-}
-template <bool kMulAdd>
-__device__ __forceinline__ float chain16(float s, const uint4 (&ev)[2], const float4 (&yv)[4]) {
-  const float yf[16] = {yv[0].x, yv[0].y, yv[0].z, yv[0].w, yv[1].x, yv[1].y, yv[1].z, yv[1].w,
-                        yv[2].x, yv[2].y, yv[2].z, yv[2].w, yv[3].x, yv[3].y, yv[3].z, yv[3].w};
-  const uint16_t* h = reinterpret_cast<const uint16_t*>(&ev[0]);
-#pragma unroll
-  for (int k = 0; k < 16; ++k) s = order_step<kMulAdd>(s, yf[k], half_to_float(h[k]));
-  return s;
-}
-
-// One candidate's score in a reference order from LDS (the same arithmetic
-// as canonical_dot).  Blocks of 16 features alternate between two register
-// sets so that block i + 1's LDS reads are in flight during block i's chain.
-template <bool kMulAdd>
-__device__ float chain_lds(const float* ys, const uint16_t* row, uint32_t H) {
-  float s = 0.0f;
-  uint32_t f = 0;
-  if ((H & 31u) == 0 && (reinterpret_cast<uintptr_t>(row) & 15u) == 0) {
-    const uint4* e = reinterpret_cast<const uint4*>(row);
-    const float4* y = reinterpret_cast<const float4*>(ys);
-    const uint32_t n16 = H / 16;  // even
-    uint4 ea[2], eb[2];
-    float4 ya[4], yb[4];
-    chain_load<kMulAdd>(e, y, 0, ea, ya);
-    for (uint32_t i = 0; i < n16; i += 2) {
-      chain_load<kMulAdd>(e, y, i + 1, eb, yb);
-      __builtin_amdgcn_sched_barrier(0);
-      s = chain16<kMulAdd>(s, ea, ya);
-      __builtin_amdgcn_sched_barrier(0);
-      chain_load<kMulAdd>(e, y, i + 2 < n16 ? i + 2 : i, ea, ya);
-      __builtin_amdgcn_sched_barrier(0);
-      s = chain16<kMulAdd>(s, eb, yb);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    f = H;
-  }
-  for (; f < H; ++f) s = order_step<kMulAdd>(s, ys[f], half_to_float(row[f]));
-  return s;
-}
-
+constexpr uint32_t kStage = 8;  // embedding rows staged in LDS per rescore pass
 constexpr uint32_t kCandMax = 2 * kWave * kTileMembers;
-constexpr uint32_t kRecBlock = 4;  // tile records per lane loaded together
-
-struct FinalizeShared {
-  uint32_t cand_token[kCandMax];
-  uint32_t cand_pos[kCandMax];
-  uint32_t n_cand;
-  uint32_t token;
-  uint32_t pos;
-  float score;
-  uint32_t need_score;
-};
-
-// Rescores candidates cand_token[0..n) of one row in the reference order,
-// kStage rows at a time staged in LDS; returns the wave's best.
-__device__ Best rescore_candidates(const FinalizeArgs& a, const float* ys, uint16_t* es,
-                                   const FinalizeShared& sh, uint32_t n) {
-  const uint32_t lane = threadIdx.x;
-  const uint32_t H = a.H;
-  Best best = best_identity();
-  for (uint32_t base = 0; base < n; base += kStage) {
-    const uint32_t m = n - base < kStage ? n - base : kStage;
-    __syncthreads();
-    if ((H & 7u) == 0) {
-      // every row's pieces in flight before their stores (kStage rows of
-      // H / 8 pieces over 64 lanes)
-      constexpr uint32_t kBatch = 10;
-      const uint32_t per = H / 8;
-      const uint32_t total = m * per;
-      for (uint32_t q0 = lane; q0 < total; q0 += kWave * kBatch) {
-        uint4 v[kBatch];
-#pragma unroll
-        for (uint32_t u = 0; u < kBatch; ++u) {
-          const uint32_t q = q0 + u * kWave;
-          const uint32_t j = q / per;
-          v[u] = q < total
-                     ? reinterpret_cast<const uint4*>(
-                           a.emb + static_cast<uint64_t>(sh.cand_token[base + j]) * H)[q % per]
-                     : uint4{0u, 0u, 0u, 0u};
-        }
-#pragma unroll
-        for (uint32_t u = 0; u < kBatch; ++u) {
-          const uint32_t q = q0 + u * kWave;
-          if (q < total) reinterpret_cast<uint4*>(es + (q / per) * H)[q % per] = v[u];
-        }
-      }
-    } else {
-      for (uint32_t q = lane; q < m * H; q += kWave) {
-        const uint32_t j = q / H;
-        es[q] = a.emb[static_cast<uint64_t>(sh.cand_token[base + j]) * H + (q % H)];
-      }
-    }
-    __syncthreads();
-    if (lane < m) {
-      const float s = a.order == 1 ? chain_lds<true>(ys, es + lane * H, H)
-                                   : chain_lds<false>(ys, es + lane * H, H);
-      best = best_of(best, best_leaf(s, sh.cand_token[base + lane], sh.cand_pos[base + lane]));
-    }
-  }
-  return wave_best(best);
-}
 
 __global__ __launch_bounds__(kWave) void finalize_kernel(FinalizeArgs a) {
   extern __shared__ __align__(16) float lds[];
-  float* ys = lds;                                            // H floats
-  uint16_t* es = reinterpret_cast<uint16_t*>(lds + a.H);      // kStage rows
-  __shared__ FinalizeShared sh;
+  __shared__ uint32_t cand_token[kCandMax];
+  __shared__ uint32_t cand_pos[kCandMax];
+  __shared__ FinalizeWords words;
+  const FinalizeLds L{lds, reinterpret_cast<uint16_t*>(lds + a.H), kStage, cand_token, cand_pos,
+                      kCandMax, &words};
   const uint32_t r = blockIdx.x;
   const uint32_t lane = threadIdx.x;
-  // the loads that need nothing else go first: the row's hidden vector, its
-  // metadata and its MFMA-head slot
+  // the loads that need nothing else go first: the row's hidden vector, then
+  // its metadata
   if ((a.H & 3u) == 0) {
-    copy16_to_lds<4>(reinterpret_cast<uint4*>(ys),
+    copy16_to_lds<4>(reinterpret_cast<uint4*>(L.ys),
                      reinterpret_cast<const uint4*>(a.y + static_cast<uint64_t>(r) * a.H), a.H / 4,
                      lane, kWave);
   } else {
-    for (uint32_t f = lane; f < a.H; f += kWave) ys[f] = a.y[static_cast<uint64_t>(r) * a.H + f];
+    for (uint32_t f = lane; f < a.H; f += kWave) L.ys[f] = a.y[static_cast<uint64_t>(r) * a.H + f];
   }
   const RowMeta meta = a.row_meta[r];
-  const uint32_t fb_slot = a.fb_map != nullptr ? a.fb_map[r] : kInvalidToken;
-  const TileRecord* recs;
-  uint32_t ntiles;
-  if (meta.kind & kRowRestricted) {
-    recs = a.records + static_cast<uint64_t>(r) * a.max_tiles;
-    ntiles = (meta.count + a.tile - 1) / a.tile;
-  } else if ((meta.kind & kRowUnrestricted) && a.fb_records != nullptr) {
-    const uint32_t m = fb_slot;
-    if (m == kInvalidToken) return;
-    recs = a.fb_records + static_cast<uint64_t>(m) * a.fb_tiles;
-    ntiles = a.fb_tiles;
-  } else if ((meta.kind & kRowUnrestricted) && a.lookup_unrestricted) {
-    recs = a.records + static_cast<uint64_t>(r) * a.max_tiles;
-    ntiles = (meta.count + a.tile - 1) / a.tile;
-  } else {
-    return;
-  }
-  const bool virtual_list = meta.kind & kRowUnrestricted;
-  __syncthreads();
-  // pass 1: validity, the best lower bound of ordinary tiles, lowest id
-  uint32_t inv = 0u;
-  uint32_t any_all = 0u;
-  float lg = -__builtin_huge_valf();
-  uint32_t mt = kInvalidToken;
-  uint32_t mp = 0u;
-  // Per tile the header (best_lower, flags, min_token, min_pos), the counts
-  // (begin, count, n_members) and the first member, kRecBlock tiles per lane
-  // loaded before any is used: one round trip per block.  A row of at most
-  // kWave kRecBlock tiles (every gather row up to 16384 candidates, every
-  // MFMA-head row up to 49152 tokens) keeps them in registers for the
-  // member collection below.
-  const bool resident = ntiles <= kWave * kRecBlock;
-  uint4 h[kRecBlock];
-  uint4 c[kRecBlock];
-  TileMember m0[kRecBlock];
-  for (uint32_t base = 0; base < ntiles; base += kWave * kRecBlock) {
-#pragma unroll
-    for (uint32_t u = 0; u < kRecBlock; ++u) {
-      const uint32_t t = base + u * kWave + lane;
-      const bool in = t < ntiles;
-      // past the row's tiles: an empty ordinary tile (no members, lowest
-      // bound, no token)
-      h[u] = in ? *reinterpret_cast<const uint4*>(&recs[t])
-                : uint4{__float_as_uint(-__builtin_huge_valf()), 0u, kInvalidToken, 0u};
-      c[u] = in ? *reinterpret_cast<const uint4*>(&recs[t].begin) : uint4{0u, 0u, 0u, 0u};
-      m0[u] = in ? recs[t].m[0] : TileMember{0u, 0u, 0.0f, -__builtin_huge_valf()};
-    }
-#pragma unroll
-    for (uint32_t u = 0; u < kRecBlock; ++u) {
-      const uint32_t flags = h[u].y;
-      inv |= (flags & kTileInvalid) ? 1u : 0u;
-      any_all |= (flags & kTileRescoreAll) ? 1u : 0u;
-      if (flags == 0u) lg = __builtin_fmaxf(lg, __uint_as_float(h[u].x));
-      if (h[u].z < mt) {
-        mt = h[u].z;
-        mp = h[u].w;
-      }
-    }
-  }
-  const bool invalid = wave_sum_u32(inv) != 0u;
-  if (invalid) {
-    // an id outside the vocabulary makes the row invalid (greedy.cu:163-166)
-    if (lane == 0) {
-      a.out_token[r] = kInvalidToken;
-      if (a.out_score != nullptr) a.out_score[r] = __builtin_nanf("");
-      if (a.out_next != nullptr) a.out_next[r] = kInvalidToken;
-    }
-    return;
-  }
-  const bool has_all = wave_sum_u32(any_all) != 0u;
-  lg = wave_max(lg);
-  wave_min_token(mt, mp);
-  __syncthreads();
-
-  // tiles that need every candidate rescored (non-finite values, crowded
-  // windows): exact scores, which then also bound the window
-  Best best = best_identity();
-  if (has_all) {
-    for (uint32_t t = 0; t < ntiles; ++t) {
-      const TileRecord& q = recs[t];
-      if (!(q.flags & kTileRescoreAll)) continue;
-      for (uint32_t c0 = 0; c0 < q.count; c0 += kWave) {
-        const uint32_t c = c0 + lane;
-        if (lane == 0) sh.n_cand = q.count - c0 < kWave ? q.count - c0 : kWave;
-        if (c < q.count) {
-          const uint32_t p = q.begin + c;
-          sh.cand_token[lane] = virtual_list ? p : a.tokens[meta.list_begin + p];
-          sh.cand_pos[lane] = p;
-        }
-        __syncthreads();
-        best = best_of(best, rescore_candidates(a, ys, es, sh, sh.n_cand));
-      }
-    }
-    if (best.token != kInvalidToken) lg = __builtin_fmaxf(lg, best.score);
-  }
-
-  // ordinary tiles: members whose upper bound reaches lg (at most
-  // kTileMembers per tile), collected over all tiles without a barrier per
-  // sweep (the record loads of every sweep are in flight together), then
-  // rescored together.  If the buffer would overflow, the collection is
-  // redone below in flushed sweeps.
-  if (lane == 0) sh.n_cand = 0u;
-  __syncthreads();
-  uint32_t overflow = 0u;
-  for (uint32_t base = 0; base < ntiles; base += kWave * kRecBlock) {
-    // a row with more blocks reloads each block's flags, member counts and
-    // first member (one round trip); the (rare) further members are read
-    // afterwards
-    if (!resident) {
-#pragma unroll
-      for (uint32_t u = 0; u < kRecBlock; ++u) {
-        const uint32_t t = base + u * kWave + lane;
-        const bool in = t < ntiles;
-        h[u] = in ? *reinterpret_cast<const uint4*>(&recs[t]) : uint4{0u, kTileInvalid, 0u, 0u};
-        c[u] = in ? *reinterpret_cast<const uint4*>(&recs[t].begin) : uint4{0u, 0u, 0u, 0u};
-        m0[u] = in ? recs[t].m[0] : TileMember{0u, 0u, 0.0f, -__builtin_huge_valf()};
-      }
-    }
-#pragma unroll
-    for (uint32_t u = 0; u < kRecBlock; ++u) {
-      const uint32_t t = base + u * kWave + lane;
-      if (h[u].y != 0u || t >= ntiles) continue;
-      const uint32_t nm = c[u].z < kTileMembers ? c[u].z : kTileMembers;
-      for (uint32_t j = 0; j < nm; ++j) {
-        const TileMember mm = j == 0 ? m0[u] : recs[t].m[j];
-        if (mm.upper >= lg) {
-          const uint32_t slot = atomicAdd(&sh.n_cand, 1u);
-          if (slot < kCandMax) {
-            sh.cand_token[slot] = mm.token;
-            sh.cand_pos[slot] = mm.pos;
-          } else {
-            overflow = 1u;
-          }
-        }
-      }
-    }
-  }
-  __syncthreads();
-  if (wave_sum_u32(overflow) == 0u) {
-    const uint32_t nc = sh.n_cand;
-    if (nc > 0) best = best_of(best, rescore_candidates(a, ys, es, sh, nc));
-  } else {
-  __syncthreads();
-  if (lane == 0) sh.n_cand = 0u;
-  __syncthreads();
-  for (uint32_t t0 = 0; t0 < ntiles; t0 += kWave) {
-    const uint32_t t = t0 + lane;
-    if (t < ntiles) {
-      const TileRecord& q = recs[t];
-      if (q.flags == 0u) {
-        const uint32_t nm = q.n_members < kTileMembers ? q.n_members : kTileMembers;
-        for (uint32_t j = 0; j < nm; ++j) {
-          const TileMember mm = q.m[j];
-          if (mm.upper >= lg) {
-            const uint32_t slot = atomicAdd(&sh.n_cand, 1u);
-            sh.cand_token[slot] = mm.token;
-            sh.cand_pos[slot] = mm.pos;
-          }
-        }
-      }
-    }
-    __syncthreads();
-    const uint32_t nc = sh.n_cand;
-    // flush when the next sweep could overflow the buffer, and at the end
-    if (nc > 0 && (nc > kCandMax - kWave * kTileMembers || t0 + kWave >= ntiles)) {
-      best = best_of(best, rescore_candidates(a, ys, es, sh, nc));
-      __syncthreads();
-      if (lane == 0) sh.n_cand = 0u;
-      __syncthreads();
-    }
-  }
-  }
-
-  if (lane == 0) {
-    sh.need_score = best.token == kInvalidToken ? 1u : 0u;
-    sh.token = sh.need_score ? mt : best.token;
-    sh.pos = sh.need_score ? mp : best.pos;
-    sh.score = best.score;
-  }
-  __syncthreads();
-  // a row whose scores are all NaN selects its lowest id (greedy.cu:206-211)
-  // and reports that id's reference-order score
-  const uint32_t token = sh.token;
-  const uint32_t pos = sh.pos;
-  float score = sh.score;
-  if (sh.need_score) {
-    const uint32_t H = a.H;
-    if ((H & 7u) == 0) {
-      copy16_to_lds<2>(reinterpret_cast<uint4*>(es),
-                       reinterpret_cast<const uint4*>(a.emb + static_cast<uint64_t>(token) * H),
-                       H / 8, lane, kWave);
-    } else {
-      for (uint32_t q = lane; q < H; q += kWave) es[q] = a.emb[static_cast<uint64_t>(token) * H + q];
-    }
-    __syncthreads();
-    score = a.order == 1 ? chain_lds<true>(ys, es, H) : chain_lds<false>(ys, es, H);
-  }
-  if (lane == 0) {
-    uint32_t next = kInvalidToken;
-    if (virtual_list) {
-      next = kStateUnrestricted;
-    } else if (a.state_next != nullptr) {
-      next = a.state_next[meta.list_begin + pos];
-    } else if (a.next_table != nullptr) {
-      next = static_cast<uint32_t>(a.next_table[static_cast<uint64_t>(meta.state) * a.V + token]);
-    }
-    a.out_token[r] = token;
-    if (a.out_score != nullptr) a.out_score[r] = score;
-    if (a.out_next != nullptr) a.out_next[r] = next;
-  }
+  finalize_row(a, r, meta, L, true);
 }
 
 } // namespace
