@@ -525,7 +525,8 @@ mf_status validate_tail(const mf_decode_tail_args* a, bool full, TailLayout& L) 
       if (in != 0 && in == outs[i]) return status(MF_INVALID_ARGUMENT);
     }
   }
-  if ((a->embedding.address % 16u) != 0 || (a->x.address % 16u) != 0) {
+  if ((a->embedding.address % 16u) != 0 || (a->x.address % 16u) != 0 ||
+      (a->norm_weight.address % 16u) != 0) {
     return status(MF_INVALID_ARGUMENT);
   }
   const uint64_t rows = a->rows;
@@ -655,6 +656,23 @@ mf::FinalizeArgs finalize_args(const mf_decode_tail_args* a, const TailLayout& L
   return f;
 }
 
+mf::FallbackArgs fallback_args(const mf_decode_tail_args* a, const TailLayout& L, char* ws) {
+  mf::FallbackArgs f{};
+  f.panel = reinterpret_cast<const uint16_t*>(ws + L.fb_panel);
+  f.slot_row = reinterpret_cast<const uint32_t*>(ws + L.fb_slot_row);
+  f.slot_norm = reinterpret_cast<const float*>(ws + L.fb_slot_norm);
+  f.m = static_cast<uint32_t>(a->unrestricted_count);
+  f.emb = ptr<const uint16_t>(a->embedding.address);
+  f.H = static_cast<uint32_t>(a->hidden);
+  f.V = static_cast<uint32_t>(a->vocab);
+  f.records = reinterpret_cast<mf::TileRecord*>(ws + L.fb_records);
+  f.fb_map = reinterpret_cast<uint32_t*>(ws + L.fb_map);
+  mfma_bound_coefs(a->hidden, f.coef, f.coef2);
+  f.slack = underflow_slack(a->hidden);
+  f.groups = device_cus();
+  return f;
+}
+
 mf_status decode_tail_stage(const mf_decode_tail_args* args, uintptr_t stream, Stage stage) {
   if (stream == 0) return status(MF_INVALID_ARGUMENT);
   TailLayout L{};
@@ -686,20 +704,7 @@ mf_status decode_tail_stage(const mf_decode_tail_args* args, uintptr_t stream, S
     }
     case Stage::kUnrestricted: {
       if (a->unrestricted_count == 0) break;
-      mf::FallbackArgs f{};
-      f.panel = reinterpret_cast<const uint16_t*>(ws + L.fb_panel);
-      f.slot_row = reinterpret_cast<const uint32_t*>(ws + L.fb_slot_row);
-      f.slot_norm = reinterpret_cast<const float*>(ws + L.fb_slot_norm);
-      f.m = static_cast<uint32_t>(a->unrestricted_count);
-      f.emb = ptr<const uint16_t>(a->embedding.address);
-      f.H = static_cast<uint32_t>(a->hidden);
-      f.V = static_cast<uint32_t>(a->vocab);
-      f.records = reinterpret_cast<mf::TileRecord*>(ws + L.fb_records);
-      f.fb_map = reinterpret_cast<uint32_t*>(ws + L.fb_map);
-      mfma_bound_coefs(a->hidden, f.coef, f.coef2);
-      f.slack = underflow_slack(a->hidden);
-      f.groups = device_cus();
-      e = mf::launch_fallback(f, s);
+      e = mf::launch_fallback(fallback_args(a, L, ws), s);
       break;
     }
     case Stage::kFinalize:

@@ -29,9 +29,13 @@ class DeviceTail:
     Infinity Cache (MALL) from the previous launch."""
 
     def __init__(self, w: Workload, device: str = "cuda", order: int = abi.ORDER_FMA_CHAIN,
-                 copies: int = 1, full: bool = False, advance: Optional[str] = None):
+                 copies: int = 1, full: bool = False, advance: Optional[str] = None,
+                 unrestricted: Optional[np.ndarray] = None):
         import torch
         self.w = w
+        # the rows handed to the MFMA head (default: the rows whose state is
+        # MF_STATE_UNRESTRICTED)
+        self._unrestricted = unrestricted
         self.device = device
         self.order = order
         self.stream = torch.cuda.Stream(device=device)
@@ -47,7 +51,8 @@ class DeviceTail:
         for _ in range(copies - 1):
             self.tables.append(self.tables[0].clone())
         self.x = _dev(w.x, device)
-        self.norm_weight = _dev(w.norm_weight, device)
+        # no weight: x is already normalized (the norm is skipped)
+        self.norm_weight = None if w.norm_weight is None else _dev(w.norm_weight, device)
         self.row_state = _dev(w.row_state, device)
         self.offsets = _dev(w.state_offsets, device)
         tokens = w.state_tokens if w.state_tokens.size else np.zeros(1, np.uint32)
@@ -61,7 +66,8 @@ class DeviceTail:
             self.state_next = _dev(w.state_next, device)
         elif advance == "dense" and w.next_table is not None:
             self.next_table = _dev(w.next_table, device)
-        unr = w.unrestricted_rows
+        unr = w.unrestricted_rows if self._unrestricted is None else \
+            np.asarray(self._unrestricted, dtype=np.uint32)
         self.unrestricted = _dev(unr, device) if unr.size else None
         self.n_unrestricted = int(unr.size)
         B = w.rows

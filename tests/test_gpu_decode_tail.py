@@ -199,3 +199,55 @@ def test_market_dfa_real_grammar_walk():
         # terminal states have no arcs: restart those rows at the root
         terminal = np.diff(offsets.astype(np.int64))[state] == 0
         state[terminal] = 0
+
+
+# ---- mf_decode_tail_f16 against its stage entry points -------------------
+
+def _staged(t):
+    """The four stage entry points in order (norm kernel, gather, head,
+    finalize), called one by one."""
+    from market_sim_amd import ops
+    a = t.args()
+    h = t.stream.cuda_stream
+    for fn in (ops.decode_tail_prepare, ops.decode_tail_restricted,
+               ops.decode_tail_unrestricted, ops.decode_tail_finalize):
+        abi.check("stage", fn(a, h))
+    return t.results()
+
+
+@pytest.mark.parametrize("rows", [40, 86, 200])
+def test_decode_tail_equals_its_stages(rows):
+    """One mf_decode_tail_f16 call and the four stage calls give the same
+    bits, and the oracle's."""
+    from market_sim_amd.tail import DeviceTail
+    w = wl.config(3, seed=21, scale_vocab=8192, scale_rows=rows)
+    assert w.unrestricted_rows.size > 0
+    t = DeviceTail(w)
+    fused = t.run()
+    staged = _staged(t)
+    for a, b in zip(fused, staged):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    _same(fused, _oracle(w))
+
+
+def test_decode_tail_without_norm_weight():
+    """norm_weight absent: x is taken as already normalized."""
+    w = wl.config(3, seed=22, scale_vocab=6000, scale_rows=48)
+    w.norm_weight = None
+    _same(_run(w), _oracle(w))
+
+
+def test_duplicate_and_foreign_unrestricted_rows():
+    """The unrestricted list names a row twice and a row whose state is
+    restricted: each row is finalized once, from its own kind."""
+    from market_sim_amd.tail import DeviceTail
+    w = wl.config(3, seed=23, scale_vocab=6000, scale_rows=48)
+    unr = w.unrestricted_rows
+    restricted = np.nonzero(w.row_state < w.states)[0]
+    listed = np.concatenate([unr, unr[:1], restricted[:1]]).astype(np.uint32)
+    t = DeviceTail(w, unrestricted=listed)
+    fused = t.run()
+    _same(fused, _oracle(w))
+    staged = _staged(t)
+    for a, b in zip(fused, staged):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
