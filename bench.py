@@ -46,6 +46,8 @@ def parse():
                    help="budget of the CPU oracle baseline sample")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-full", action="store_true")
+    p.add_argument("--no-reference-bench", action="store_true",
+                   help="skip the reference's 12-cell output-head benchmark")
     p.add_argument("--calibration-copy-mib", type=int, default=0,
                    help="after the timed loop, run 4 FP32 x1.0 copies of this many MiB "
                         "(a known-traffic kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -214,6 +216,37 @@ def cpu_baseline(w, budget_s: float) -> dict:
             "_outputs": outputs["full"]}
 
 
+def reference_bench() -> dict:
+    """The reference's own restricted output-head benchmark (12 cells,
+    src/tools/cuda_restricted_output_head_bench.cu) run by the C++ tool
+    market_sim_amd/bench/restricted_output_head_bench in a child process;
+    its document is checked against the reference schema and summarized
+    next to the published L4 cells."""
+    import subprocess
+    from market_sim_amd import schema
+    tool = os.path.join(ROOT, "market_sim_amd", "bench", "_build", "restricted_output_head_bench")
+    if not os.path.exists(tool):
+        return {"error": "tool not built (make -C market_sim_amd/bench)"}
+    r = subprocess.run([tool], capture_output=True, text=True, timeout=300)
+    if r.returncode != 0:
+        return {"error": f"exit {r.returncode}: {r.stderr.strip()[-300:]}"}
+    doc = json.loads(r.stdout)
+    schema.check_output_head_benchmark(doc)
+    cells = schema.compare_with_l4(doc)
+    ratios = [c["restricted_vs_l4"] for c in cells]
+    return {
+        "tool": "market_sim_amd/bench/restricted_output_head_bench",
+        "gpu": doc["gpu"],
+        "schema_ok": True,
+        "token_parity_cells": sum(m["exact_token_parity"] for m in doc["measurements"]),
+        "columns": ["rows", "allowed", "restricted_us", "full_us", "l4_restricted_us",
+                    "l4_full_us"],
+        "cells": [[c["rows"], c["allowed"], c["restricted_us"], c["full_us"],
+                   c["l4_restricted_us"], c["l4_full_us"]] for c in cells],
+        "restricted_vs_l4": [min(ratios), max(ratios)],
+    }
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -291,6 +324,8 @@ def main() -> int:
         result["full_head_ms"] = round(full_ms, 4)
         result["full_head_token_parity"] = bool(np.array_equal(ftok, tok))
         del full
+    if not args.no_reference_bench:
+        result["reference_bench"] = reference_bench()
     if not args.no_cpu:
         cb = cpu_baseline(w, args.cpu_seconds)
         etok, esc, enx = cb.pop("_outputs")

@@ -10,13 +10,17 @@
 // with the namespace changed; CudaStream and CublasHandle are provided
 // under their reference names too.
 //
-// Everything is noexcept and allocation-free except DeviceBuffer::allocate and
-// the stream/handle factories; ops never synchronize.
+// Everything is noexcept and allocation-free except DeviceBuffer::allocate,
+// the stream/handle factories and the set-up of the DFA and decoder objects
+// at the end (host vectors, device buffers); ops never synchronize.
 #pragma once
 
+#include <algorithm>
 #include <cstdint>
 #include <optional>
+#include <type_traits>
 #include <utility>
+#include <vector>
 
 #include "marketforge_hip.h"
 
@@ -294,6 +298,9 @@ enum class DotOrder : std::int32_t {
 
 inline constexpr std::uint32_t state_unrestricted = MF_STATE_UNRESTRICTED;
 inline constexpr std::uint32_t state_invalid = MF_STATE_INVALID;
+// DecodeTailArgs::flags: a row in a state with an empty list (a finished
+// sequence) keeps that state instead of becoming invalid.
+inline constexpr std::uint64_t tail_hold_finished = MF_TAIL_HOLD_FINISHED;
 
 // Buffers and shape of one decode-tail call (see marketforge_hip.h); null
 // pointers are the optional buffers left out.
@@ -319,6 +326,11 @@ struct DecodeTailArgs {
   std::uint64_t nnz = 0;
   std::uint64_t max_count = 0;
   std::uint64_t unrestricted_count = 0;
+  // Sequence table: row r's state is (*row_state)[(*row_sequence)[r]] and its
+  // next state goes to the same index of out_next_state, which may be
+  // row_state itself.  Null: row_state and out_next_state hold one entry per row.
+  const DeviceBuffer* row_sequence = nullptr;       // u32 [rows] or null
+  std::uint64_t flags = 0;                          // 0 or tail_hold_finished
 };
 
 namespace detail {
@@ -350,6 +362,8 @@ namespace detail {
   c.nnz = a.nnz;
   c.max_count = a.max_count;
   c.unrestricted_count = a.unrestricted_count;
+  c.row_sequence = view_or_null(a.row_sequence);
+  c.flags = a.flags;
   return c;
 }
 }  // namespace detail
@@ -376,5 +390,310 @@ namespace detail {
   const mf_decode_tail_args c = detail::to_c(args, &workspace);
   return detail::from_c(mf_decode_tail_f16(&c, stream.value));
 }
+
+// ---- token DFA export and the device-resident decode loop -----------------
+
+inline constexpr std::uint32_t no_choice = 0xFFFFFFFFu;
+
+// A token DFA as the decode tail reads it: CSR offsets [S + 1], arc tokens
+// and arc next states [A] (the allowed spans of token_dfa.cpp:100-109 laid
+// end to end), each state's terminal choice (no_choice otherwise), the
+// longest list and the most tokens on a root-to-terminal path.
+struct DfaTables {
+  std::vector<std::uint32_t> offsets;
+  std::vector<std::uint32_t> tokens;
+  std::vector<std::uint32_t> next;
+  std::vector<std::uint32_t> choice;
+  std::uint32_t max_count = 0;
+  std::uint32_t depth = 0;
+
+  [[nodiscard]] std::uint64_t states() const noexcept {
+    return offsets.empty() ? 0 : offsets.size() - 1;
+  }
+  [[nodiscard]] std::uint64_t arcs() const noexcept { return tokens.size(); }
+
+  // Checks the layout (offsets frame the arcs, tokens strictly ascending per
+  // state and below vocabulary_size, next states in range, no cycle) and
+  // fills max_count and depth.  invalid_format when it does not hold.
+  [[nodiscard]] Status finish(std::uint64_t vocabulary_size) noexcept {
+    const std::uint64_t S = states();
+    if (S == 0 || offsets.front() != 0 || offsets.back() != tokens.size() ||
+        next.size() != tokens.size() || choice.size() != S) {
+      return Status::failure(ErrorCode::invalid_format);
+    }
+    max_count = 0;
+    for (std::uint64_t s = 0; s < S; ++s) {
+      if (offsets[s + 1] < offsets[s]) return Status::failure(ErrorCode::invalid_format);
+      max_count = std::max<std::uint32_t>(max_count, offsets[s + 1] - offsets[s]);
+      for (std::uint32_t i = offsets[s]; i < offsets[s + 1]; ++i) {
+        if (tokens[i] >= vocabulary_size || next[i] >= S ||
+            (i > offsets[s] && tokens[i] <= tokens[i - 1])) {
+          return Status::failure(ErrorCode::invalid_format);
+        }
+      }
+    }
+    // breadth-first levels from the root; more levels than states is a cycle
+    std::vector<std::uint8_t> in_level(S, 0);
+    std::vector<std::uint32_t> level{0}, following;
+    depth = 0;
+    for (std::uint64_t round = 0;; ++round) {
+      following.clear();
+      for (const std::uint32_t s : level) {
+        for (std::uint32_t i = offsets[s]; i < offsets[s + 1]; ++i) {
+          if (!in_level[next[i]]) {
+            in_level[next[i]] = 1;
+            following.push_back(next[i]);
+          }
+        }
+      }
+      for (const std::uint32_t s : following) in_level[s] = 0;
+      if (following.empty()) break;
+      if (round >= S) return Status::failure(ErrorCode::invalid_format);
+      ++depth;
+      level.swap(following);
+    }
+    return Status::success();
+  }
+};
+
+// Exports a DFA through the reference grammar layer's public queries
+// (TokenDfa / ActionDfa: state_count(), root(), allowed(state) returning a
+// Result over a span of GrammarArc{token, next}, terminal(state),
+// decode_terminal(state); include/marketforge/grammar/token_dfa.hpp:30-74).
+// choice_of maps a terminal state to the uint32 the tables store (TokenDfa:
+// its ChoiceId; ActionDfa: e.g. the action's catalog index).
+template <class Dfa, class ChoiceOf>
+[[nodiscard]] Result<DfaTables> export_token_dfa(const Dfa& dfa, std::uint64_t vocabulary_size,
+                                                 ChoiceOf choice_of) {
+  using State = std::remove_cv_t<decltype(dfa.root())>;
+  DfaTables t;
+  const std::uint64_t S = dfa.state_count();
+  if (S == 0 || S > 0xFFFFFFFEull) return Result<DfaTables>::failure(Status::failure(ErrorCode::resource_limit));
+  t.offsets.reserve(S + 1);
+  t.choice.assign(S, no_choice);
+  for (std::uint64_t s = 0; s < S; ++s) {
+    t.offsets.push_back(static_cast<std::uint32_t>(t.tokens.size()));
+    const State state{static_cast<std::uint32_t>(s)};
+    const auto allowed = dfa.allowed(state);
+    if (!allowed) return Result<DfaTables>::failure(Status::failure(ErrorCode::invalid_argument));
+    for (const auto& arc : allowed.value()) {
+      t.tokens.push_back(arc.token);
+      t.next.push_back(arc.next.value);
+    }
+    if (dfa.terminal(state)) t.choice[s] = choice_of(dfa, state);
+  }
+  t.offsets.push_back(static_cast<std::uint32_t>(t.tokens.size()));
+  const Status st = t.finish(vocabulary_size);
+  if (!st.ok()) return Result<DfaTables>::failure(st);
+  return Result<DfaTables>::success(std::move(t));
+}
+
+// TokenDfa: the terminal's ChoiceId.
+template <class Dfa>
+[[nodiscard]] Result<DfaTables> export_token_dfa(const Dfa& dfa, std::uint64_t vocabulary_size) {
+  return export_token_dfa(dfa, vocabulary_size, [](const Dfa& d, auto state) {
+    const auto c = d.decode_terminal(state);
+    return c ? static_cast<std::uint32_t>(c.value()) : no_choice;
+  });
+}
+
+namespace detail {
+template <typename T>
+[[nodiscard]] inline Result<DeviceBuffer> upload_vector(const std::vector<T>& host,
+                                                        StreamHandle stream) noexcept {
+  // a zero-length list still gets a valid (4-byte) buffer
+  const std::uint64_t n = host.empty() ? sizeof(T) : host.size() * sizeof(T);
+  auto b = DeviceBuffer::allocate(n);
+  if (!b || host.empty()) return b;
+  const Status s = b.value().copy_from_host_async(host.data(), n, 0, stream);
+  if (!s.ok()) return Result<DeviceBuffer>::failure(s);
+  return b;
+}
+}  // namespace detail
+
+// The tables on the device (offsets, tokens, next); the terminal choices
+// stay on the host.  upload() synchronizes the stream once (the host
+// vectors are copied by then).
+class DeviceDfa {
+ public:
+  [[nodiscard]] static Result<DeviceDfa> upload(DfaTables tables, StreamHandle stream) noexcept {
+    DeviceDfa d;
+    auto o = detail::upload_vector(tables.offsets, stream);
+    auto t = detail::upload_vector(tables.tokens, stream);
+    auto n = detail::upload_vector(tables.next, stream);
+    if (!o) return Result<DeviceDfa>::failure(o.status());
+    if (!t) return Result<DeviceDfa>::failure(t.status());
+    if (!n) return Result<DeviceDfa>::failure(n.status());
+    const Status s = detail::from_c(mf_stream_synchronize(stream.value));
+    if (!s.ok()) return Result<DeviceDfa>::failure(s);
+    d.offsets_ = std::move(o).value();
+    d.tokens_ = std::move(t).value();
+    d.next_ = std::move(n).value();
+    d.tables_ = std::move(tables);
+    return Result<DeviceDfa>::success(std::move(d));
+  }
+  [[nodiscard]] const DfaTables& tables() const noexcept { return tables_; }
+  [[nodiscard]] const DeviceBuffer& offsets() const noexcept { return offsets_; }
+  [[nodiscard]] const DeviceBuffer& tokens() const noexcept { return tokens_; }
+  [[nodiscard]] const DeviceBuffer& next() const noexcept { return next_; }
+
+ private:
+  DfaTables tables_;
+  DeviceBuffer offsets_, tokens_, next_;
+};
+
+// What a decode loop produced: tokens [steps x rows] (row-major by step;
+// MF_INVALID_TOKEN after a row has finished), the final states and their
+// terminal choices.
+struct DecodeOutput {
+  std::uint64_t steps = 0;
+  std::uint64_t rows = 0;
+  std::vector<std::uint32_t> tokens;
+  std::vector<std::uint32_t> states;
+  std::vector<std::uint32_t> choice;
+};
+
+// Greedy restricted decoding of `rows` sequences in lock step with the DFA
+// state on the device: step() enqueues one decode-tail call (states alternate
+// between two device buffers, finished rows hold their terminal state) and
+// never synchronizes; finish() synchronizes once and copies every step's
+// tokens.  The replacement of the reference's per-token
+// CudaSmolLm2::decode_restricted round trip (src/cuda/smollm2.cu:336-366).
+class RestrictedDecoder {
+ public:
+  struct Config {
+    std::uint64_t rows = 0;
+    std::uint64_t hidden = 0;
+    std::uint64_t vocab = 0;
+    std::uint64_t max_steps = 0;
+    float epsilon = 1e-5f;
+    DotOrder order = DotOrder::fma_chain;
+  };
+
+  // embedding, norm_weight (null: hidden rows arrive normalized) and dfa
+  // are borrowed and must outlive the decoder.
+  [[nodiscard]] static Result<RestrictedDecoder> create(const DeviceBuffer& embedding,
+                                                        const DeviceBuffer* norm_weight,
+                                                        const DeviceDfa& dfa, Config config,
+                                                        StreamHandle stream) noexcept {
+    RestrictedDecoder d;
+    d.config_ = config;
+    d.dfa_ = &dfa;
+    if (config.rows == 0 || config.max_steps == 0) {
+      return Result<RestrictedDecoder>::failure(Status::failure(ErrorCode::invalid_argument));
+    }
+    auto states = DeviceBuffer::allocate(2 * config.rows * 4);
+    auto tokens = DeviceBuffer::allocate(config.max_steps * config.rows * 4);
+    auto scores = DeviceBuffer::allocate(config.max_steps * config.rows * 4);
+    if (!states) return Result<RestrictedDecoder>::failure(states.status());
+    if (!tokens) return Result<RestrictedDecoder>::failure(tokens.status());
+    if (!scores) return Result<RestrictedDecoder>::failure(scores.status());
+    d.states_ = std::move(states).value();
+    d.tokens_ = std::move(tokens).value();
+    d.scores_ = std::move(scores).value();
+    for (int parity = 0; parity < 2; ++parity) {
+      mf_decode_tail_args& a = d.args_[parity];
+      a = mf_decode_tail_args{};
+      a.x = mf_buffer{256, config.rows * config.hidden * 4};  // set per step
+      a.norm_weight = norm_weight != nullptr ? norm_weight->view() : mf_buffer{0, 0};
+      a.epsilon = config.epsilon;
+      a.order = static_cast<std::int32_t>(config.order);
+      a.embedding = embedding.view();
+      a.row_state = d.state_view(parity);
+      a.state_offsets = dfa.offsets().view();
+      a.state_tokens = dfa.tokens().view();
+      a.state_next = dfa.next().view();
+      a.out_token = d.step_view(d.tokens_, 0);
+      a.out_score = d.step_view(d.scores_, 0);
+      a.out_next_state = d.state_view(1 - parity);
+      a.rows = config.rows;
+      a.hidden = config.hidden;
+      a.vocab = config.vocab;
+      a.states = dfa.tables().states();
+      a.nnz = dfa.tables().arcs();
+      a.max_count = dfa.tables().max_count;
+      a.flags = MF_TAIL_HOLD_FINISHED;
+    }
+    std::uint64_t ws = 0;
+    Status s = detail::from_c(mf_decode_tail_workspace_bytes(&d.args_[0], &ws));
+    if (!s.ok()) return Result<RestrictedDecoder>::failure(s);
+    auto workspace = DeviceBuffer::allocate(ws);
+    if (!workspace) return Result<RestrictedDecoder>::failure(workspace.status());
+    d.workspace_ = std::move(workspace).value();
+    d.args_[0].workspace = d.args_[1].workspace = d.workspace_.view();
+    s = workspace_init(d.workspace_, stream);
+    if (!s.ok()) return Result<RestrictedDecoder>::failure(s);
+    return Result<RestrictedDecoder>::success(std::move(d));
+  }
+
+  // Every row at the DFA root (states == nullptr) or at states[0..rows).
+  // The host array must stay valid until the stream reaches the copy.
+  [[nodiscard]] Status start(const std::uint32_t* states, StreamHandle stream) noexcept {
+    step_ = 0;
+    if (states != nullptr) {
+      return states_.copy_from_host_async(states, config_.rows * 4, 0, stream);
+    }
+    root_.assign(config_.rows, 0u);
+    return states_.copy_from_host_async(root_.data(), config_.rows * 4, 0, stream);
+  }
+
+  // One decode step: hidden is this step's FP32 [rows, hidden] (a view, e.g.
+  // a slice of a larger buffer).
+  [[nodiscard]] Status step(mf_buffer hidden, StreamHandle stream) noexcept {
+    if (step_ >= config_.max_steps) return Status::failure(ErrorCode::resource_limit);
+    mf_decode_tail_args& a = args_[step_ % 2];
+    a.x = hidden;
+    a.out_token = step_view(tokens_, step_);
+    a.out_score = step_view(scores_, step_);
+    const Status s = detail::from_c(mf_decode_tail_f16(&a, stream.value));
+    if (s.ok()) ++step_;
+    return s;
+  }
+
+  [[nodiscard]] std::uint64_t steps() const noexcept { return step_; }
+  // For callers that capture steps into a graph and replay it after start():
+  // the buffers now hold k steps (k <= max_steps).
+  void assume_steps(std::uint64_t k) noexcept { step_ = std::min(k, config_.max_steps); }
+  // The states after the last step (device view).
+  [[nodiscard]] mf_buffer current_states() const noexcept { return state_view(step_ % 2); }
+
+  // Synchronizes once and copies the tokens of every step so far, the final
+  // states and their terminal choices.
+  [[nodiscard]] Result<DecodeOutput> finish(StreamHandle stream) {
+    DecodeOutput out;
+    out.steps = step_;
+    out.rows = config_.rows;
+    out.tokens.resize(step_ * config_.rows);
+    out.states.resize(config_.rows);
+    Status s = Status::success();
+    if (step_ > 0) s = tokens_.copy_to_host_async(out.tokens.data(), step_ * config_.rows * 4, 0, stream);
+    if (s.ok())
+      s = states_.copy_to_host_async(out.states.data(), config_.rows * 4,
+                                     (step_ % 2) * config_.rows * 4, stream);
+    if (s.ok()) s = detail::from_c(mf_stream_synchronize(stream.value));
+    if (!s.ok()) return Result<DecodeOutput>::failure(s);
+    out.choice.assign(config_.rows, no_choice);
+    const DfaTables& t = dfa_->tables();
+    for (std::uint64_t r = 0; r < config_.rows; ++r) {
+      if (out.states[r] < t.states()) out.choice[r] = t.choice[out.states[r]];
+    }
+    return Result<DecodeOutput>::success(std::move(out));
+  }
+
+ private:
+  [[nodiscard]] mf_buffer state_view(std::uint64_t parity) const noexcept {
+    return mf_buffer{states_.address().value + parity * config_.rows * 4, config_.rows * 4};
+  }
+  [[nodiscard]] mf_buffer step_view(const DeviceBuffer& b, std::uint64_t k) const noexcept {
+    return mf_buffer{b.address().value + k * config_.rows * 4, config_.rows * 4};
+  }
+
+  Config config_{};
+  const DeviceDfa* dfa_ = nullptr;
+  DeviceBuffer states_, tokens_, scores_, workspace_;
+  mf_decode_tail_args args_[2]{};
+  std::vector<std::uint32_t> root_;
+  std::uint64_t step_ = 0;
+};
 
 }  // namespace marketforge::gpu

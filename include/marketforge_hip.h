@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define MF_ABI_VERSION 1u
+#define MF_ABI_VERSION 2u
 
 /* Status: include/marketforge/core/status.hpp:7-49.  The numeric codes equal
  * the reference ErrorCode enumerators so results stay schema-compatible. */
@@ -186,6 +186,21 @@ mf_status mf_linear_f16(mf_buffer input, mf_buffer weight, mf_buffer output,
  * u32[rows] (optional; MF_STATE_INVALID for invalid rows,
  * MF_STATE_UNRESTRICTED for unrestricted rows).
  *
+ * Sequence table (row_sequence given, for continuous batching): row_state is
+ * then a table of per-sequence DFA states with capacity = row_state.bytes / 4
+ * entries.  Row r reads its state at row_state[row_sequence[r]] and writes its
+ * next state to out_next_state[row_sequence[r]]; out_next_state has the
+ * table's size and may be row_state itself (the table is updated in place).
+ * A row whose index is >= capacity is invalid and writes no state.  The
+ * sequences of one call must be distinct: two rows with one index race.
+ *
+ * flags: MF_TAIL_HOLD_FINISHED -- a row whose state has an empty list (a
+ * terminal state of the token DFA: its trie ends every choice at a leaf and
+ * extends no choice through one, src/grammar/token_dfa.cpp:49-53, 67-71) writes its own state as next state
+ * (token MF_INVALID_TOKEN, score NaN), so a decode loop can run past a
+ * sequence's end with no host check.  Without the flag such a row's next
+ * state is MF_STATE_INVALID, as for every invalid row.
+ *
  * Workspace: caller-allocated device memory of mf_decode_tail_workspace_bytes
  * bytes, zero-filled once by mf_workspace_init before first use.  Every call
  * leaves it ready for the next one; calls that overlap in time on the same
@@ -213,7 +228,11 @@ typedef struct mf_decode_tail_args {
   uint64_t nnz;
   uint64_t max_count;          /* longest state list (table builder's figure) */
   uint64_t unrestricted_count;
+  mf_buffer row_sequence;      /* u32 [rows] or address 0: see "Sequence table" */
+  uint64_t flags;              /* 0 or MF_TAIL_HOLD_FINISHED */
 } mf_decode_tail_args;
+
+#define MF_TAIL_HOLD_FINISHED 1u
 
 mf_status mf_decode_tail_workspace_bytes(const mf_decode_tail_args* args,
                                          uint64_t* bytes);

@@ -29,6 +29,8 @@ STATE_UNRESTRICTED = 0xFFFFFFFE
 STATE_INVALID = 0xFFFFFFFF
 ORDER_FMA_CHAIN = 0
 ORDER_MUL_ADD_CHAIN = 1
+TAIL_HOLD_FINISHED = 1
+ABI_VERSION = 2
 
 _U64 = ctypes.c_uint64
 _UP = ctypes.c_size_t  # uintptr_t
@@ -55,6 +57,7 @@ class DecodeTailArgs(ctypes.Structure):
         ("out_score", Buffer), ("out_next_state", Buffer), ("workspace", Buffer),
         ("rows", _U64), ("hidden", _U64), ("vocab", _U64), ("states", _U64),
         ("nnz", _U64), ("max_count", _U64), ("unrestricted_count", _U64),
+        ("row_sequence", Buffer), ("flags", _U64),
     ]
 
 
@@ -118,6 +121,9 @@ def lib() -> ctypes.CDLL:
             fn = getattr(l, name)
             fn.restype = restype
             fn.argtypes = argtypes
+        if l.mf_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"{LIB_PATH} has ABI version {l.mf_abi_version()}, this binding "
+                               f"expects {ABI_VERSION}: rebuild it")
         _lib = l
     return _lib
 

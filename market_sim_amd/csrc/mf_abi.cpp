@@ -496,33 +496,47 @@ mf_status validate_tail(const mf_decode_tail_args* a, bool full, TailLayout& L) 
       te > kU64Max / 4u) {
     return status(MF_ARITHMETIC_OVERFLOW);
   }
+  // the state buffers: one entry per row, or a sequence table of any
+  // capacity that row_sequence indexes
+  const bool table = a->row_sequence.address != 0;
+  if ((a->flags & ~static_cast<uint64_t>(MF_TAIL_HOLD_FINISHED)) != 0) {
+    return status(MF_INVALID_ARGUMENT);
+  }
+  if (table && (a->row_state.bytes / 4u > kU32Max || a->row_state.bytes == 0 ||
+                (a->row_state.bytes % 4u) != 0 || !buffer_is(a->row_sequence, a->rows * 4u))) {
+    return status(a->row_state.bytes / 4u > kU32Max ? MF_RESOURCE_LIMIT : MF_INVALID_ARGUMENT);
+  }
+  const uint64_t state_bytes = table ? a->row_state.bytes : a->rows * 4u;
   if (!buffer_is(a->x, xe * 4u) || !buffer_is(a->embedding, ee * 2u) ||
-      !optional_is(a->norm_weight, a->hidden * 4u) || !buffer_is(a->row_state, a->rows * 4u) ||
+      !optional_is(a->norm_weight, a->hidden * 4u) || !buffer_is(a->row_state, state_bytes) ||
       !buffer_is(a->state_offsets, (a->states + 1) * 4u) ||
       !(a->nnz == 0 || buffer_is(a->state_tokens, a->nnz * 4u)) ||
       !optional_is(a->state_next, a->nnz * 4u) || !optional_is(a->next_table, te * 4u) ||
       (a->state_next.address != 0 && a->next_table.address != 0) ||
       !buffer_is(a->out_token, a->rows * 4u) || !optional_is(a->out_score, a->rows * 4u) ||
-      !optional_is(a->out_next_state, a->rows * 4u) ||
+      !optional_is(a->out_next_state, state_bytes) ||
       (a->unrestricted_count > 0 &&
        !buffer_is(a->unrestricted_rows, a->unrestricted_count * 4u))) {
     return status(MF_INVALID_ARGUMENT);
   }
-  // outputs must not alias each other or any input
+  // outputs must not alias each other or any input; with a sequence table the
+  // next states may update the table in place
   const uintptr_t outs[3] = {a->out_token.address, a->out_score.address,
                              a->out_next_state.address};
-  const uintptr_t ins[10] = {a->x.address, a->embedding.address, a->norm_weight.address,
+  const uintptr_t ins[11] = {a->x.address, a->embedding.address, a->norm_weight.address,
                              a->row_state.address, a->state_offsets.address,
                              a->state_tokens.address, a->state_next.address,
                              a->next_table.address, a->unrestricted_rows.address,
-                             a->workspace.address};
+                             a->workspace.address, a->row_sequence.address};
   for (int i = 0; i < 3; ++i) {
     if (outs[i] == 0) continue;
     for (int j = 0; j < 3; ++j) {
       if (j != i && outs[j] == outs[i]) return status(MF_INVALID_ARGUMENT);
     }
     for (uintptr_t in : ins) {
-      if (in != 0 && in == outs[i]) return status(MF_INVALID_ARGUMENT);
+      const bool in_place = table && i == 2 && in == a->row_state.address &&
+                            a->out_next_state.bytes == a->row_state.bytes;
+      if (in != 0 && in == outs[i] && !in_place) return status(MF_INVALID_ARGUMENT);
     }
   }
   if ((a->embedding.address % 16u) != 0 || (a->x.address % 16u) != 0 ||
@@ -600,6 +614,9 @@ mf::TailNormArgs norm_args(const mf_decode_tail_args* a, const TailLayout& L, ch
   n.out_token = ptr<uint32_t>(a->out_token.address);
   n.out_score = ptr<float>(a->out_score.address);
   n.out_next = ptr<uint32_t>(a->out_next_state.address);
+  n.row_sequence = ptr<const uint32_t>(a->row_sequence.address);
+  n.capacity = static_cast<uint32_t>(n.row_sequence != nullptr ? a->row_state.bytes / 4u : a->rows);
+  n.hold = (a->flags & MF_TAIL_HOLD_FINISHED) ? 1u : 0u;
   if (L.fb_rows > 0) {  // the MFMA head's panel
     n.fb_rows = ptr<const uint32_t>(a->unrestricted_rows.address);
     n.fb_m = static_cast<uint32_t>(a->unrestricted_count);
@@ -649,6 +666,8 @@ mf::FinalizeArgs finalize_args(const mf_decode_tail_args* a, const TailLayout& L
   f.out_token = ptr<uint32_t>(a->out_token.address);
   f.out_score = ptr<float>(a->out_score.address);
   f.out_next = ptr<uint32_t>(a->out_next_state.address);
+  f.row_sequence = ptr<const uint32_t>(a->row_sequence.address);
+  f.capacity = static_cast<uint32_t>(f.row_sequence != nullptr ? a->row_state.bytes / 4u : a->rows);
   f.rows = static_cast<uint32_t>(a->rows);
   f.H = static_cast<uint32_t>(a->hidden);
   f.V = static_cast<uint32_t>(a->vocab);

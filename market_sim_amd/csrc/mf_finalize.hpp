@@ -242,7 +242,8 @@ __device__ inline void finalize_row(const FinalizeArgs& a, uint32_t r, const Row
     if (lane == 0) {
       a.out_token[r] = kInvalidToken;
       if (a.out_score != nullptr) a.out_score[r] = __builtin_nanf("");
-      if (a.out_next != nullptr) a.out_next[r] = kInvalidToken;
+      uint32_t* next = next_state_slot(a.out_next, a.row_sequence, a.capacity, r);
+      if (next != nullptr) *next = kInvalidToken;
     }
     return;
   }
@@ -366,7 +367,8 @@ __device__ inline void finalize_row(const FinalizeArgs& a, uint32_t r, const Row
     }
     a.out_token[r] = token;
     if (a.out_score != nullptr) a.out_score[r] = score;
-    if (a.out_next != nullptr) a.out_next[r] = next;
+    uint32_t* slot = next_state_slot(a.out_next, a.row_sequence, a.capacity, r);
+    if (slot != nullptr) *slot = next;
   }
   wave_sync();
 }

@@ -94,6 +94,12 @@ struct TailNormArgs {
   uint32_t* out_token;
   float* out_score;
   uint32_t* out_next;
+  // Sequence table: row r's state is row_state[row_sequence[r]] and its next
+  // state goes to out_next[row_sequence[r]] (null: index r); indices >=
+  // capacity make the row invalid.  hold: an empty list keeps the state.
+  const uint32_t* row_sequence;
+  uint32_t capacity;
+  uint32_t hold;
   // The MFMA head's panel (fb_panel null: none).  Workgroup rows + j
   // normalizes row fb_rows[j] again (the same arithmetic, so the same bits)
   // and writes slot j: its FP16 split into the panel, its norm bound and its
@@ -157,11 +163,24 @@ struct FinalizeArgs {
   uint32_t* out_token;
   float* out_score;
   uint32_t* out_next;
+  const uint32_t* row_sequence;  // as in TailNormArgs
+  uint32_t capacity;
   uint32_t rows;
   uint32_t H;
   uint32_t V;
   int order;
 };
+
+// Where row r's next state goes: out_next[row_sequence[r]] with a sequence
+// table, else out_next[r]; null when there is no output or the index is
+// outside the table.
+__device__ __forceinline__ uint32_t* next_state_slot(uint32_t* out_next,
+                                                     const uint32_t* row_sequence,
+                                                     uint32_t capacity, uint32_t r) {
+  if (out_next == nullptr) return nullptr;
+  const uint32_t q = row_sequence != nullptr ? row_sequence[r] : r;
+  return q < capacity ? out_next + q : nullptr;
+}
 
 hipError_t launch_tail_norm(const TailNormArgs& args, hipStream_t stream);
 hipError_t launch_gather(ScoreSource source, const GatherArgs& args, hipStream_t stream);

@@ -97,9 +97,18 @@ __global__ __launch_bounds__(kWave) void tail_norm_kernel(TailNormArgs a) {
       return;
     }
   }
-  // the row's state first: its list offsets depend on it
+  // the row's state first: its list offsets depend on it (through the
+  // sequence table when there is one)
   uint32_t s = 0u;
-  if (!slot && lane == 0) s = a.row_state[r];
+  uint32_t q = static_cast<uint32_t>(r);
+  if (!slot && lane == 0) {
+    if (a.row_sequence != nullptr) {
+      q = a.row_sequence[r];
+      s = q < a.capacity ? a.row_state[q] : kInvalidToken;
+    } else {
+      s = a.row_state[r];
+    }
+  }
   float* ws = lds + 2u * H;  // weight (when given)
   const bool weighted = a.weight != nullptr;
   if ((H & 3u) == 0) {
@@ -162,10 +171,13 @@ __global__ __launch_bounds__(kWave) void tail_norm_kernel(TailNormArgs a) {
       a.row_meta[r] = meta;
       if (meta.kind != kRowRestricted) {
         // invalid rows keep these; unrestricted rows are overwritten by the
-        // finalize kernel when the MFMA head was given them
+        // finalize kernel when the MFMA head was given them.  A finished row
+        // (empty list) holds its state when asked to.
         a.out_token[r] = kInvalidToken;
         if (a.out_score != nullptr) a.out_score[r] = __builtin_nanf("");
-        if (a.out_next != nullptr) a.out_next[r] = kInvalidToken;
+        if (a.out_next != nullptr && q < a.capacity) {
+          a.out_next[q] = (a.hold && s < a.states && e == b) ? s : kInvalidToken;
+        }
       }
       if (a.fb_map != nullptr) a.fb_map[r] = kInvalidToken;
     }

@@ -163,12 +163,13 @@ class DecodeTailBuffers:
     out_score: DeviceBuffer = DeviceBuffer()
     out_next_state: DeviceBuffer = DeviceBuffer()
     workspace: DeviceBuffer = DeviceBuffer()
+    row_sequence: DeviceBuffer = DeviceBuffer()
 
 
 def decode_tail_args(b: DecodeTailBuffers, *, rows: int, hidden: int, vocab: int,
                      states: int, nnz: int, max_count: int,
                      unrestricted_count: int = 0, epsilon: float = 1e-5,
-                     order: int = abi.ORDER_FMA_CHAIN) -> abi.DecodeTailArgs:
+                     order: int = abi.ORDER_FMA_CHAIN, flags: int = 0) -> abi.DecodeTailArgs:
     a = abi.DecodeTailArgs()
     a.x = b.x.c()
     a.norm_weight = b.norm_weight.c()
@@ -187,6 +188,8 @@ def decode_tail_args(b: DecodeTailBuffers, *, rows: int, hidden: int, vocab: int
     a.workspace = b.workspace.c()
     a.rows, a.hidden, a.vocab, a.states = rows, hidden, vocab, states
     a.nnz, a.max_count, a.unrestricted_count = nnz, max_count, unrestricted_count
+    a.row_sequence = b.row_sequence.c()
+    a.flags = flags
     return a
 
 

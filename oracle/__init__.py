@@ -102,7 +102,9 @@ def ref() -> Optional[ctypes.CDLL]:
         r.mfref_token_dfa_advance.restype = _I
         r.mfref_token_dfa_advance.argtypes = [_P, _P, _P, u32, u32, u32, u32, _P]
         r.mfref_market_dfa_export.restype = _I
-        r.mfref_market_dfa_export.argtypes = [_P, _P, _P, u32, u32, _P, _P]
+        r.mfref_market_dfa_export.argtypes = [_P, _P, _P, _P, u32, u32, _P, _P]
+        r.mfref_market_language.restype = _I
+        r.mfref_market_language.argtypes = [_P, _P, u32, u32, _P, _P]
         _ref = r
     return _ref
 
@@ -263,3 +265,39 @@ def decode_tail(x, norm_weight, eps, emb_bits, row_state, state_offsets,
                           rows, _ptr(so), _ptr(st), states, _ptr(sn), _ptr(nt),
                           order, _ptr(tok), _ptr(sc), _ptr(nx), threads)
     return tok, sc, nx
+
+
+def decode_tail_sequences(x, norm_weight, eps, emb_bits, table, row_sequence,
+                          state_offsets, state_tokens, state_next=None, next_table=None,
+                          order=ORDER_FMA_CHAIN, hold=False, threads=1):
+    """The decode tail over a per-sequence state table, with the device
+    library's conventions for it (the "Sequence table" and
+    MF_TAIL_HOLD_FINISHED of include/marketforge_hip.h), restated around
+    ``decode_tail``:
+
+    * row r uses the state table[row_sequence[r]] (``row_sequence=None``: row
+      r uses table[r]); an index outside the table makes the row invalid and
+      writes nothing back;
+    * the next states are written back to the same indices of a copy of the
+      table, which is returned;
+    * ``hold``: a row whose state has an empty list keeps that state.
+
+    Returns (tokens, scores, updated table)."""
+    table = np.array(table, dtype=np.uint32)
+    rows = np.asarray(x).shape[0]
+    seq = np.arange(rows, dtype=np.uint64) if row_sequence is None else \
+        np.asarray(row_sequence, dtype=np.uint64)
+    inside = seq < table.size
+    states = np.full(rows, 0xFFFFFFFF, np.uint32)
+    states[inside] = table[seq[inside]]
+    tok, sc, nx = decode_tail(x, norm_weight, eps, emb_bits, states, state_offsets,
+                              state_tokens, state_next=state_next, next_table=next_table,
+                              order=order, threads=threads)
+    if hold:
+        so = np.asarray(state_offsets, dtype=np.uint32)
+        known = states < so.size - 1
+        empty = np.zeros(rows, bool)
+        empty[known] = so[states[known] + 1] == so[states[known]]
+        nx = np.where(empty, states, nx)
+    table[seq[inside]] = nx[inside]
+    return tok, sc, table

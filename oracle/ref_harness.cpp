@@ -155,9 +155,12 @@ int mfref_token_dfa_advance(const std::uint32_t* choice_ids,
   return 0;
 }
 
-// Exports the SmolLM2 market-action DFA (src/grammar/generated data) as CSR.
+// Exports the SmolLM2 market-action DFA (src/grammar/generated data) as CSR,
+// plus per state the index of its terminal action in catalog.entries()
+// (UINT32_MAX when not terminal; out_terminal may be null).
 int mfref_market_dfa_export(std::uint32_t* out_offsets,
                             std::uint32_t* out_tokens, std::uint32_t* out_next,
+                            std::uint32_t* out_terminal,
                             std::uint32_t state_capacity,
                             std::uint32_t arc_capacity,
                             std::uint32_t* out_states,
@@ -183,8 +186,47 @@ int mfref_market_dfa_export(std::uint32_t* out_offsets,
       out_next[cursor] = arc.next.value;
       ++cursor;
     }
+    if (out_terminal != nullptr) {
+      out_terminal[s] = UINT32_MAX;
+      const auto decoded = dfa.decode_terminal(marketforge::GrammarState{s});
+      if (decoded) {
+        const auto entries = catalog.value().entries();
+        for (std::uint32_t i = 0; i < entries.size(); ++i) {
+          if (entries[i].action == decoded.value()) {
+            out_terminal[s] = i;
+            break;
+          }
+        }
+      }
+    }
   }
   out_offsets[states] = cursor;
+  return 0;
+}
+
+// The market-action language: token sequence of every catalog entry, as
+// offsets[entries + 1] into tokens.
+int mfref_market_language(std::uint32_t* out_offsets, std::uint32_t* out_tokens,
+                          std::uint32_t entry_capacity, std::uint32_t token_capacity,
+                          std::uint32_t* out_entries, std::uint32_t* out_token_count) {
+  auto catalog = marketforge::SmolLm2MarketActionCatalog::create();
+  if (!catalog) {
+    return static_cast<int>(catalog.status().code);
+  }
+  const auto entries = catalog.value().entries();
+  std::uint32_t n = 0;
+  for (const auto& e : entries) n += static_cast<std::uint32_t>(e.tokens.size());
+  *out_entries = static_cast<std::uint32_t>(entries.size());
+  *out_token_count = n;
+  if (entries.size() + 1 > entry_capacity || n > token_capacity) {
+    return -1;
+  }
+  std::uint32_t cursor = 0;
+  for (std::uint32_t i = 0; i < entries.size(); ++i) {
+    out_offsets[i] = cursor;
+    for (const auto t : entries[i].tokens) out_tokens[cursor++] = t;
+  }
+  out_offsets[entries.size()] = cursor;
   return 0;
 }
 

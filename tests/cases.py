@@ -60,6 +60,19 @@ def market_dfa():
     return d["offsets"], d["tokens"], d["next"]
 
 
+def market_dfa_terminal():
+    """Per state, the index of its terminal action among the catalog's
+    entries (0xFFFFFFFF: not terminal)."""
+    return np.load(os.path.join(GOLDEN, "market_dfa.npz"))["terminal"]
+
+
+def market_language():
+    """The catalog's entries as token sequences, in catalog order."""
+    d = np.load(os.path.join(GOLDEN, "market_dfa.npz"))
+    o, t = d["language_offsets"], d["language_tokens"]
+    return [t[o[i]:o[i + 1]].tolist() for i in range(o.size - 1)]
+
+
 def market_restricted_greedy_case():
     """tests/cuda/cuda_tests.cu:567-651: the first 8 non-empty market-DFA
     states; row 0 all 4.0 (lowest id wins), row 1 all NaN (lowest id), other

@@ -12,6 +12,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <span>
 #include <string>
 #include <vector>
 
@@ -361,6 +362,131 @@ void test_decode_tail(const mg::GpuStream& stream, mg::DotOrder order) {
   CHECK(etok[5] == mg::restricted_greedy_invalid_token_id);
 }
 
+// A DFA with the reference grammar layer's interface (token_dfa.hpp:30-74):
+// the trie of {41: [9, 4], 7: [3, 8, 1], 99: [9, 6]} the reference builds
+// (token_dfa_tests.cpp:22-49), states in creation order.
+struct MockState {
+  uint32_t value{0};
+};
+struct MockArc {
+  uint32_t token{0};
+  MockState next{};
+};
+struct MockDfa {
+  std::vector<uint32_t> first{0, 2, 4, 4, 5, 6, 6}, count{2, 2, 0, 1, 1, 0, 0};
+  std::vector<MockArc> arcs{{3, {3}}, {9, {1}}, {4, {2}}, {6, {6}}, {8, {4}}, {1, {5}}};
+  std::vector<uint32_t> term{UINT32_MAX, UINT32_MAX, 41, UINT32_MAX, UINT32_MAX, 7, 99};
+  MockState root() const { return {}; }
+  size_t state_count() const { return first.size(); }
+  mg::Result<std::span<const MockArc>> allowed(MockState s) const {
+    if (s.value >= first.size())
+      return mg::Result<std::span<const MockArc>>::failure(
+          mg::Status::failure(mg::ErrorCode::invalid_argument));
+    return mg::Result<std::span<const MockArc>>::success(
+        std::span<const MockArc>(arcs).subspan(first[s.value], count[s.value]));
+  }
+  bool terminal(MockState s) const { return s.value < term.size() && term[s.value] != UINT32_MAX; }
+  mg::Result<uint32_t> decode_terminal(MockState s) const {
+    if (!terminal(s))
+      return mg::Result<uint32_t>::failure(mg::Status::failure(mg::ErrorCode::invalid_argument));
+    return mg::Result<uint32_t>::success(term[s.value]);
+  }
+};
+
+void test_dfa_export() {
+  const MockDfa dfa;
+  auto t = mg::export_token_dfa(dfa, 64);
+  CHECK(t.has_value());
+  if (!t) return;
+  const mg::DfaTables& d = t.value();
+  CHECK((d.offsets == std::vector<uint32_t>{0, 2, 4, 4, 5, 6, 6, 6}));
+  CHECK((d.tokens == std::vector<uint32_t>{3, 9, 4, 6, 8, 1}));
+  CHECK((d.next == std::vector<uint32_t>{3, 1, 2, 6, 4, 5}));
+  CHECK((d.choice == std::vector<uint32_t>{mg::no_choice, mg::no_choice, 41, mg::no_choice,
+                                           mg::no_choice, 7, 99}));
+  CHECK(d.max_count == 2 && d.depth == 3 && d.states() == 7 && d.arcs() == 6);
+  // a token beyond the vocabulary, descending tokens, a cycle
+  CHECK(mg::export_token_dfa(dfa, 9).status().code == mg::ErrorCode::invalid_format);
+  mg::DfaTables bad = d;
+  std::swap(bad.tokens[0], bad.tokens[1]);
+  CHECK(bad.finish(64).code == mg::ErrorCode::invalid_format);
+  bad = d;
+  bad.next[5] = 0;  // 4 --1--> root
+  CHECK(bad.finish(64).code == mg::ErrorCode::invalid_format);
+}
+
+// The device-resident decode loop on the mock DFA against the oracle run
+// step by step on the host (finished rows hold their terminal state).
+void test_restricted_decoder(const mg::GpuStream& stream) {
+  const uint64_t rows = 6, hidden = 64, vocab = 64, steps = 5;
+  auto exported = mg::export_token_dfa(MockDfa{}, vocab);
+  if (!exported) {
+    ++failures;
+    return;
+  }
+  const mg::DfaTables tables = exported.value();
+  uint64_t seed = 0xD1B54A32D192ED03ull;
+  auto unit = [&seed]() {
+    seed ^= seed << 13;
+    seed ^= seed >> 7;
+    seed ^= seed << 17;
+    return static_cast<float>(seed >> 40) * 0x1p-24f;
+  };
+  std::vector<float> e(vocab * hidden), x(steps * rows * hidden);
+  for (auto& v : e) v = (unit() - 0.5f) * 0.2f;
+  for (auto& v : x) v = unit() * 2.0f - 1.0f;
+  const auto e16 = to_half(e);
+  const auto h = stream.handle();
+  auto de = upload(e16, stream);
+  auto dx = upload(x, stream);
+  auto dfa = mg::DeviceDfa::upload(tables, h);
+  if (!de || !dx || !dfa) {
+    ++failures;
+    return;
+  }
+  mg::RestrictedDecoder::Config cfg;
+  cfg.rows = rows;
+  cfg.hidden = hidden;
+  cfg.vocab = vocab;
+  cfg.max_steps = steps;
+  auto dec = mg::RestrictedDecoder::create(de.value(), nullptr, dfa.value(), cfg, h);
+  if (!dec) {
+    std::fprintf(stderr, "decoder: code %d\n", static_cast<int>(dec.status().code));
+    ++failures;
+    return;
+  }
+  const std::vector<uint32_t> start{0, 0, 1, 3, 2, 0};  // root, mid-way, already finished
+  REQUIRE_OK(dec.value().start(start.data(), h));
+  for (uint64_t k = 0; k < steps; ++k) {
+    const mf_buffer view{dx.value().address().value + k * rows * hidden * 4, rows * hidden * 4};
+    REQUIRE_OK(dec.value().step(view, h));
+  }
+  auto out = dec.value().finish(h);
+  if (!out) {
+    ++failures;
+    return;
+  }
+  std::vector<uint32_t> state = start, tok(rows), nx(rows);
+  std::vector<float> sc(rows);
+  bool same = out.value().steps == steps;
+  for (uint64_t k = 0; same && k < steps; ++k) {
+    orc_decode_tail(x.data() + k * rows * hidden, nullptr, 1e-5f, e16.data(), nullptr, vocab,
+                    hidden, state.data(), rows, tables.offsets.data(), tables.tokens.data(),
+                    tables.states(), tables.next.data(), nullptr, 0, tok.data(), sc.data(),
+                    nx.data(), 1);
+    for (uint64_t r = 0; r < rows; ++r) {
+      const bool empty = state[r] < tables.states() &&
+                         tables.offsets[state[r] + 1] == tables.offsets[state[r]];
+      state[r] = empty ? state[r] : nx[r];
+      same = same && out.value().tokens[k * rows + r] == tok[r];
+    }
+  }
+  CHECK(same);
+  CHECK(out.value().states == state);
+  for (uint64_t r = 0; r < rows; ++r) CHECK(out.value().choice[r] == tables.choice[state[r]]);
+  CHECK(out.value().choice[4] == 41u);  // started finished, held there
+}
+
 void run_gpu() {
   auto stream = mg::GpuStream::create();
   if (!stream) {
@@ -379,6 +505,8 @@ void run_gpu() {
   test_decode_tail(stream.value(), mg::DotOrder::fma_chain);
   std::printf("gpu: decode tail (mul-add chain)\n");
   test_decode_tail(stream.value(), mg::DotOrder::mul_add_chain);
+  std::printf("gpu: restricted decoder\n");
+  test_restricted_decoder(stream.value());
   std::fflush(stdout);
 }
 
@@ -389,6 +517,7 @@ int main(int argc, char** argv) {
   test_status_and_result();
   test_buffers_without_device();
   test_validation_order();
+  test_dfa_export();
   if (mode == "--gpu") run_gpu();
   std::printf("%s: %d checks, %d failures\n", mode.c_str(), checks, failures);
   return failures == 0 ? 0 : 1;

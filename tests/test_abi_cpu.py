@@ -26,7 +26,7 @@ def test_library_exports_every_declared_symbol():
     lib = abi.lib()
     for name in declared_functions():
         assert hasattr(lib, name), name
-    assert lib.mf_abi_version() == 1
+    assert lib.mf_abi_version() == 2
 
 
 def b(addr, n):
@@ -144,3 +144,32 @@ def test_decode_tail_validation():
     assert l.mf_decode_tail_f16(ctypes.byref(bad), FAKE_STREAM).code == abi.MF_RESOURCE_LIMIT
     bad = _tail_args(unrestricted_count=2)  # rows list missing
     assert l.mf_decode_tail_f16(ctypes.byref(bad), FAKE_STREAM).code == abi.MF_INVALID_ARGUMENT
+
+
+def test_decode_tail_sequence_table_and_flags_validation():
+    """The sequence table: row_sequence sized by rows, a state table of any
+    whole-entry size, next states of the table's size that may update it in
+    place; unknown flag bits are rejected."""
+    l = abi.lib()
+    n = ctypes.c_uint64()
+    rs = _tail_args().row_state
+
+    def ws_code(**kw):
+        a = _tail_args(**kw)
+        return l.mf_decode_tail_workspace_bytes(ctypes.byref(a), ctypes.byref(n)).code
+
+    table = b(rs.address, 40)                       # 10 entries for 4 rows
+    seq = b(0xA00000, 16)
+    assert ws_code(row_state=table, row_sequence=seq) == abi.MF_OK
+    assert ws_code(row_state=table, row_sequence=seq, out_next_state=table) == abi.MF_OK
+    assert ws_code(row_state=table, row_sequence=seq, out_next_state=b(0xB00000, 40)) == abi.MF_OK
+    assert ws_code(row_state=table, row_sequence=seq,
+                   out_next_state=b(0xB00000, 16)) == abi.MF_INVALID_ARGUMENT
+    assert ws_code(row_state=table, row_sequence=b(0xA00000, 12)) == abi.MF_INVALID_ARGUMENT
+    assert ws_code(row_state=b(rs.address, 42), row_sequence=seq) == abi.MF_INVALID_ARGUMENT
+    assert ws_code(row_state=table) == abi.MF_INVALID_ARGUMENT   # no table: rows entries
+    # without a sequence table the next states must not overwrite the states
+    assert ws_code(out_next_state=rs) == abi.MF_INVALID_ARGUMENT
+    assert ws_code(row_state=table, row_sequence=seq, out_token=seq) == abi.MF_INVALID_ARGUMENT
+    assert ws_code(flags=abi.TAIL_HOLD_FINISHED) == abi.MF_OK
+    assert ws_code(flags=2) == abi.MF_INVALID_ARGUMENT

@@ -1,0 +1,234 @@
+"""GPU parity of the decode loops (market_sim_amd/decode.py) and of the C ABI's
+sequence table and hold-finished flag, on the reference's real market-action
+DFA (tests/golden/market_dfa.npz), against the oracle restated per step
+(oracle.decode_tail_sequences).  Bar: tokens, scores and states bit-exact.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from market_sim_amd import abi, ops
+from market_sim_amd import workloads as wl
+from market_sim_amd.dfa import NO_CHOICE, DfaTables
+from tests import cases
+
+pytestmark = pytest.mark.gpu
+
+VOCAB = 49152
+
+
+@pytest.fixture(autouse=True)
+def _lib(hip):
+    return hip
+
+
+@pytest.fixture(scope="module")
+def market():
+    o, t, n = cases.market_dfa()
+    return DfaTables.from_arrays(o, t, n, cases.market_dfa_terminal(), vocab=VOCAB)
+
+
+def _table(seed, hidden):
+    return wl.normal_table_f16(np.random.default_rng(seed), VOCAB, hidden, 0.02)
+
+
+def _hidden(rng, rows, hidden):
+    return rng.standard_normal((rows, hidden), dtype=np.float32)
+
+
+def _same(tok, sc, etok, esc):
+    bad = np.nonzero(tok != etok)[0]
+    assert bad.size == 0, f"rows {bad[:8]}: got {tok[bad[:8]]} want {etok[bad[:8]]}"
+    nan = np.isnan(esc)
+    assert np.array_equal(np.isnan(sc), nan)
+    assert np.array_equal(sc[~nan].view(np.uint32), esc[~nan].view(np.uint32))
+
+
+@pytest.mark.parametrize("hold", [False, True])
+def test_sequence_table_updates_states_in_place(market, hold):
+    """One call over a 100-entry state table: 40 rows at distinct random
+    entries (any market state, terminal ones included, and two unrestricted
+    sequences) plus one row whose index is outside the table."""
+    import torch
+    from market_sim_amd.decode import DeviceDfa
+    rng = np.random.default_rng(11 + hold)
+    H, cap, B = 64, 100, 41
+    emb = _table(3, H)
+    table = rng.integers(0, market.states, cap).astype(np.uint32)
+    table[[7, 19]] = abi.STATE_UNRESTRICTED
+    seq = rng.permutation(cap)[:B].astype(np.uint32)
+    seq[17] = 150                                   # outside the table
+    for e in (7, 19):                               # the unrestricted sequences ride along
+        if e not in seq[:B]:
+            seq[rng.integers(0, 17)] = e
+    unr = np.nonzero(np.isin(seq, [7, 19]))[0].astype(np.uint32)
+    x = _hidden(rng, B, H)
+    w = (1.0 + 0.02 * rng.standard_normal(H)).astype(np.float32)
+    etok, esc, etable = oracle.decode_tail_sequences(
+        x, w, 1e-5, emb, table, seq, market.offsets, market.tokens, state_next=market.next,
+        hold=hold, threads=8)
+
+    dfa = DeviceDfa(market)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    t_emb = dev(emb.view(np.int16))
+    t_x, t_w = dev(x), dev(w)
+    t_state = dev(table.view(np.int32))
+    t_seq = dev(seq.view(np.int32))
+    t_unr = dev(unr.view(np.int32))
+    t_tok = torch.empty(B, dtype=torch.int32, device="cuda")
+    t_sc = torch.empty(B, dtype=torch.float32, device="cuda")
+    D = ops.DeviceBuffer.of
+    b = ops.DecodeTailBuffers(x=D(t_x), embedding=D(t_emb), row_state=D(t_state),
+                              state_offsets=D(dfa.offsets), state_tokens=D(dfa.tokens),
+                              out_token=D(t_tok), norm_weight=D(t_w), state_next=D(dfa.next),
+                              unrestricted_rows=D(t_unr), out_score=D(t_sc),
+                              out_next_state=D(t_state), row_sequence=D(t_seq))
+    a = ops.decode_tail_args(b, rows=B, hidden=H, vocab=VOCAB, states=market.states,
+                             nnz=market.arcs, max_count=market.max_count,
+                             unrestricted_count=unr.size,
+                             flags=abi.TAIL_HOLD_FINISHED if hold else 0)
+    n = ops.decode_tail_workspace_bytes(a)
+    ws_t = torch.zeros(n // 4 + 64, dtype=torch.int32, device="cuda")
+    ws = ops.DeviceBuffer(ws_t.data_ptr() + (-ws_t.data_ptr()) % 256, n)
+    a.workspace = ws.c()
+    torch.cuda.synchronize()           # the uploads above ran on torch's stream
+    stream = torch.cuda.Stream()       # the C ABI rejects the null stream
+    abi.check("init", ops.workspace_init(ws, stream.cuda_stream))
+    abi.check("tail", ops.decode_tail_f16(a, stream.cuda_stream))
+    stream.synchronize()
+    _same(t_tok.cpu().numpy().view(np.uint32), t_sc.cpu().numpy(), etok, esc)
+    assert np.array_equal(t_state.cpu().numpy().view(np.uint32), etable)
+    # entries no row referenced keep their states
+    untouched = np.setdiff1d(np.arange(cap), seq)
+    assert np.array_equal(etable[untouched], table[untouched])
+    if hold:
+        terminal = market.choice[np.minimum(table[seq[seq < cap]], market.states - 1)] != NO_CHOICE
+        assert terminal.any()
+
+
+def test_restricted_decoder_generates_market_actions(market):
+    """64 sequences from the root through the real market grammar, one
+    decode-tail call per step with no host round trip, against the oracle
+    step by step; every sequence ends in a terminal state whose action's
+    token sequence is exactly what was generated."""
+    import torch
+    from market_sim_amd.decode import DeviceDfa, RestrictedDecoder
+    H, B = 576, 64
+    steps = market.depth + 2                 # past every sequence's end
+    emb = _table(5, H)
+    rng = np.random.default_rng(9)
+    w = (1.0 + 0.02 * rng.standard_normal(H)).astype(np.float32)
+    xs = [_hidden(rng, B, H) for _ in range(steps)]
+    dec = RestrictedDecoder(emb, DeviceDfa(market), B, steps, norm_weight=w)
+    dev_x = [torch.from_numpy(x).cuda() for x in xs]
+    dec.start()
+    for x in dev_x:
+        dec.step(x)
+    res = dec.result()
+
+    table = np.zeros(B, np.uint32)
+    for k, x in enumerate(xs):
+        etok, esc, table = oracle.decode_tail_sequences(
+            x, w, 1e-5, emb, table, None, market.offsets, market.tokens,
+            state_next=market.next, hold=True, threads=8)
+        _same(res.tokens[k], res.scores[k], etok, esc)
+    assert np.array_equal(res.states, table)
+    assert res.finished.all()
+    language = cases.market_language()
+    for r in range(B):
+        assert res.generated(r) == language[int(res.choice[r])]
+    # after the end every row emits the invalid token and holds its state
+    assert np.all(res.tokens[-1] == abi.INVALID_TOKEN)
+
+
+def test_restricted_decoder_starts_anywhere_and_reuses_buffers(market):
+    import torch
+    from market_sim_amd.decode import DeviceDfa, RestrictedDecoder
+    H, B = 64, 30
+    emb = _table(6, H)
+    rng = np.random.default_rng(12)
+    start = rng.integers(0, market.states, B).astype(np.uint32)
+    dec = RestrictedDecoder(emb, DeviceDfa(market), B, 4, norm_weight=None)
+    for rep in range(2):
+        xs = [_hidden(rng, B, H) for _ in range(3)]
+        dec.start(start)
+        for x in xs:
+            dec.step(torch.from_numpy(x).cuda())
+        res = dec.result()
+        table = start.copy()
+        for k, x in enumerate(xs):
+            etok, esc, table = oracle.decode_tail_sequences(
+                x, None, 1e-5, emb, table, None, market.offsets, market.tokens,
+                state_next=market.next, hold=True, threads=8)
+            _same(res.tokens[k], res.scores[k], etok, esc)
+        assert np.array_equal(res.states, table)
+
+
+def test_sequence_packer_follows_a_continuous_batching_schedule(market):
+    """Sequences join and leave between batches, batches change membership
+    and order, two sequences are unrestricted; each pack's tokens and the
+    whole state table match the oracle on a host mirror of the table."""
+    import torch
+    from market_sim_amd.decode import BatchItem, DeviceDfa, SequencePacker, WORK_DECODE
+    H = 64
+    emb = _table(7, H)
+    rng = np.random.default_rng(21)
+    w = (1.0 + 0.02 * rng.standard_normal(H)).astype(np.float32)
+    packer = SequencePacker(emb, DeviceDfa(market), capacity=24, max_rows=16, norm_weight=w)
+    mirror = {}                                  # id -> state, the oracle's view
+    unrestricted = {5, 13}
+    next_id = 1
+    live = []
+    for step in range(14):
+        # admissions: up to 3 new sequences per step while there is room
+        for _ in range(int(rng.integers(0, 4))):
+            if packer.resident() < 20:
+                uid = next_id
+                next_id += 1
+                packer.admit(uid, unrestricted=uid in unrestricted)
+                mirror[uid] = abi.STATE_UNRESTRICTED if uid in unrestricted else 0
+                live.append(uid)
+        if not live:
+            continue
+        k = int(rng.integers(1, min(16, len(live)) + 1))
+        ids = [live[i] for i in rng.permutation(len(live))[:k]]
+        items = [BatchItem(i, WORK_DECODE, 10 + step, slot) for slot, i in enumerate(ids)]
+        x = _hidden(rng, k, H)
+        got = packer.run(items, torch.from_numpy(x).cuda())
+        states = np.array([mirror[i] for i in ids], np.uint32)
+        etok, esc, enext = oracle.decode_tail_sequences(
+            x, w, 1e-5, emb, states, None, market.offsets, market.tokens,
+            state_next=market.next, hold=True, threads=8)
+        _same(got.tokens, got.scores, etok, esc)
+        assert np.array_equal(got.states, enext)
+        for i, s in zip(ids, enext):
+            mirror[i] = int(s)
+        # retire finished sequences (the scheduler's complete(..., terminal))
+        for i, term in zip(ids, got.terminal):
+            if term and rng.random() < 0.7:
+                packer.release(i)
+                live.remove(i)
+                del mirror[i]
+    assert np.array_equal(packer.states_of(live), np.array([mirror[i] for i in live], np.uint32))
+
+
+def test_decode_loop_bench_tool(tmp_path, market):
+    """The C++ decode-loop benchmark on the market grammar, few repeats: the
+    device-resident loop, its HIP-graph replay and the per-token round trip
+    give identical tokens, and every sequence finishes."""
+    import json
+    import os
+    import subprocess
+    from market_sim_amd.dfa import write_tables
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    tool = os.path.join(root, "market_sim_amd", "bench", "_build", "decode_loop_bench")
+    assert os.path.exists(tool), "market_sim_amd/bench is not built: run __graft_entry__.build()"
+    path = str(tmp_path / "market.dfa")
+    write_tables(market, path)
+    r = subprocess.run([tool, "--dfa", path, "--rows", "48", "--repeats", "3"],
+                       capture_output=True, text=True, timeout=180)
+    assert r.returncode == 0, r.stdout + r.stderr
+    doc = json.loads(r.stdout)
+    assert doc["finished_rows"] == 48 and doc["steps"] == market.depth
+    assert doc["graph_ok"] and doc["graph_token_parity"]
+    assert doc["round_trip_token_parity"] and doc["resident_repeatable"]

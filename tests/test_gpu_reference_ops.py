@@ -219,3 +219,23 @@ def _ordered(bits: np.ndarray) -> np.ndarray:
     floats across the sign boundary."""
     b = bits.astype(np.int32)
     return np.where(b & 0x8000, -(b & 0x7FFF), b)
+
+
+@pytest.mark.gpu
+def test_reference_output_head_benchmark_tool():
+    """The reference's 12-cell output-head benchmark, run by the C++ tool with
+    shortened iteration counts: a schema-valid document with token parity
+    between the full and the restricted head in every cell."""
+    import json
+    import os
+    import subprocess
+    from market_sim_amd import schema
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    tool = os.path.join(root, "market_sim_amd", "bench", "_build", "restricted_output_head_bench")
+    assert os.path.exists(tool), "market_sim_amd/bench is not built: run __graft_entry__.build()"
+    r = subprocess.run([tool, "--iterations-divisor", "50"], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 0, r.stderr
+    doc = json.loads(r.stdout)
+    schema.check_output_head_benchmark(doc)
+    assert all(m["exact_token_parity"] for m in doc["measurements"])

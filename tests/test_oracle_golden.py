@@ -316,11 +316,20 @@ def test_market_dfa_fixture_matches_reference_build():
     offsets, tokens, nxt = cases.market_dfa()
     cap = 8192
     o = np.zeros(cap, np.uint32); t = np.zeros(cap, np.uint32); n = np.zeros(cap, np.uint32)
+    term = np.zeros(cap, np.uint32)
     ns, na = ctypes.c_uint32(), ctypes.c_uint32()
     assert r.mfref_market_dfa_export(o.ctypes.data, t.ctypes.data, n.ctypes.data,
-                                     cap, cap, ctypes.byref(ns), ctypes.byref(na)) == 0
+                                     term.ctypes.data, cap, cap, ctypes.byref(ns),
+                                     ctypes.byref(na)) == 0
     assert np.array_equal(o[:ns.value + 1], offsets)
     assert np.array_equal(t[:na.value], tokens) and np.array_equal(n[:na.value], nxt)
+    assert np.array_equal(term[:ns.value], cases.market_dfa_terminal())
+    lo = np.zeros(4096, np.uint32); lt = np.zeros(65536, np.uint32)
+    ne, nt = ctypes.c_uint32(), ctypes.c_uint32()
+    assert r.mfref_market_language(lo.ctypes.data, lt.ctypes.data, 4096, 65536,
+                                   ctypes.byref(ne), ctypes.byref(nt)) == 0
+    lang = [lt[lo[i]:lo[i + 1]].tolist() for i in range(ne.value)]
+    assert lang == cases.market_language()
 
 
 # -------------------------------------------------------- decode tail ------
