@@ -78,15 +78,20 @@ float dot_bound_coef(uint64_t H) {
   return static_cast<float>(4.0 * g / (1.0 - g) + std::ldexp(1.0, -20));
 }
 
-// MFMA score (hi + lo split of y, exact FP16 products, 2H FP32 additions with
-// up to one ulp each) vs reference order, bounded through ||y|| ||e||:
-//   |g - r| <= (gamma_H + 1.001 gamma'_2H + 2^-22) ||y|| ||e||
-//              + 2^-25 sqrt(H) ||e||        (FP16 residual of small y)
-// doubled for safety.
+// MFMA score g on z = x * w (hi + lo FP16 split, exact FP16 products, 2H FP32
+// additions with up to one ulp each) against the reference-order score r on
+// y = (x * inv) * w, in the scale of z (inv > 0 orders both alike):
+//   |g - S_z|         <= (1.001 gamma'_2H + 2^-22) ||z|| ||e|| + 2^-25 sqrt(H) ||e||
+//   |S_y / inv - S_z| <= 3.0001 u ||z|| ||e||   (y_f / inv and z_f differ by
+//                                               three roundings, u = 2^-24)
+//   |r - S_y| / inv   <= gamma_H (1 + 3.0001 u) ||z|| ||e||
+// (S_v = the exact dot product of v with e; Sum |y e| / inv <= (1 + 3.0001 u)
+// ||z|| ||e||), doubled for safety.  Without a norm weight z = y and inv = 1.
 void mfma_bound_coefs(uint64_t H, float& coef, float& coef2) {
   const double h = static_cast<double>(H);
-  const double c = gamma(h, std::ldexp(1.0, -24)) + 1.001 * gamma(2.0 * h, std::ldexp(1.0, -23)) +
-                   std::ldexp(1.0, -22);
+  const double u = std::ldexp(1.0, -24);
+  const double c = gamma(h, u) * (1.0 + 4.0 * u) + 4.0 * u +
+                   1.001 * gamma(2.0 * h, std::ldexp(1.0, -23)) + std::ldexp(1.0, -22);
   coef = static_cast<float>(2.0 * c + std::ldexp(1.0, -20));
   coef2 = static_cast<float>(2.0 * std::ldexp(1.0, -25) * std::sqrt(h));
 }
@@ -94,6 +99,14 @@ void mfma_bound_coefs(uint64_t H, float& coef, float& coef2) {
 // Absolute term for underflow: each of up to 2H operations may lose 2^-126.
 float underflow_slack(uint64_t H) {
   return static_cast<float>(4.0 * static_cast<double>(H) * std::ldexp(1.0, -126));
+}
+
+// The underflow of the reference score and of y, per unit of 1 / inv (the
+// norm kernel multiplies it by its bound of 1 / inv): the chain's 2H
+// operations, and two roundings of each y_f against |e_f| <= 65504.
+float scaled_slack(uint64_t H) {
+  const double h = static_cast<double>(H);
+  return static_cast<float>(4.0 * h * std::ldexp(1.0, -126) + 2.0 * h * 65504.0 * std::ldexp(1.0, -148));
 }
 
 // Compute units of the current device (cached per device id).
@@ -453,8 +466,8 @@ namespace {
 constexpr uint32_t kFullTile = 256;  // selection over projected scores
 
 struct TailLayout {
-  uint64_t y, row_norm, row_meta, y_hi, y_lo, fb_map, records, fb_records, fb_panel,
-      fb_slot_row, fb_slot_norm, scores, tok_norm, total;
+  uint64_t y, row_inv, row_norm, row_slack, row_meta, y_hi, y_lo, fb_map, records, fb_records,
+      fb_panel, fb_slot_row, fb_slot_norm, fb_slot_slack, scores, tok_norm, total;
   uint32_t tile, max_tiles, fb_tiles, fb_rows;
 };
 
@@ -563,7 +576,9 @@ mf_status validate_tail(const mf_decode_tail_args* a, bool full, TailLayout& L) 
     return at;
   };
   L.y = take(xe * 4u);
+  L.row_inv = take(rows * 4u);
   L.row_norm = take(rows * 4u);
+  L.row_slack = take(rows * 4u);
   L.row_meta = take(rows * sizeof(mf::RowMeta));
   const bool split = full || mfma_gather(a->hidden);
   L.y_hi = take(split ? xe * 2u : 0u);
@@ -575,6 +590,7 @@ mf_status validate_tail(const mf_decode_tail_args* a, bool full, TailLayout& L) 
                     mf::panel_tile_bytes(a->hidden));
   L.fb_slot_row = take(fb_rows * 4u);
   L.fb_slot_norm = take(fb_rows * 4u);
+  L.fb_slot_slack = take(fb_rows * 4u);
   L.scores = take(full ? rows * a->vocab * 4u : 0u);
   L.tok_norm = take(full ? a->vocab * 4u : 0u);
   L.total = off;
@@ -599,7 +615,11 @@ mf::TailNormArgs norm_args(const mf_decode_tail_args* a, const TailLayout& L, ch
   n.weight = ptr<const float>(a->norm_weight.address);
   n.epsilon = a->epsilon;
   n.y = reinterpret_cast<float*>(ws + L.y);
+  n.row_inv = reinterpret_cast<float*>(ws + L.row_inv);
   n.row_norm = reinterpret_cast<float*>(ws + L.row_norm);
+  n.row_slack = reinterpret_cast<float*>(ws + L.row_slack);
+  n.slack = underflow_slack(a->hidden);
+  n.slack_scaled = scaled_slack(a->hidden);
   n.y_hi = split ? reinterpret_cast<uint16_t*>(ws + L.y_hi) : nullptr;
   n.y_lo = split ? reinterpret_cast<uint16_t*>(ws + L.y_lo) : nullptr;
   n.row_state = ptr<const uint32_t>(a->row_state.address);
@@ -623,6 +643,7 @@ mf::TailNormArgs norm_args(const mf_decode_tail_args* a, const TailLayout& L, ch
     n.fb_panel = reinterpret_cast<uint16_t*>(ws + L.fb_panel);
     n.fb_slot_row = reinterpret_cast<uint32_t*>(ws + L.fb_slot_row);
     n.fb_slot_norm = reinterpret_cast<float*>(ws + L.fb_slot_norm);
+    n.fb_slot_slack = reinterpret_cast<float*>(ws + L.fb_slot_slack);
   }
   return n;
 }
@@ -640,6 +661,8 @@ mf::GatherArgs gather_args(const mf_decode_tail_args* a, const TailLayout& L, ch
   g.tile = L.tile;
   g.max_tiles = L.max_tiles;
   g.slack = underflow_slack(a->hidden);
+  // the MFMA gather and the comparator's lookup bound scores on z per row
+  g.row_slack = reinterpret_cast<const float*>(ws + L.row_slack);
   // persistent workgroups: the launcher multiplies by the resident count
   g.groups = device_cus();
   return g;
@@ -649,6 +672,9 @@ mf::FinalizeArgs finalize_args(const mf_decode_tail_args* a, const TailLayout& L
                                bool full) {
   mf::FinalizeArgs f{};
   f.y = reinterpret_cast<const float*>(ws + L.y);
+  // the MFMA gather, the MFMA head and the comparator's GEMMs score z
+  f.row_inv = (full || mfma_gather(a->hidden)) ? reinterpret_cast<const float*>(ws + L.row_inv)
+                                              : nullptr;
   f.emb = ptr<const uint16_t>(a->embedding.address);
   f.tokens = ptr<const uint32_t>(a->state_tokens.address);
   f.row_meta = reinterpret_cast<const mf::RowMeta*>(ws + L.row_meta);
@@ -680,6 +706,7 @@ mf::FallbackArgs fallback_args(const mf_decode_tail_args* a, const TailLayout& L
   f.panel = reinterpret_cast<const uint16_t*>(ws + L.fb_panel);
   f.slot_row = reinterpret_cast<const uint32_t*>(ws + L.fb_slot_row);
   f.slot_norm = reinterpret_cast<const float*>(ws + L.fb_slot_norm);
+  f.slot_slack = reinterpret_cast<const float*>(ws + L.fb_slot_slack);
   f.m = static_cast<uint32_t>(a->unrestricted_count);
   f.emb = ptr<const uint16_t>(a->embedding.address);
   f.H = static_cast<uint32_t>(a->hidden);
@@ -687,7 +714,6 @@ mf::FallbackArgs fallback_args(const mf_decode_tail_args* a, const TailLayout& L
   f.records = reinterpret_cast<mf::TileRecord*>(ws + L.fb_records);
   f.fb_map = reinterpret_cast<uint32_t*>(ws + L.fb_map);
   mfma_bound_coefs(a->hidden, f.coef, f.coef2);
-  f.slack = underflow_slack(a->hidden);
   f.groups = device_cus();
   return f;
 }

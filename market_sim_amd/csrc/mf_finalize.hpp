@@ -162,6 +162,18 @@ __device__ __forceinline__ uint32_t collect_members(const TileRecord* recs, uint
   return overflow;
 }
 
+// A lower bound, in the scale of the row's records, of the exact score s:
+// s itself for records scored on y, else s / inv rounded down (the division
+// is within half an ulp; the margins cover it and subnormal quotients).  No
+// bound (-inf) when inv or the quotient is not a positive finite number.
+__device__ __forceinline__ float records_lower(const FinalizeArgs& a, uint32_t r, float s) {
+  if (a.row_inv == nullptr) return s;
+  const float inv = a.row_inv[r];
+  const float q = s / inv;
+  if (!(inv > 0.0f) || !__builtin_isfinite(q)) return -__builtin_huge_valf();
+  return q - __builtin_fabsf(q) * 0x1p-20f - 0x1p-126f;
+}
+
 // Finalizes row r (meta = its metadata) with one wave.  ys_ready: L.ys
 // already holds the row's normalized hidden vector (otherwise it is loaded
 // from a.y).  Writes token, score and next state of the row; rows that are
@@ -270,7 +282,7 @@ __device__ inline void finalize_row(const FinalizeArgs& a, uint32_t r, const Row
         best = best_of(best, rescore_candidates(a, L, n));
       }
     }
-    if (best.token != kInvalidToken) lg = __builtin_fmaxf(lg, best.score);
+    if (best.token != kInvalidToken) lg = __builtin_fmaxf(lg, records_lower(a, r, best.score));
   }
 
   // ordinary tiles: members whose upper bound reaches lg (at most

@@ -5,9 +5,10 @@
 // the granularity of the window records the finalize kernel merges.  It
 // scores them 16 at a time with v_mfma_f32_16x16x32_f16:
 //
-//   scores  A = [y_hi; y_lo; 0 ...] (16 x 32)  x  B = 16 embedding rows
-//           -> D[0][t] + D[1][t] = y . e_t with the FP32 y split into the
-//              FP16 pair hi = rne(y), lo = rne(y - hi)
+//   scores  A = [z_hi; z_lo; 0 ...] (16 x 32)  x  B = 16 embedding rows
+//           -> D[0][t] + D[1][t] = z . e_t with z = x * w (the normalized
+//              row up to its positive factor inv) split into the FP16 pair
+//              hi = rne(z), lo = rne(z - hi)
 //   norms   A = B = the same 16 embedding rows
 //           -> the Gram diagonal D[t][t] = ||e_t||^2 (FP16 products are exact
 //              in FP32), which bounds the error of both the fast score and
@@ -104,6 +105,7 @@ __device__ void mfma_tile(const GatherArgs& a, uint32_t r, uint32_t k, uint32_t 
   const uint32_t id = a.tokens[list_begin + begin + (live ? lane : n - 1)];
   const uint32_t t = live ? id : 0u;
   const float yn = a.row_norm[r];
+  const float row_slack = a.row_slack[r];
   TileRecord* rec = a.records + static_cast<uint64_t>(r) * a.max_tiles + k;
   if (__ballot(live && t >= a.V) != 0ull) {
     // an id outside the vocabulary: the row's result is the invalid sentinel
@@ -205,10 +207,11 @@ __device__ void mfma_tile(const GatherArgs& a, uint32_t r, uint32_t k, uint32_t 
   }
 
   // window summary of the tile (the candidate of lane l is list position
-  // begin + l); the bound is |g - r| <= ||e|| (coef ||y|| + coef2) + slack
+  // begin + l); the bound is |g - r / inv| <= ||e|| (coef ||z|| + coef2) +
+  // the row's slack, r the reference-order score
   const float tn = __fsqrt_rn(sq_mine) * (1.0f + 0x1p-7f);
   const float g = g_mine;
-  const float b = __builtin_fmaf(tn, __builtin_fmaf(a.coef, yn, a.coef2), a.slack);
+  const float b = __builtin_fmaf(tn, __builtin_fmaf(a.coef, yn, a.coef2), row_slack);
   const bool fin = !live || (__builtin_isfinite(g) && __builtin_isfinite(b) && b < 0x1p100f);
   const bool all_finite = __ballot(!fin) == 0ull;
   const float L = wave_max(live ? g - b : -__builtin_huge_valf());
@@ -298,7 +301,7 @@ hipError_t launch_variant(const GatherArgs& a, hipStream_t stream) {
 
 hipError_t launch_gather_mfma(const GatherArgs& a, hipStream_t stream) {
   if (a.H == 0 || a.H % kStep != 0 || a.tile != kGatherWaveTile || a.y_hi == nullptr ||
-      a.y_lo == nullptr || a.row_norm == nullptr) {
+      a.y_lo == nullptr || a.row_norm == nullptr || a.row_slack == nullptr) {
     return hipErrorInvalidValue;
   }
   const uint32_t steps = a.H / kStep;

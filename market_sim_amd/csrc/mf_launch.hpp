@@ -79,9 +79,15 @@ struct TailNormArgs {
   const float* weight;     // [H] or null (x already normalized)
   float epsilon;
   float* y;                // [rows, H] reference-order normalized hidden
-  float* row_norm;         // [rows] upper bound of ||y||
-  uint16_t* y_hi;          // [rows, H] FP16 split hi = rne(y), lo = rne(y - hi) (or null)
+  float* row_inv;          // [rows] the reference's 1 / sqrt(mean + eps) (1: no norm)
+  // The fast scores use z = x * w (x without a weight): the normalized row
+  // up to the positive per-row factor inv, which orders scores alike.
+  float* row_norm;         // [rows] upper bound of ||z||
+  float* row_slack;        // [rows] absolute error term of the row's bounds
+  uint16_t* y_hi;          // [rows, H] FP16 split of z: hi = rne(z), lo = rne(z - hi) (or null)
   uint16_t* y_lo;
+  float slack;             // absolute term of the fast score itself
+  float slack_scaled;      // absolute term of the reference score, per unit of 1 / inv
   const uint32_t* row_state;
   const uint32_t* offsets;
   uint32_t states;
@@ -109,6 +115,7 @@ struct TailNormArgs {
   uint16_t* fb_panel;      // [panel_tiles(fb_m)] x panel_tile_bytes(H)
   uint32_t* fb_slot_row;   // [fb_m]
   float* fb_slot_norm;     // [fb_m]
+  float* fb_slot_slack;    // [fb_m]
 };
 
 // Panel of the MFMA head: per tile of kPanelRows slots, the slots' FP16
@@ -130,7 +137,8 @@ struct GatherArgs {
   const uint16_t* y_lo;
   const uint16_t* emb;     // [V, H]
   const float* scores;     // [rows, V] (lookup)
-  const float* row_norm;   // (lookup, MFMA)
+  const float* row_norm;   // (lookup, MFMA) bound of ||z||
+  const float* row_slack;  // (lookup, MFMA) the row's absolute error term
   const float* tok_norm;   // (lookup)
   const uint32_t* tokens;  // state lists
   const RowMeta* row_meta;
@@ -148,6 +156,9 @@ struct GatherArgs {
 
 struct FinalizeArgs {
   const float* y;
+  // records scored on z = x * w (row_inv given) or on y (null); exact
+  // scores tighten a window only after conversion to the records' scale
+  const float* row_inv;
   const uint16_t* emb;
   const uint32_t* tokens;
   const RowMeta* row_meta;
@@ -215,7 +226,8 @@ hipError_t launch_projection(const ProjArgs& args, hipStream_t stream);
 struct FallbackArgs {
   const uint16_t* panel;    // the norm kernel's panel of the m unrestricted rows
   const uint32_t* slot_row; // [m] source row of each slot (kInvalidToken: none)
-  const float* slot_norm;   // [m] norm bound of each slot's row
+  const float* slot_norm;   // [m] bound of ||z|| of each slot's row
+  const float* slot_slack;  // [m] absolute error term of each slot's row
   uint32_t m;
   const uint16_t* emb;
   uint32_t H;
@@ -224,9 +236,8 @@ struct FallbackArgs {
   uint32_t* fb_map;         // [rows] written: row -> slot
   uint32_t groups;          // compute units: workgroups per M-tile
   uint32_t tiles_per_group; // set by the launcher
-  float coef;               // b = ||e|| * (coef * ||y|| + coef2) + slack
+  float coef;               // b = ||e|| * (coef * ||z|| + coef2) + slot slack
   float coef2;
-  float slack;
 };
 
 uint32_t fallback_tiles(uint32_t vocab);

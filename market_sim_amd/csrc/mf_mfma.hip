@@ -296,15 +296,18 @@ struct HeadAcc {
 // for slots past m or without a row) and norm bound; block column 0 also
 // records row -> slot for the finalize kernel.  Straight-line loads.
 __device__ __forceinline__ void head_slots(const FallbackArgs& f, uint32_t m0,
-                                           uint32_t* src_row, float* src_norm) {
+                                           uint32_t* src_row, float* src_norm,
+                                           float* src_slack) {
   if (threadIdx.x < kMTile) {
     const uint32_t i = m0 + threadIdx.x;
     const uint32_t at = i < f.m ? i : f.m - 1u;
     const uint32_t row = f.slot_row[at];
     const float norm = f.slot_norm[at];
+    const float slack = f.slot_slack[at];
     const uint32_t r = i < f.m ? row : kInvalidToken;
     src_row[threadIdx.x] = r;
     src_norm[threadIdx.x] = r != kInvalidToken ? norm : 0.0f;
+    src_slack[threadIdx.x] = r != kInvalidToken ? slack : 0.0f;
     if (blockIdx.x == 0 && r != kInvalidToken && f.fb_map != nullptr) f.fb_map[r] = i;
   }
 }
@@ -330,7 +333,7 @@ __device__ __forceinline__ float lane8_max(float v) {
 // acc[rb][tb][2 jj + 1]; the Gram diagonal of column c sits in lane
 // c + 16 (c / 4), element c % 4.
 //
-// One bound per slot and tile: b = tn_max (coef ||y|| + coef2) + slack with
+// One bound per slot and tile: b = tn_max (coef ||z|| + coef2) + slack with
 // tn_max the largest token-norm bound of the tile, which is at least every
 // token's own bound.  Then the best lower bound is L = fl(max g - b) (the
 // rounding is monotone) and a token is a member when fl(g + b) >= L.  The
@@ -341,7 +344,8 @@ __device__ __forceinline__ float lane8_max(float v) {
 template <int kWaves, int kBlocks>
 __device__ __forceinline__ void head_records(const FallbackArgs& f, const HeadAcc<kBlocks>& h,
                                              HeadEpi& epi, const uint32_t* src_row,
-                                             const float* src_norm, uint32_t m0, uint32_t tile,
+                                             const float* src_norm, const float* src_slack,
+                                             uint32_t m0, uint32_t tile,
                                              uint32_t tiles) {
   static_assert(kWaves == kEpiWaves && kMTile == 8 * kWaves, "eight slots per wave");
   const uint32_t lane = threadIdx.x % 64;
@@ -415,7 +419,7 @@ __device__ __forceinline__ void head_records(const FallbackArgs& f, const HeadAc
   const uint64_t fin_lanes = __ballot(__builtin_isfinite(sum));
   const bool slot_finite = ((fin_lanes >> (8u * sl)) & 0xFFull) == 0xFFull;
   const float G = lane8_max(gm);
-  const float bs = __builtin_fmaf(tn_max, __builtin_fmaf(f.coef, src_norm[i], f.coef2), f.slack);
+  const float bs = __builtin_fmaf(tn_max, __builtin_fmaf(f.coef, src_norm[i], f.coef2), src_slack[i]);
   const float L = G - bs;
   uint32_t members = 0u;  // bit k: token t0 + k
 #pragma unroll
@@ -476,6 +480,7 @@ __global__ __launch_bounds__(kWaves * 64) void vocab_head_lds_kernel(FallbackArg
   extern __shared__ __align__(16) unsigned char dyn[];
   __shared__ uint32_t src_row[kMTile];
   __shared__ float src_norm[kMTile];
+  __shared__ float src_slack[kMTile];
   HeadEpi& epi = *reinterpret_cast<HeadEpi*>(dyn);
   uint16_t* stage = reinterpret_cast<uint16_t*>(dyn + sizeof(HeadEpi));
   const uint32_t m0 = blockIdx.y * kMTile;
@@ -502,7 +507,7 @@ __global__ __launch_bounds__(kWaves * 64) void vocab_head_lds_kernel(FallbackArg
     }
   };
   load_tile(t_begin);
-  head_slots(f, m0, src_row, src_norm);
+  head_slots(f, m0, src_row, src_norm, src_slack);
   wait_vector_memory();
   __syncthreads();
   const uint16_t* a_lane = stage + col * kRowHalves + kb * 8u;
@@ -549,7 +554,7 @@ __global__ __launch_bounds__(kWaves * 64) void vocab_head_lds_kernel(FallbackArg
 #pragma unroll
       for (int rb = 0; rb < 4; ++rb) a_cur[rb] = a_nxt[rb];
     }
-    head_records<kWaves, kBlocks>(f, h, epi, src_row, src_norm, m0, tile, tiles);
+    head_records<kWaves, kBlocks>(f, h, epi, src_row, src_norm, src_slack, m0, tile, tiles);
   }
 }
 
@@ -617,6 +622,7 @@ __global__ __launch_bounds__(kWideWaves * 64) void vocab_head_wide_kernel(Fallba
   extern __shared__ __align__(16) unsigned char dyn[];
   __shared__ uint32_t src_row[kMTile];
   __shared__ float src_norm[kMTile];
+  __shared__ float src_slack[kMTile];
   HeadEpi& epi = *reinterpret_cast<HeadEpi*>(dyn);
   const uint32_t m0 = blockIdx.y * kMTile;
   const uint32_t tiles = (f.V + kHeadTileTokens - 1) / kHeadTileTokens;
@@ -631,7 +637,7 @@ __global__ __launch_bounds__(kWideWaves * 64) void vocab_head_wide_kernel(Fallba
   const uint16_t* panel = f.panel + static_cast<uint64_t>(blockIdx.y) * (panel_tile_bytes(H) / 2u);
   const uint32_t units = H / (32 * KC);
   constexpr uint32_t kUnitF = 32 * KC;
-  head_slots(f, m0, src_row, src_norm);
+  head_slots(f, m0, src_row, src_norm, src_slack);
   __syncthreads();
   const uint16_t* aptr[4];
   uint32_t amask[4];
@@ -675,7 +681,8 @@ __global__ __launch_bounds__(kWideWaves * 64) void vocab_head_wide_kernel(Fallba
     } else {
       unit_mma<KC>(u0, amask, h);
     }
-    head_records<kWideWaves, kWideBlocks>(f, h, epi, src_row, src_norm, m0, tile, tiles);
+    head_records<kWideWaves, kWideBlocks>(f, h, epi, src_row, src_norm, src_slack, m0, tile,
+                                          tiles);
   }
 }
 

@@ -155,7 +155,8 @@ __global__ __launch_bounds__(kWave) void tail_norm_kernel(TailNormArgs a) {
       b = a.offsets[s];
       e = a.offsets[s + 1];
     }
-    if (weighted) {
+    // the reference-order chain: rows only (a slot needs z, not y)
+    if (weighted && !slot) {
       const float sum_squares = sequential_sum(sq, H);
       const float mean = div_rn(sum_squares, static_cast<float>(H));
       inverse_shared = div_rn(1.0f, sqrt_rn(mean + a.epsilon));
@@ -183,7 +184,7 @@ __global__ __launch_bounds__(kWave) void tail_norm_kernel(TailNormArgs a) {
     }
   }
   __syncthreads();
-  const float inverse = inverse_shared;
+  const float inverse = (weighted && !slot) ? inverse_shared : 1.0f;
   const bool split = a.y_hi != nullptr;
   // slot workgroups: the slot's [hi | lo] rows of the panel
   uint16_t* panel_hi = nullptr;
@@ -191,21 +192,29 @@ __global__ __launch_bounds__(kWave) void tail_norm_kernel(TailNormArgs a) {
     panel_hi = a.fb_panel + static_cast<uint64_t>(j / kPanelRows) * (panel_tile_bytes(H) / 2u) +
                static_cast<uint64_t>(j % kPanelRows) * 2u * (H + kPanelPad);
   }
+  // y = (x * inv) * w in the reference's roundings (operators.cpp:533-534)
+  // for the rescore; z = x * w, the fast scores' operand, split into FP16
+  // hi + lo.  z differs from y / inv by at most 3 roundings per element.
   float norm_sq = 0.0f;
+  float x_sq = 0.0f;
   for (uint32_t c = lane; c < H; c += kWave) {
-    float v = xs[c];
+    const float xv = xs[c];
+    float yv = xv;
+    float zv = xv;
     if (weighted) {
-      const float scaled = v * inverse;
-      v = scaled * ws[c];
+      const float scaled = xv * inverse;
+      yv = scaled * ws[c];
+      zv = xv * ws[c];
+      x_sq += sq[c];
     }
-    norm_sq = __builtin_fmaf(v, v, norm_sq);
-    const _Float16 hi = static_cast<_Float16>(v);
-    const uint16_t lo = float_to_half_rne(v - static_cast<float>(hi));
+    norm_sq = __builtin_fmaf(zv, zv, norm_sq);
+    const _Float16 hi = static_cast<_Float16>(zv);
+    const uint16_t lo = float_to_half_rne(zv - static_cast<float>(hi));
     if (slot) {
       panel_hi[c] = __builtin_bit_cast(uint16_t, hi);
       panel_hi[H + kPanelPad + c] = lo;
     } else {
-      a.y[r * H + c] = v;
+      a.y[r * H + c] = yv;
       if (split) {
         a.y_hi[r * H + c] = __builtin_bit_cast(uint16_t, hi);
         a.y_lo[r * H + c] = lo;
@@ -213,15 +222,31 @@ __global__ __launch_bounds__(kWave) void tail_norm_kernel(TailNormArgs a) {
     }
   }
   norm_sq = wave_sum_f32(norm_sq);
+  x_sq = wave_sum_f32(x_sq);
   if (lane == 0) {
     // FP32 sum of H squares is within a relative H 2^-24 of the exact value;
     // the factor covers that and the sqrt for any H <= 2^16
     const float bound = __fsqrt_rn(norm_sq) * (1.0f + 0x1p-7f);
+    // an upper bound of 1 / inv: the reference sums the same rounded
+    // squares in another order (relative H 2^-23 apart at most, H <= 8192),
+    // then divides, adds eps, takes the square root and the reciprocal
+    // (a few roundings); 2^-9 margins cover all of them.  An infinite or NaN
+    // value (overflowing or non-finite x) makes every bound of the row
+    // infinite, and the row is then rescored in full.
+    float slack = a.slack;
+    if (weighted) {
+      const float scale =
+          __fsqrt_rn(x_sq * (1.0f + 0x1p-9f) / static_cast<float>(H) + a.epsilon) * (1.0f + 0x1p-9f);
+      slack = __builtin_fmaf(scale, a.slack_scaled, a.slack);
+    }
     if (slot) {
       a.fb_slot_norm[j] = bound;
+      a.fb_slot_slack[j] = slack;
       a.fb_slot_row[j] = static_cast<uint32_t>(r);
     } else {
       a.row_norm[r] = bound;
+      a.row_slack[r] = slack;
+      a.row_inv[r] = inverse;
     }
   }
 }
@@ -329,10 +354,11 @@ __device__ void gather_scores_lookup(const GatherArgs& a, uint32_t r, GatherShar
                                      uint32_t n) {
   const float* srow = a.scores + static_cast<uint64_t>(r) * a.V;
   const float yn = a.row_norm[r];
+  const float row_slack = a.row_slack[r];
   for (uint32_t c = threadIdx.x; c < n; c += kThreads) {
     const uint32_t t = sh.tk[c];
     sh.sc[c] = srow[t];
-    sh.bd[c] = __builtin_fmaf(a.tok_norm[t], __builtin_fmaf(a.coef, yn, a.coef2), a.slack);
+    sh.bd[c] = __builtin_fmaf(a.tok_norm[t], __builtin_fmaf(a.coef, yn, a.coef2), row_slack);
   }
 }
 

@@ -157,6 +157,33 @@ def test_exact_ties_pick_the_lowest_id():
         assert got[0][r] == lowest
 
 
+@pytest.mark.parametrize("order", [abi.ORDER_FMA_CHAIN, abi.ORDER_MUL_ADD_CHAIN])
+def test_extreme_row_scales_and_near_ties(order):
+    """The fast scores use x * w and leave the norm's positive factor to the
+    rescore; rows scaled from 1e-20 to 1e18 (the norm then cancels the scale,
+    up to its eps), with near-tied candidates (pairs of embedding rows one
+    FP16 ulp apart) and unrestricted rows, must still select exactly."""
+    w = wl.config(3, seed=31, scale_vocab=8192, scale_rows=60)
+    w.embedding = w.embedding.copy()
+    rng = np.random.default_rng(5)
+    for r in range(w.rows):
+        s = int(w.row_state[r])
+        if s >= w.states:
+            continue
+        ids = w.state_tokens[w.state_offsets[s]:w.state_offsets[s + 1]]
+        if ids.size >= 2:
+            # the second id becomes the first one's row nudged by one ulp in
+            # a single feature
+            a, b = int(ids[0]), int(ids[1])
+            w.embedding[b] = w.embedding[a]
+            f = int(rng.integers(0, w.hidden))
+            w.embedding[b, f] = w.embedding[b, f] + 1
+    scales = np.array([1e-20, 1e-6, 1.0, 1e6, 1e18], np.float32)
+    w.x = (w.x * scales[np.arange(w.rows) % scales.size][:, None]).astype(np.float32)
+    got = _run(w, order=order)
+    _same(got, _oracle(w, order=order))
+
+
 def test_workspace_reuse_across_calls_and_shapes():
     """Arrival counters reset themselves: repeated calls on one workspace
     give identical results."""
