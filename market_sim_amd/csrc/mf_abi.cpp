@@ -607,8 +607,16 @@ mf_status check_workspace(const mf_decode_tail_args* a, const TailLayout& L) {
 
 enum class Stage { kPrepare, kRestricted, kUnrestricted, kFinalize };
 
+// The norm's reference-order chains run in the gather launch (next to the
+// MFMA gather, which scores z and does not need y) when the gather plans its
+// tiles; otherwise in the norm kernel.
+bool defer_chain(const mf_decode_tail_args* a) {
+  return mfma_gather(a->hidden) && a->rows <= mf::kPlanRowsMax && a->norm_weight.address != 0 &&
+         (a->hidden % 4u) == 0;
+}
+
 mf::TailNormArgs norm_args(const mf_decode_tail_args* a, const TailLayout& L, char* ws,
-                           bool split) {
+                           bool split, bool chain) {
   mf::TailNormArgs n{};
   n.rows = static_cast<uint32_t>(a->rows);
   n.x = ptr<const float>(a->x.address);
@@ -620,6 +628,7 @@ mf::TailNormArgs norm_args(const mf_decode_tail_args* a, const TailLayout& L, ch
   n.row_slack = reinterpret_cast<float*>(ws + L.row_slack);
   n.slack = underflow_slack(a->hidden);
   n.slack_scaled = scaled_slack(a->hidden);
+  n.chain = chain ? 1u : 0u;
   n.y_hi = split ? reinterpret_cast<uint16_t*>(ws + L.y_hi) : nullptr;
   n.y_lo = split ? reinterpret_cast<uint16_t*>(ws + L.y_lo) : nullptr;
   n.row_state = ptr<const uint32_t>(a->row_state.address);
@@ -731,7 +740,7 @@ mf_status decode_tail_stage(const mf_decode_tail_args* args, uintptr_t stream, S
   hipError_t e = hipSuccess;
   switch (stage) {
     case Stage::kPrepare:
-      e = mf::launch_tail_norm(norm_args(a, L, ws, mfma_gather(a->hidden)), s);
+      e = mf::launch_tail_norm(norm_args(a, L, ws, mfma_gather(a->hidden), !defer_chain(a)), s);
       break;
     case Stage::kRestricted: {
       mf::GatherArgs g = gather_args(a, L, ws);
@@ -740,6 +749,14 @@ mf_status decode_tail_stage(const mf_decode_tail_args* args, uintptr_t stream, S
         g.y_lo = reinterpret_cast<const uint16_t*>(ws + L.y_lo);
         g.row_norm = reinterpret_cast<const float*>(ws + L.row_norm);
         mfma_bound_coefs(a->hidden, g.coef, g.coef2);
+        if (defer_chain(a)) {
+          g.x = ptr<const float>(a->x.address);
+          g.weight = ptr<const float>(a->norm_weight.address);
+          g.epsilon = a->epsilon;
+          g.y_out = reinterpret_cast<float*>(ws + L.y);
+          g.inv_out = reinterpret_cast<float*>(ws + L.row_inv);
+          g.chain_rows = static_cast<uint32_t>(a->rows);
+        }
         e = mf::launch_gather_mfma(g, s);
       } else {
         g.coef = dot_bound_coef(a->hidden);
@@ -825,7 +842,7 @@ mf_status mf_decode_tail_full_f16(const mf_decode_tail_args* args, uintptr_t str
   float* tok_norm = reinterpret_cast<float*>(ws + L.tok_norm);
 
   // 1. final RMSNorm (and its FP16 split for the MFMA projection)
-  hipError_t e = mf::launch_tail_norm(norm_args(a, L, ws, true), s);
+  hipError_t e = mf::launch_tail_norm(norm_args(a, L, ws, true, true), s);
   if (e != hipSuccess) return launch_status(e);
   // 2. full output projection of every row: FP32 scores [rows, V] as two
   // FP16 GEMMs of the hidden split (hi, then lo accumulated) on rocBLAS --

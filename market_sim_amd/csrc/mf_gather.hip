@@ -22,8 +22,11 @@
 // unit's MFMAs run, and waves never wait on one another.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
+
 #include "mf_device.hpp"
 #include "mf_launch.hpp"
+#include "mf_norm.hpp"
 #include "mf_plan.hpp"
 
 namespace mf {
@@ -237,17 +240,51 @@ __device__ void mfma_tile(const GatherArgs& a, uint32_t r, uint32_t k, uint32_t 
   }
 }
 
+// LDS of a chain workgroup: the weight [H], one inv per wave (4 floats), then
+// per wave x and its squares [2 H] (H % 4 == 0 keeps every part 16-byte
+// aligned).
+__host__ __device__ constexpr uint32_t chain_lds_bytes(uint32_t H) {
+  return (H + 4u + static_cast<uint32_t>(kWaves) * 2u * H) * 4u;
+}
+
+// Chain workgroup b: its waves normalize rows kWaves b .. kWaves b + 3 in the
+// reference order (the finalize's rescore needs y and inv; the fast scores
+// of this launch do not).
+__device__ void chain_block(const GatherArgs& a, float* lds) {
+  const uint32_t H = a.H;
+  float* w = lds;
+  float* inv = lds + H;
+  const uint32_t wave = threadIdx.x / kWave;
+  float* xs = lds + H + 4u + wave * 2u * H;
+  float* sq = xs + H;
+  for (uint32_t q = threadIdx.x; q < H / 4u; q += kThreads) {
+    reinterpret_cast<float4*>(w)[q] = reinterpret_cast<const float4*>(a.weight)[q];
+  }
+  __syncthreads();
+  const uint32_t r = blockIdx.x * kWaves + wave;
+  if (r < a.chain_rows) {
+    norm_chain_wave(a.x, w, a.y_out, a.inv_out, r, H, a.epsilon, xs, sq, inv + wave);
+  }
+}
+
 // Planned mode: the tile plan, then wave slot s of the grid's S slots walks
-// tiles [W s / S, W (s + 1) / S).
+// tiles [W s / S, W (s + 1) / S).  The first chain workgroups of the grid run
+// the norm's reference-order chains instead.
 template <int KC>
 __global__ __launch_bounds__(kThreads) void gather_mfma_kernel(GatherArgs a) {
   __shared__ TilePlan<kThreads> plan;
   extern __shared__ __align__(16) uint16_t stages[];  // [waves][2 H]
+  const uint32_t chain_groups = (a.chain_rows + kWaves - 1) / kWaves;
+  if (blockIdx.x < chain_groups) {
+    chain_block(a, reinterpret_cast<float*>(stages));
+    return;
+  }
   uint16_t* stage = stages + static_cast<size_t>(threadIdx.x / kWave) * 2u * a.H;
   uint32_t staged = kInvalidToken;
   const uint64_t W = plan_tiles<kThreads>(a.row_meta, a.rows, kGatherWaveTile, false, plan);
-  const uint64_t slots = static_cast<uint64_t>(gridDim.x) * kWaves;
-  const uint64_t me = static_cast<uint64_t>(blockIdx.x) * kWaves + threadIdx.x / kWave;
+  const uint64_t slots = static_cast<uint64_t>(gridDim.x - chain_groups) * kWaves;
+  const uint64_t me =
+      static_cast<uint64_t>(blockIdx.x - chain_groups) * kWaves + threadIdx.x / kWave;
   const uint32_t w0 = static_cast<uint32_t>(W * me / slots);
   const uint32_t w1 = static_cast<uint32_t>(W * (me + 1) / slots);
   if (w0 >= w1) return;
@@ -271,25 +308,56 @@ __global__ __launch_bounds__(kWave) void gather_mfma_grid_kernel(GatherArgs a) {
   mfma_tile<KC>(a, r, k, meta.list_begin, meta.count, stages, staged);
 }
 
+// Workgroups of gather_mfma_kernel<KC> one compute unit holds with `lds`
+// bytes of dynamic LDS (cached per size: with and without chain waves).
+template <int KC>
+int resident_groups(uint32_t lds) {
+  static std::atomic<uint64_t> cache[2];  // (lds << 8) | count
+  for (auto& c : cache) {
+    const uint64_t v = c.load(std::memory_order_relaxed);
+    if (v != 0 && (v >> 8) == lds) return static_cast<int>(v & 0xFFu);
+  }
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+          &n, reinterpret_cast<const void*>(gather_mfma_kernel<KC>), kThreads, lds) != hipSuccess ||
+      n <= 0) {
+    n = 1;
+  }
+  if (n > 255) n = 255;
+  const uint64_t v = (static_cast<uint64_t>(lds) << 8) | static_cast<uint64_t>(n);
+  for (auto& c : cache) {
+    uint64_t expected = 0;
+    if (c.compare_exchange_strong(expected, v)) break;
+  }
+  return n;
+}
+
 template <int KC>
 hipError_t launch_variant(const GatherArgs& a, hipStream_t stream) {
   if (a.rows <= kPlanRowsMax && a.groups > 0) {
-    const uint32_t lds = kWaves * 4u * a.H;
-    static int resident = 0;
-    if (resident == 0) {
-      int n = 0;
-      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-              &n, reinterpret_cast<const void*>(gather_mfma_kernel<KC>), kThreads, lds) !=
-              hipSuccess ||
-          n <= 0) {
-        n = 2;
-      }
-      resident = n;
+    const uint32_t stage_lds = kWaves * 4u * a.H;
+    const uint32_t chain_groups = (a.chain_rows + kWaves - 1) / kWaves;
+    if (chain_groups > 0 && (a.H % 4u != 0 || a.x == nullptr || a.weight == nullptr ||
+                             a.y_out == nullptr || a.inv_out == nullptr)) {
+      return hipErrorInvalidValue;
     }
-    const uint32_t g = a.groups * static_cast<uint32_t>(resident);
-    hipLaunchKernelGGL((gather_mfma_kernel<KC>), dim3(g), dim3(kThreads), lds, stream, a);
+    const uint32_t lds =
+        chain_groups > 0 && chain_lds_bytes(a.H) > stage_lds ? chain_lds_bytes(a.H) : stage_lds;
+    // with chain workgroups the gather takes two workgroups per compute unit
+    // so that every CU carries the same gather share (a CU's share is
+    // bounded by what its memory pipeline moves) and the chain workgroups
+    // find a free slot
+    uint32_t per_cu = static_cast<uint32_t>(resident_groups<KC>(stage_lds));
+    if (chain_groups > 0) {
+      const uint32_t with_chain = static_cast<uint32_t>(resident_groups<KC>(lds));
+      per_cu = with_chain > 2u ? 2u : (with_chain > 1u ? with_chain - 1u : 1u);
+    }
+    const uint32_t g = a.groups * per_cu;
+    hipLaunchKernelGGL((gather_mfma_kernel<KC>), dim3(chain_groups + g), dim3(kThreads), lds,
+                       stream, a);
     return hipGetLastError();
   }
+  if (a.chain_rows > 0) return hipErrorInvalidValue;  // chains run in planned mode only
   const uint64_t slots = static_cast<uint64_t>(a.rows) * a.max_tiles;
   if (slots > 0x7FFFFFFFull) return hipErrorInvalidValue;
   hipLaunchKernelGGL((gather_mfma_grid_kernel<KC>), dim3(static_cast<uint32_t>(slots)),

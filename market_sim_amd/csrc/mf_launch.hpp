@@ -88,6 +88,7 @@ struct TailNormArgs {
   uint16_t* y_lo;
   float slack;             // absolute term of the fast score itself
   float slack_scaled;      // absolute term of the reference score, per unit of 1 / inv
+  uint32_t chain;          // 0: y and row_inv come from the gather launch's chain waves
   const uint32_t* row_state;
   const uint32_t* offsets;
   uint32_t states;
@@ -149,6 +150,15 @@ struct GatherArgs {
   uint32_t tile;           // candidates per tile (<= kGatherTileMax)
   uint32_t max_tiles;
   uint32_t groups;         // compute units for the planned mode (0 = grid mode)
+  // Chain waves (MFMA gather, planned mode): the first chain_groups
+  // workgroups normalize rows 0 .. chain_rows - 1 in the reference order into
+  // y_out / inv_out while the others gather (the fast scores need only z).
+  const float* x;
+  const float* weight;
+  float epsilon;
+  float* y_out;
+  float* inv_out;
+  uint32_t chain_rows;
   float coef;              // dot: b = coef * sum|y e| + slack
   float coef2;             // lookup, MFMA: b = ||e|| (coef ||y|| + coef2) + slack
   float slack;

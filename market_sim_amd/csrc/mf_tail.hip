@@ -23,56 +23,13 @@
 #include "mf_device.hpp"
 #include "mf_launch.hpp"
 #include "mf_finalize.hpp"
+#include "mf_norm.hpp"
 #include "mf_plan.hpp"
 
 namespace mf {
 namespace {
 
 constexpr int kThreads = 256;
-
-// Sum of squares in the reference order (operators.cpp:527-531): every square
-// rounded (lanes compute them in parallel into sq[]), then added in column
-// order by one lane.  Blocks of 16 values alternate between two register
-// sets: the LDS reads of block i + 1 are issued before the adds of block i
-// (sched_barrier keeps the scheduler from sinking them to their use, which
-// would pay an LDS round trip per block).
-__device__ __forceinline__ void load16(const float4* q, uint32_t i, float4 (&v)[4]) {
-#pragma unroll
-  for (int k = 0; k < 4; ++k) v[k] = q[4 * i + k];
-}
-__device__ __forceinline__ float add16(float s, const float4 (&v)[4]) {
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    s = s + v[k].x;
-    s = s + v[k].y;
-    s = s + v[k].z;
-    s = s + v[k].w;
-  }
-  return s;
-}
-__device__ float sequential_sum(const float* sq, uint32_t H) {
-  float s = 0.0f;
-  uint32_t c = 0;
-  if ((H & 31u) == 0) {
-    const float4* q = reinterpret_cast<const float4*>(sq);
-    const uint32_t n16 = H / 16;  // even
-    float4 a[4], b[4];
-    load16(q, 0, a);
-    for (uint32_t i = 0; i < n16; i += 2) {
-      load16(q, i + 1, b);
-      __builtin_amdgcn_sched_barrier(0);
-      s = add16(s, a);
-      __builtin_amdgcn_sched_barrier(0);
-      load16(q, i + 2 < n16 ? i + 2 : i, a);
-      __builtin_amdgcn_sched_barrier(0);
-      s = add16(s, b);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    c = H;
-  }
-  for (; c < H; ++c) s = s + sq[c];
-  return s;
-}
 
 // Workgroup r < rows normalizes row r; workgroup rows + j normalizes row
 // fb_rows[j] again for slot j of the MFMA head's panel (the same code on the
@@ -93,6 +50,7 @@ __global__ __launch_bounds__(kWave) void tail_norm_kernel(TailNormArgs a) {
       if (lane == 0) {
         a.fb_slot_row[j] = kInvalidToken;
         a.fb_slot_norm[j] = 0.0f;
+        a.fb_slot_slack[j] = 0.0f;
       }
       return;
     }
@@ -111,6 +69,9 @@ __global__ __launch_bounds__(kWave) void tail_norm_kernel(TailNormArgs a) {
   }
   float* ws = lds + 2u * H;  // weight (when given)
   const bool weighted = a.weight != nullptr;
+  // rows compute y here unless the chain waves of the gather launch do
+  const bool chain = weighted && !slot && a.chain;
+  const bool write_y = !slot && (!weighted || a.chain);
   if ((H & 3u) == 0) {
     // x and the weight: four float4 loads of each per lane in flight before
     // the LDS stores
@@ -155,12 +116,9 @@ __global__ __launch_bounds__(kWave) void tail_norm_kernel(TailNormArgs a) {
       b = a.offsets[s];
       e = a.offsets[s + 1];
     }
-    // the reference-order chain: rows only (a slot needs z, not y)
-    if (weighted && !slot) {
-      const float sum_squares = sequential_sum(sq, H);
-      const float mean = div_rn(sum_squares, static_cast<float>(H));
-      inverse_shared = div_rn(1.0f, sqrt_rn(mean + a.epsilon));
-    }
+    // the reference-order chain: rows only (a slot needs z, not y), and
+    // only when it is not deferred to the gather launch
+    if (chain) inverse_shared = norm_inverse(sequential_sum(sq, H), H, a.epsilon);
     if (!slot) {
       meta.state = s;
       if (s == kStateUnrestricted) {
@@ -184,7 +142,7 @@ __global__ __launch_bounds__(kWave) void tail_norm_kernel(TailNormArgs a) {
     }
   }
   __syncthreads();
-  const float inverse = (weighted && !slot) ? inverse_shared : 1.0f;
+  const float inverse = chain ? inverse_shared : 1.0f;
   const bool split = a.y_hi != nullptr;
   // slot workgroups: the slot's [hi | lo] rows of the panel
   uint16_t* panel_hi = nullptr;
@@ -214,7 +172,7 @@ __global__ __launch_bounds__(kWave) void tail_norm_kernel(TailNormArgs a) {
       panel_hi[c] = __builtin_bit_cast(uint16_t, hi);
       panel_hi[H + kPanelPad + c] = lo;
     } else {
-      a.y[r * H + c] = yv;
+      if (write_y) a.y[r * H + c] = yv;
       if (split) {
         a.y_hi[r * H + c] = __builtin_bit_cast(uint16_t, hi);
         a.y_lo[r * H + c] = lo;
@@ -246,7 +204,7 @@ __global__ __launch_bounds__(kWave) void tail_norm_kernel(TailNormArgs a) {
     } else {
       a.row_norm[r] = bound;
       a.row_slack[r] = slack;
-      a.row_inv[r] = inverse;
+      if (write_y) a.row_inv[r] = inverse;
     }
   }
 }
