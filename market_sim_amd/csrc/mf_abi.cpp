@@ -820,8 +820,11 @@ mf_status mf_decode_tail_finalize(const mf_decode_tail_args* args, uintptr_t str
   return decode_tail_stage(args, stream, Stage::kFinalize);
 }
 
+// The MFMA head runs before the gather: it streams the whole table in
+// order, and the gather's row lookups then find most rows in the
+// last-level cache.
 mf_status mf_decode_tail_f16(const mf_decode_tail_args* args, uintptr_t stream) {
-  for (Stage st : {Stage::kPrepare, Stage::kRestricted, Stage::kUnrestricted, Stage::kFinalize}) {
+  for (Stage st : {Stage::kPrepare, Stage::kUnrestricted, Stage::kRestricted, Stage::kFinalize}) {
     const mf_status v = decode_tail_stage(args, stream, st);
     if (v.code != MF_OK) return v;
   }

@@ -366,6 +366,13 @@ __device__ __forceinline__ void wait_vector_memory() {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
+// LDS writes of this wave are visible to every lane of the wave afterwards.
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // Per-row metadata written by the decode-tail norm kernel.
 enum : uint32_t { kRowRestricted = 1u, kRowUnrestricted = 2u, kRowInvalid = 4u };
 struct alignas(16) RowMeta {

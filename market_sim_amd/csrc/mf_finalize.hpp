@@ -14,13 +14,6 @@
 
 namespace mf {
 
-// LDS writes of this wave are visible to every lane of the wave afterwards.
-__device__ __forceinline__ void wave_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 struct FinalizeWords {
   uint32_t n_cand;
   uint32_t token;

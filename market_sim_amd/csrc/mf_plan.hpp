@@ -25,12 +25,13 @@ __device__ __forceinline__ bool row_gathered(const RowMeta& m, bool lookup) {
 }
 
 // Fills the plan (all threads call; ends with a barrier) and returns W.
-template <int kThreads>
-__device__ uint32_t plan_tiles(const RowMeta* row_meta, uint32_t rows, uint32_t tile,
-                               bool lookup, TilePlan<kThreads>& p) {
+// meta_of(r) gives row r's metadata.
+template <int kThreads, typename MetaOf>
+__device__ uint32_t plan_tiles_by(MetaOf meta_of, uint32_t rows, uint32_t tile, bool lookup,
+                                  TilePlan<kThreads>& p) {
   const uint32_t tid = threadIdx.x;
   for (uint32_t r = tid; r < rows; r += kThreads) {
-    const RowMeta m = row_meta[r];
+    const RowMeta m = meta_of(r);
     const bool use = row_gathered(m, lookup);
     p.begin[r] = m.list_begin;
     p.count[r] = use ? m.count : 0u;
@@ -62,6 +63,14 @@ __device__ uint32_t plan_tiles(const RowMeta* row_meta, uint32_t rows, uint32_t 
   if (tid == 0) p.prefix[0] = 0u;
   __syncthreads();
   return p.prefix[rows];
+}
+
+// The plan from the metadata the norm kernel wrote.
+template <int kThreads>
+__device__ uint32_t plan_tiles(const RowMeta* row_meta, uint32_t rows, uint32_t tile,
+                               bool lookup, TilePlan<kThreads>& p) {
+  return plan_tiles_by<kThreads>([row_meta](uint32_t r) { return row_meta[r]; }, rows, tile,
+                                 lookup, p);
 }
 
 // The row holding tile w: largest r with prefix[r] <= w < prefix[r + 1].

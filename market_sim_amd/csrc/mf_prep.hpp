@@ -1,0 +1,226 @@
+// The decode tail's per-row preparation, one wave per item: the norm kernel
+// runs one item per workgroup, the fused gather launch four per workgroup
+// beside its gather workgroups.
+//
+// Item r < rows (a row): its list (the state through the sequence table, the
+// state's CSR span, the validity rules) into row_meta, the preset outputs of
+// rows the gather does not serve, the reference-order RMSNorm y and inv
+// (operators.cpp:523-535), and -- when the caller asks -- the FP16 split of
+// z = x * w with its bounds.  Item rows + j (a slot of the MFMA head): the
+// split of row fb_rows[j] into slot j of the head's panel, with its bounds.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "mf_device.hpp"
+#include "mf_launch.hpp"
+#include "mf_norm.hpp"
+
+namespace mf {
+
+// Row r's list: state s (through the sequence table: q = row_sequence[r],
+// MF_STATE_INVALID when q is outside it), the CSR span [b, e) of s and the
+// row's metadata (restricted when s < states and 0 < e - b <= max_count with
+// e <= nnz; unrestricted for MF_STATE_UNRESTRICTED; invalid otherwise).
+struct RowList {
+  RowMeta meta;
+  uint32_t q;  // state-table index (r without a table)
+  uint32_t b;
+  uint32_t e;
+};
+
+__device__ __forceinline__ RowList row_list(const TailNormArgs& a, uint32_t r) {
+  RowList l;
+  l.q = r;
+  uint32_t s;
+  if (a.row_sequence != nullptr) {
+    l.q = a.row_sequence[r];
+    s = l.q < a.capacity ? a.row_state[l.q] : kInvalidToken;
+  } else {
+    s = a.row_state[r];
+  }
+  l.b = 0u;
+  l.e = 0u;
+  if (s < a.states) {
+    l.b = a.offsets[s];
+    l.e = a.offsets[s + 1];
+  }
+  l.meta = RowMeta{0u, 0u, s, kRowInvalid};
+  if (s == kStateUnrestricted) {
+    l.meta = RowMeta{0u, a.V, s, kRowUnrestricted};
+  } else if (s < a.states && l.e > l.b && l.e <= a.nnz && l.e - l.b <= a.max_count) {
+    l.meta = RowMeta{l.b, l.e - l.b, s, kRowRestricted};
+  }
+  return l;
+}
+
+// Bound of ||z|| from the wave's per-lane sums of z^2, and the row's absolute
+// error term from its per-lane sums of the rounded squares x^2.  1 / inv <=
+// sqrt(x_sq (1 + 2^-9) / H + eps) (1 + 2^-9): the reference sums the same
+// rounded squares in another order (relative H 2^-23 apart at most,
+// H <= 8192), then divides, adds eps, takes the square root and the
+// reciprocal (a few roundings); the 2^-9 margins cover all of them.  An
+// infinite or NaN value (overflowing or non-finite x) makes every bound of
+// the row infinite, and the row is then rescored in full.
+__device__ __forceinline__ void z_bounds(float z_sq, float x_sq, bool weighted, uint32_t H,
+                                         float epsilon, float slack_base, float slack_scaled,
+                                         float& z_norm, float& slack) {
+  z_sq = wave_sum_f32(z_sq);
+  x_sq = wave_sum_f32(x_sq);
+  // FP32 sum of H squares is within a relative H 2^-24 of the exact value;
+  // the factor covers that and the sqrt for any H <= 2^16
+  z_norm = __fsqrt_rn(z_sq) * (1.0f + 0x1p-7f);
+  slack = slack_base;
+  if (weighted) {
+    const float scale =
+        __fsqrt_rn(x_sq * (1.0f + 0x1p-9f) / static_cast<float>(H) + epsilon) * (1.0f + 0x1p-9f);
+    slack = __builtin_fmaf(scale, slack_scaled, slack_base);
+  }
+}
+
+// One wave, item `item`.  lds: the wave's own 3 H floats (16-byte aligned);
+// inv_slot: one float of the wave's own.  split_rows: also write the row's
+// FP16 split of z and its bounds (row_norm, row_slack); the fused gather
+// computes those itself.
+__device__ inline void prep_item(const TailNormArgs& a, uint32_t item, float* lds,
+                                 float* inv_slot, bool split_rows) {
+  const uint32_t H = a.H;
+  const uint32_t lane = threadIdx.x % kWave;
+  float* xs = lds;
+  float* sq = lds + H;
+  float* ws = lds + 2u * H;
+  const bool slot = item >= a.rows;
+  const uint32_t j = item - a.rows;  // the slot (slot items)
+  uint64_t r = item;
+  if (slot) {
+    r = a.fb_rows[j];
+    if (r >= a.rows) {
+      if (lane == 0) {
+        a.fb_slot_row[j] = kInvalidToken;
+        a.fb_slot_norm[j] = 0.0f;
+        a.fb_slot_slack[j] = 0.0f;
+      }
+      return;
+    }
+  }
+  const bool weighted = a.weight != nullptr;
+  // rows compute y here unless the chain waves of the gather launch do
+  const bool chain = weighted && !slot && a.chain;
+  const bool write_y = !slot && (!weighted || a.chain);
+  const bool split = slot || (split_rows && a.y_hi != nullptr);
+  // the row's list first: its loads are in flight during the staging
+  RowList l{};
+  if (!slot && lane == 0) l = row_list(a, static_cast<uint32_t>(r));
+  if ((H & 3u) == 0) {
+    // x and the weight: four float4 loads of each per lane in flight before
+    // the LDS stores
+    constexpr uint32_t kBatch = 4;
+    const float4* x4 = reinterpret_cast<const float4*>(a.x + r * H);
+    const float4* w4 = reinterpret_cast<const float4*>(a.weight);
+    const uint32_t n = H / 4;
+    for (uint32_t base = lane; base < n; base += kWave * kBatch) {
+      float4 v[kBatch];
+      float4 wv[kBatch];
+#pragma unroll
+      for (uint32_t u = 0; u < kBatch; ++u) {
+        const uint32_t q = base + u * kWave;
+        v[u] = q < n ? x4[q] : float4{0.0f, 0.0f, 0.0f, 0.0f};
+        wv[u] = (weighted && q < n) ? w4[q] : float4{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+#pragma unroll
+      for (uint32_t u = 0; u < kBatch; ++u) {
+        const uint32_t q = base + u * kWave;
+        if (q < n) {
+          reinterpret_cast<float4*>(xs)[q] = v[u];
+          reinterpret_cast<float4*>(sq)[q] =
+              float4{v[u].x * v[u].x, v[u].y * v[u].y, v[u].z * v[u].z, v[u].w * v[u].w};
+          if (weighted) reinterpret_cast<float4*>(ws)[q] = wv[u];
+        }
+      }
+    }
+  } else {
+    for (uint32_t c = lane; c < H; c += kWave) {
+      const float v = a.x[r * H + c];
+      xs[c] = v;
+      sq[c] = v * v;
+      if (weighted) ws[c] = a.weight[c];
+    }
+  }
+  wave_sync();
+  if (lane == 0) {
+    // the reference-order chain: rows only (a slot needs z, not y), and
+    // only when it is not deferred to the gather launch
+    if (chain) *inv_slot = norm_inverse(sequential_sum(sq, H), H, a.epsilon);
+    if (!slot) {
+      a.row_meta[r] = l.meta;
+      if (l.meta.kind != kRowRestricted) {
+        // invalid rows keep these; unrestricted rows are overwritten by the
+        // finalize kernel when the MFMA head was given them.  A finished row
+        // (empty list) holds its state when asked to.
+        a.out_token[r] = kInvalidToken;
+        if (a.out_score != nullptr) a.out_score[r] = __builtin_nanf("");
+        if (a.out_next != nullptr && l.q < a.capacity) {
+          const uint32_t s = l.meta.state;
+          a.out_next[l.q] = (a.hold && s < a.states && l.e == l.b) ? s : kInvalidToken;
+        }
+      }
+      if (a.fb_map != nullptr) a.fb_map[r] = kInvalidToken;
+    }
+  }
+  wave_sync();
+  const float inverse = chain ? *inv_slot : 1.0f;
+  // slot items: the slot's [hi | lo] rows of the panel
+  uint16_t* panel_hi = nullptr;
+  if (slot) {
+    panel_hi = a.fb_panel + static_cast<uint64_t>(j / kPanelRows) * (panel_tile_bytes(H) / 2u) +
+               static_cast<uint64_t>(j % kPanelRows) * 2u * (H + kPanelPad);
+  }
+  // y = (x * inv) * w in the reference's roundings (operators.cpp:533-534)
+  // for the rescore; z = x * w, the fast scores' operand, split into FP16
+  // hi + lo.  z differs from y / inv by at most 3 roundings per element.
+  float z_sq = 0.0f;
+  float x_sq = 0.0f;
+  for (uint32_t c = lane; c < H; c += kWave) {
+    const float xv = xs[c];
+    float yv = xv;
+    float zv = xv;
+    if (weighted) {
+      const float scaled = xv * inverse;
+      yv = scaled * ws[c];
+      zv = xv * ws[c];
+      x_sq += sq[c];
+    }
+    if (write_y) a.y[r * H + c] = yv;
+    if (split) {
+      z_sq = __builtin_fmaf(zv, zv, z_sq);
+      const _Float16 hi = static_cast<_Float16>(zv);
+      const uint16_t lo = float_to_half_rne(zv - static_cast<float>(hi));
+      if (slot) {
+        panel_hi[c] = __builtin_bit_cast(uint16_t, hi);
+        panel_hi[H + kPanelPad + c] = lo;
+      } else {
+        a.y_hi[r * H + c] = __builtin_bit_cast(uint16_t, hi);
+        a.y_lo[r * H + c] = lo;
+      }
+    }
+  }
+  if (!split) {
+    if (write_y && lane == 0) a.row_inv[r] = inverse;
+    return;
+  }
+  float z_norm, slack;
+  z_bounds(z_sq, x_sq, weighted, H, a.epsilon, a.slack, a.slack_scaled, z_norm, slack);
+  if (lane == 0) {
+    if (slot) {
+      a.fb_slot_norm[j] = z_norm;
+      a.fb_slot_slack[j] = slack;
+      a.fb_slot_row[j] = static_cast<uint32_t>(r);
+    } else {
+      a.row_norm[r] = z_norm;
+      a.row_slack[r] = slack;
+      if (write_y) a.row_inv[r] = inverse;
+    }
+  }
+}
+
+}  // namespace mf

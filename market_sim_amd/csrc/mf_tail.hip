@@ -23,190 +23,20 @@
 #include "mf_device.hpp"
 #include "mf_launch.hpp"
 #include "mf_finalize.hpp"
-#include "mf_norm.hpp"
 #include "mf_plan.hpp"
+#include "mf_prep.hpp"
 
 namespace mf {
 namespace {
 
 constexpr int kThreads = 256;
 
-// Workgroup r < rows normalizes row r; workgroup rows + j normalizes row
-// fb_rows[j] again for slot j of the MFMA head's panel (the same code on the
-// same data, so the same bits) and writes only the slot.
+// Workgroup i runs prep item i (mf_prep.hpp): row i < rows, else slot
+// i - rows of the MFMA head's panel.
 __global__ __launch_bounds__(kWave) void tail_norm_kernel(TailNormArgs a) {
   extern __shared__ __align__(16) float lds[];
-  float* xs = lds;
-  float* sq = lds + a.H;
   __shared__ float inverse_shared;
-  const bool slot = blockIdx.x >= a.rows;
-  const uint32_t j = blockIdx.x - a.rows;  // the slot (slot workgroups)
-  uint64_t r = blockIdx.x;
-  const uint32_t lane = threadIdx.x;
-  const uint32_t H = a.H;
-  if (slot) {
-    r = a.fb_rows[j];
-    if (r >= a.rows) {
-      if (lane == 0) {
-        a.fb_slot_row[j] = kInvalidToken;
-        a.fb_slot_norm[j] = 0.0f;
-        a.fb_slot_slack[j] = 0.0f;
-      }
-      return;
-    }
-  }
-  // the row's state first: its list offsets depend on it (through the
-  // sequence table when there is one)
-  uint32_t s = 0u;
-  uint32_t q = static_cast<uint32_t>(r);
-  if (!slot && lane == 0) {
-    if (a.row_sequence != nullptr) {
-      q = a.row_sequence[r];
-      s = q < a.capacity ? a.row_state[q] : kInvalidToken;
-    } else {
-      s = a.row_state[r];
-    }
-  }
-  float* ws = lds + 2u * H;  // weight (when given)
-  const bool weighted = a.weight != nullptr;
-  // rows compute y here unless the chain waves of the gather launch do
-  const bool chain = weighted && !slot && a.chain;
-  const bool write_y = !slot && (!weighted || a.chain);
-  if ((H & 3u) == 0) {
-    // x and the weight: four float4 loads of each per lane in flight before
-    // the LDS stores
-    constexpr uint32_t kBatch = 4;
-    const float4* x4 = reinterpret_cast<const float4*>(a.x + r * H);
-    const float4* w4 = reinterpret_cast<const float4*>(a.weight);
-    const uint32_t n = H / 4;
-    for (uint32_t base = lane; base < n; base += kWave * kBatch) {
-      float4 v[kBatch];
-      float4 wv[kBatch];
-#pragma unroll
-      for (uint32_t u = 0; u < kBatch; ++u) {
-        const uint32_t q = base + u * kWave;
-        v[u] = q < n ? x4[q] : float4{0.0f, 0.0f, 0.0f, 0.0f};
-        wv[u] = (weighted && q < n) ? w4[q] : float4{0.0f, 0.0f, 0.0f, 0.0f};
-      }
-#pragma unroll
-      for (uint32_t u = 0; u < kBatch; ++u) {
-        const uint32_t q = base + u * kWave;
-        if (q < n) {
-          reinterpret_cast<float4*>(xs)[q] = v[u];
-          reinterpret_cast<float4*>(sq)[q] =
-              float4{v[u].x * v[u].x, v[u].y * v[u].y, v[u].z * v[u].z, v[u].w * v[u].w};
-          if (weighted) reinterpret_cast<float4*>(ws)[q] = wv[u];
-        }
-      }
-    }
-  } else {
-    for (uint32_t c = lane; c < H; c += kWave) {
-      const float v = a.x[r * H + c];
-      xs[c] = v;
-      sq[c] = v * v;
-      if (weighted) ws[c] = a.weight[c];
-    }
-  }
-  __syncthreads();
-  RowMeta meta{0u, 0u, 0u, kRowInvalid};
-  if (lane == 0) {
-    // the offsets loads are in flight during the serial sum
-    uint32_t b = 0u, e = 0u;
-    if (!slot && s < a.states) {
-      b = a.offsets[s];
-      e = a.offsets[s + 1];
-    }
-    // the reference-order chain: rows only (a slot needs z, not y), and
-    // only when it is not deferred to the gather launch
-    if (chain) inverse_shared = norm_inverse(sequential_sum(sq, H), H, a.epsilon);
-    if (!slot) {
-      meta.state = s;
-      if (s == kStateUnrestricted) {
-        meta.kind = kRowUnrestricted;
-        meta.count = a.V;
-      } else if (s < a.states && e > b && e <= a.nnz && e - b <= a.max_count) {
-        meta = RowMeta{b, e - b, s, kRowRestricted};
-      }
-      a.row_meta[r] = meta;
-      if (meta.kind != kRowRestricted) {
-        // invalid rows keep these; unrestricted rows are overwritten by the
-        // finalize kernel when the MFMA head was given them.  A finished row
-        // (empty list) holds its state when asked to.
-        a.out_token[r] = kInvalidToken;
-        if (a.out_score != nullptr) a.out_score[r] = __builtin_nanf("");
-        if (a.out_next != nullptr && q < a.capacity) {
-          a.out_next[q] = (a.hold && s < a.states && e == b) ? s : kInvalidToken;
-        }
-      }
-      if (a.fb_map != nullptr) a.fb_map[r] = kInvalidToken;
-    }
-  }
-  __syncthreads();
-  const float inverse = chain ? inverse_shared : 1.0f;
-  const bool split = a.y_hi != nullptr;
-  // slot workgroups: the slot's [hi | lo] rows of the panel
-  uint16_t* panel_hi = nullptr;
-  if (slot) {
-    panel_hi = a.fb_panel + static_cast<uint64_t>(j / kPanelRows) * (panel_tile_bytes(H) / 2u) +
-               static_cast<uint64_t>(j % kPanelRows) * 2u * (H + kPanelPad);
-  }
-  // y = (x * inv) * w in the reference's roundings (operators.cpp:533-534)
-  // for the rescore; z = x * w, the fast scores' operand, split into FP16
-  // hi + lo.  z differs from y / inv by at most 3 roundings per element.
-  float norm_sq = 0.0f;
-  float x_sq = 0.0f;
-  for (uint32_t c = lane; c < H; c += kWave) {
-    const float xv = xs[c];
-    float yv = xv;
-    float zv = xv;
-    if (weighted) {
-      const float scaled = xv * inverse;
-      yv = scaled * ws[c];
-      zv = xv * ws[c];
-      x_sq += sq[c];
-    }
-    norm_sq = __builtin_fmaf(zv, zv, norm_sq);
-    const _Float16 hi = static_cast<_Float16>(zv);
-    const uint16_t lo = float_to_half_rne(zv - static_cast<float>(hi));
-    if (slot) {
-      panel_hi[c] = __builtin_bit_cast(uint16_t, hi);
-      panel_hi[H + kPanelPad + c] = lo;
-    } else {
-      if (write_y) a.y[r * H + c] = yv;
-      if (split) {
-        a.y_hi[r * H + c] = __builtin_bit_cast(uint16_t, hi);
-        a.y_lo[r * H + c] = lo;
-      }
-    }
-  }
-  norm_sq = wave_sum_f32(norm_sq);
-  x_sq = wave_sum_f32(x_sq);
-  if (lane == 0) {
-    // FP32 sum of H squares is within a relative H 2^-24 of the exact value;
-    // the factor covers that and the sqrt for any H <= 2^16
-    const float bound = __fsqrt_rn(norm_sq) * (1.0f + 0x1p-7f);
-    // an upper bound of 1 / inv: the reference sums the same rounded
-    // squares in another order (relative H 2^-23 apart at most, H <= 8192),
-    // then divides, adds eps, takes the square root and the reciprocal
-    // (a few roundings); 2^-9 margins cover all of them.  An infinite or NaN
-    // value (overflowing or non-finite x) makes every bound of the row
-    // infinite, and the row is then rescored in full.
-    float slack = a.slack;
-    if (weighted) {
-      const float scale =
-          __fsqrt_rn(x_sq * (1.0f + 0x1p-9f) / static_cast<float>(H) + a.epsilon) * (1.0f + 0x1p-9f);
-      slack = __builtin_fmaf(scale, a.slack_scaled, a.slack);
-    }
-    if (slot) {
-      a.fb_slot_norm[j] = bound;
-      a.fb_slot_slack[j] = slack;
-      a.fb_slot_row[j] = static_cast<uint32_t>(r);
-    } else {
-      a.row_norm[r] = bound;
-      a.row_slack[r] = slack;
-      if (write_y) a.row_inv[r] = inverse;
-    }
-  }
+  prep_item(a, blockIdx.x, lds, &inverse_shared, true);
 }
 
 // ---------------------------------------------------------------------------
@@ -479,7 +309,7 @@ __global__ __launch_bounds__(kWave) void finalize_kernel(FinalizeArgs a) {
 } // namespace
 
 hipError_t launch_tail_norm(const TailNormArgs& args, hipStream_t stream) {
-  const size_t lds = (args.weight != nullptr ? 3u : 2u) * static_cast<size_t>(args.H) * sizeof(float);
+  const size_t lds = 3u * static_cast<size_t>(args.H) * sizeof(float);
   const uint32_t slots = args.fb_panel != nullptr ? args.fb_m : 0u;
   hipLaunchKernelGGL(tail_norm_kernel, dim3(args.rows + slots), dim3(kWave), lds, stream, args);
   return hipGetLastError();
