@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define MF_ABI_VERSION 2u
+#define MF_ABI_VERSION 3u
 
 /* Status: include/marketforge/core/status.hpp:7-49.  The numeric codes equal
  * the reference ErrorCode enumerators so results stay schema-compatible. */
@@ -201,6 +201,14 @@ mf_status mf_linear_f16(mf_buffer input, mf_buffer weight, mf_buffer output,
  * sequence's end with no host check.  Without the flag such a row's next
  * state is MF_STATE_INVALID, as for every invalid row.
  *
+ * flags: MF_TAIL_SORTED_LISTS -- every state's list is strictly ascending,
+ * as TokenDfa keeps its arcs (src/grammar/token_dfa.cpp:100-109).  With
+ * hidden % 64 == 0, hidden <= 576 and rows <= 256 the tail then scores the
+ * restricted and the unrestricted rows in one pass over the table (the
+ * restricted-stage entry point runs it; the unrestricted one does nothing).
+ * Results are the same with or without the flag; a list that turns out not
+ * to be ascending is rescored in full, exactly.
+ *
  * Workspace: caller-allocated device memory of mf_decode_tail_workspace_bytes
  * bytes, zero-filled once by mf_workspace_init before first use.  Every call
  * leaves it ready for the next one; calls that overlap in time on the same
@@ -229,10 +237,11 @@ typedef struct mf_decode_tail_args {
   uint64_t max_count;          /* longest state list (table builder's figure) */
   uint64_t unrestricted_count;
   mf_buffer row_sequence;      /* u32 [rows] or address 0: see "Sequence table" */
-  uint64_t flags;              /* 0 or MF_TAIL_HOLD_FINISHED */
+  uint64_t flags;              /* MF_TAIL_HOLD_FINISHED | MF_TAIL_SORTED_LISTS */
 } mf_decode_tail_args;
 
 #define MF_TAIL_HOLD_FINISHED 1u
+#define MF_TAIL_SORTED_LISTS 2u
 
 mf_status mf_decode_tail_workspace_bytes(const mf_decode_tail_args* args,
                                          uint64_t* bytes);

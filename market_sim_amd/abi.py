@@ -30,7 +30,8 @@ STATE_INVALID = 0xFFFFFFFF
 ORDER_FMA_CHAIN = 0
 ORDER_MUL_ADD_CHAIN = 1
 TAIL_HOLD_FINISHED = 1
-ABI_VERSION = 2
+TAIL_SORTED_LISTS = 2
+ABI_VERSION = 3
 
 _U64 = ctypes.c_uint64
 _UP = ctypes.c_size_t  # uintptr_t

@@ -96,6 +96,23 @@ void mfma_bound_coefs(uint64_t H, float& coef, float& coef2) {
   coef2 = static_cast<float>(2.0 * std::ldexp(1.0, -25) * std::sqrt(h));
 }
 
+// The table pass's candidate score g on hi = rne_f16(z) alone (exact FP16
+// products, H FP32 additions): |hi_f - z_f| <= 2^-11 |z_f| + 2^-25 (FP16
+// subnormals; |z_f| past the FP16 range makes g infinite and the candidate
+// is rescored), so
+//   |g - S_hi|   <= 1.001 gamma'_H (1 + 2^-10) ||z|| ||e||   (+ the 2^-25 term)
+//   |S_hi - S_z| <= 2^-11 ||z|| ||e|| + 2^-25 sqrt(H) ||e||
+// and the reference-order terms of mfma_bound_coefs, doubled for safety.
+void pass_bound_coefs(uint64_t H, float& coef, float& coef2) {
+  const double h = static_cast<double>(H);
+  const double u = std::ldexp(1.0, -24);
+  const double acc = 1.001 * gamma(h, std::ldexp(1.0, -23));
+  const double c = gamma(h, u) * (1.0 + 4.0 * u) + 4.0 * u +
+                   acc * (1.0 + std::ldexp(1.0, -10)) + std::ldexp(1.0, -11);
+  coef = static_cast<float>(2.0 * c + std::ldexp(1.0, -20));
+  coef2 = static_cast<float>(2.0 * std::ldexp(1.0, -25) * std::sqrt(h) * (1.0 + acc));
+}
+
 // Absolute term for underflow: each of up to 2H operations may lose 2^-126.
 float underflow_slack(uint64_t H) {
   return static_cast<float>(4.0 * static_cast<double>(H) * std::ldexp(1.0, -126));
@@ -467,8 +484,10 @@ constexpr uint32_t kFullTile = 256;  // selection over projected scores
 
 struct TailLayout {
   uint64_t y, row_inv, row_norm, row_slack, row_meta, y_hi, y_lo, fb_map, records, fb_records,
-      fb_panel, fb_slot_row, fb_slot_norm, fb_slot_slack, scores, tok_norm, total;
+      fb_panel, fb_slot_row, fb_slot_norm, fb_slot_slack, scores, tok_norm, range_off, range_rec,
+      row_tiles, total;
   uint32_t tile, max_tiles, fb_tiles, fb_rows;
+  bool pass;  // the table pass serves both kinds of rows
 };
 
 bool buffer_is(const mf_buffer& b, uint64_t bytes) { return b.address != 0 && b.bytes == bytes; }
@@ -482,6 +501,13 @@ bool mfma_gather(uint64_t H) { return H % 32u == 0; }
 uint32_t gather_tile(uint64_t H) {
   if (mfma_gather(H)) return mf::kGatherWaveTile;
   return H == 2048 ? 128u : 64u;
+}
+
+// The table pass (one launch for restricted and unrestricted rows): lists
+// declared ascending, the panel tile of the head in LDS, the row plan in LDS.
+bool table_pass(const mf_decode_tail_args* a) {
+  return (a->flags & MF_TAIL_SORTED_LISTS) && a->hidden % 64u == 0 &&
+         mf::panel_tile_bytes(a->hidden) <= mf::kPanelLdsMaxBytes && a->rows <= mf::kPassRowsMax;
 }
 
 // Validation common to both decode-tail entry points; fills the layout.
@@ -512,7 +538,7 @@ mf_status validate_tail(const mf_decode_tail_args* a, bool full, TailLayout& L) 
   // the state buffers: one entry per row, or a sequence table of any
   // capacity that row_sequence indexes
   const bool table = a->row_sequence.address != 0;
-  if ((a->flags & ~static_cast<uint64_t>(MF_TAIL_HOLD_FINISHED)) != 0) {
+  if ((a->flags & ~static_cast<uint64_t>(MF_TAIL_HOLD_FINISHED | MF_TAIL_SORTED_LISTS)) != 0) {
     return status(MF_INVALID_ARGUMENT);
   }
   if (table && (a->row_state.bytes / 4u > kU32Max || a->row_state.bytes == 0 ||
@@ -567,6 +593,12 @@ mf_status validate_tail(const mf_decode_tail_args* a, bool full, TailLayout& L) 
     L.max_tiles = static_cast<uint32_t>(a->max_count == 0 ? 1 : (a->max_count + L.tile - 1) / L.tile);
   }
   L.fb_tiles = mf::fallback_tiles(static_cast<uint32_t>(a->vocab));
+  // table pass: one record per (row, 192-token range) holding its ids
+  L.pass = !full && table_pass(a);
+  if (L.pass) {
+    const uint64_t longest = a->max_count == 0 ? 1 : a->max_count;
+    L.max_tiles = static_cast<uint32_t>(longest < L.fb_tiles ? longest : L.fb_tiles);
+  }
   const uint64_t fb_rows = full ? 0 : a->unrestricted_count;
   L.fb_rows = static_cast<uint32_t>(fb_rows);
   uint64_t off = 0;
@@ -593,6 +625,9 @@ mf_status validate_tail(const mf_decode_tail_args* a, bool full, TailLayout& L) 
   L.fb_slot_slack = take(fb_rows * 4u);
   L.scores = take(full ? rows * a->vocab * 4u : 0u);
   L.tok_norm = take(full ? a->vocab * 4u : 0u);
+  L.range_off = take(L.pass ? (L.fb_tiles + 1u) * rows * 4u : 0u);
+  L.range_rec = take(L.pass ? L.fb_tiles * rows * 4u : 0u);
+  L.row_tiles = take(L.pass ? rows * 4u : 0u);
   L.total = off;
   return ok();
 }
@@ -654,6 +689,15 @@ mf::TailNormArgs norm_args(const mf_decode_tail_args* a, const TailLayout& L, ch
     n.fb_slot_norm = reinterpret_cast<float*>(ws + L.fb_slot_norm);
     n.fb_slot_slack = reinterpret_cast<float*>(ws + L.fb_slot_slack);
   }
+  if (L.pass) {  // the range index of the table pass
+    n.tokens = ptr<const uint32_t>(a->state_tokens.address);
+    n.range_off = reinterpret_cast<uint32_t*>(ws + L.range_off);
+    n.range_rec = reinterpret_cast<uint32_t*>(ws + L.range_rec);
+    n.row_tiles = reinterpret_cast<uint32_t*>(ws + L.row_tiles);
+    n.ranges = L.fb_tiles;
+    n.records = reinterpret_cast<mf::TileRecord*>(ws + L.records);
+    n.max_recs = L.max_tiles;
+  }
   return n;
 }
 
@@ -690,6 +734,7 @@ mf::FinalizeArgs finalize_args(const mf_decode_tail_args* a, const TailLayout& L
   f.records = reinterpret_cast<const mf::TileRecord*>(ws + L.records);
   f.max_tiles = L.max_tiles;
   f.tile = L.tile;
+  f.row_tiles = L.pass ? reinterpret_cast<const uint32_t*>(ws + L.row_tiles) : nullptr;
   if (!full && a->unrestricted_count > 0) {
     f.fb_records = reinterpret_cast<const mf::TileRecord*>(ws + L.fb_records);
     f.fb_map = reinterpret_cast<const uint32_t*>(ws + L.fb_map);
@@ -727,6 +772,25 @@ mf::FallbackArgs fallback_args(const mf_decode_tail_args* a, const TailLayout& L
   return f;
 }
 
+mf::PassArgs pass_args(const mf_decode_tail_args* a, const TailLayout& L, char* ws) {
+  mf::PassArgs p{};
+  p.head = fallback_args(a, L, ws);
+  p.row_meta = reinterpret_cast<const mf::RowMeta*>(ws + L.row_meta);
+  p.row_tiles = reinterpret_cast<const uint32_t*>(ws + L.row_tiles);
+  p.range_off = reinterpret_cast<const uint32_t*>(ws + L.range_off);
+  p.range_rec = reinterpret_cast<const uint32_t*>(ws + L.range_rec);
+  p.tokens = ptr<const uint32_t>(a->state_tokens.address);
+  p.z_hi = reinterpret_cast<const uint16_t*>(ws + L.y_hi);
+  p.row_norm = reinterpret_cast<const float*>(ws + L.row_norm);
+  p.row_slack = reinterpret_cast<const float*>(ws + L.row_slack);
+  p.records = reinterpret_cast<mf::TileRecord*>(ws + L.records);
+  p.max_recs = L.max_tiles;
+  p.rows = static_cast<uint32_t>(a->rows);
+  p.ranges = L.fb_tiles;
+  pass_bound_coefs(a->hidden, p.coef, p.coef2);
+  return p;
+}
+
 mf_status decode_tail_stage(const mf_decode_tail_args* args, uintptr_t stream, Stage stage) {
   if (stream == 0) return status(MF_INVALID_ARGUMENT);
   TailLayout L{};
@@ -740,9 +804,14 @@ mf_status decode_tail_stage(const mf_decode_tail_args* args, uintptr_t stream, S
   hipError_t e = hipSuccess;
   switch (stage) {
     case Stage::kPrepare:
-      e = mf::launch_tail_norm(norm_args(a, L, ws, mfma_gather(a->hidden), !defer_chain(a)), s);
+      e = mf::launch_tail_norm(
+          norm_args(a, L, ws, mfma_gather(a->hidden), L.pass || !defer_chain(a)), s);
       break;
     case Stage::kRestricted: {
+      if (L.pass) {
+        e = mf::launch_pass(pass_args(a, L, ws), s);
+        break;
+      }
       mf::GatherArgs g = gather_args(a, L, ws);
       if (mfma_gather(a->hidden)) {
         g.y_hi = reinterpret_cast<const uint16_t*>(ws + L.y_hi);
@@ -765,7 +834,7 @@ mf_status decode_tail_stage(const mf_decode_tail_args* args, uintptr_t stream, S
       break;
     }
     case Stage::kUnrestricted: {
-      if (a->unrestricted_count == 0) break;
+      if (a->unrestricted_count == 0 || L.pass) break;
       e = mf::launch_fallback(fallback_args(a, L, ws), s);
       break;
     }

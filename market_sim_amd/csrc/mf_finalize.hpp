@@ -179,7 +179,8 @@ __device__ inline void finalize_row(const FinalizeArgs& a, uint32_t r, const Row
   uint32_t ntiles;
   if (meta.kind & kRowRestricted) {
     recs = a.records + static_cast<uint64_t>(r) * a.max_tiles;
-    ntiles = (meta.count + a.tile - 1) / a.tile;
+    ntiles = a.row_tiles != nullptr ? (a.row_tiles[r] & ~kRangesUnused)
+                                    : (meta.count + a.tile - 1) / a.tile;
   } else if ((meta.kind & kRowUnrestricted) && a.fb_records != nullptr) {
     const uint32_t m = a.fb_map[r];
     if (m == kInvalidToken) return;

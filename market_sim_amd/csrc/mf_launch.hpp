@@ -117,7 +117,27 @@ struct TailNormArgs {
   uint32_t* fb_slot_row;   // [fb_m]
   float* fb_slot_norm;     // [fb_m]
   float* fb_slot_slack;    // [fb_m]
+  // Range index of the table pass (range_off null: none).  A second wave of
+  // each row's workgroup walks the row's list (ascending ids expected) and
+  // writes, per 192-token range g of the vocabulary, the list position of
+  // the row's first id >= 192 g (range_off[g * rows + r], g <= ranges)
+  // and, for ranges holding ids of the row, their record index among the
+  // row's non-empty ranges (range_rec[g * rows + r]); row_tiles[r] = the row's
+  // record count, with kRangesUnused set when the list is not strictly
+  // ascending or holds an id >= V (the wave then writes the row's single
+  // record itself: rescore the whole list, or the invalid row).
+  const uint32_t* tokens;  // the state lists (range index only)
+  uint32_t* range_off;     // [ranges + 1, rows]
+  uint32_t* range_rec;     // [ranges, rows]
+  uint32_t* row_tiles;     // [rows]
+  uint32_t ranges;
+  TileRecord* records;     // [rows, max_recs]
+  uint32_t max_recs;
 };
+
+// row_tiles flag: the row's ranges are not used (its one record comes from
+// the norm kernel).
+constexpr uint32_t kRangesUnused = 0x80000000u;
 
 // Panel of the MFMA head: per tile of kPanelRows slots, the slots' FP16
 // split [slot][hi | lo][H + kPanelPad] halves -- the head's LDS image of its
@@ -131,6 +151,13 @@ __host__ __device__ constexpr uint64_t panel_tile_bytes(uint64_t H) {
 __host__ __device__ constexpr uint32_t panel_tiles(uint32_t m) {
   return (m + kPanelRows - 1) / kPanelRows;
 }
+// Tokens per tile of the MFMA head (one window record per row and tile) and
+// of the table pass (one workgroup step); the largest panel tile the
+// LDS-resident variants stage.
+constexpr uint32_t kHeadTileTokens = 192;
+// Rows the table pass plans in LDS (one per thread of its workgroup).
+constexpr uint32_t kPassRowsMax = 256;
+constexpr uint32_t kPanelLdsMaxBytes = 76u * 1024u;
 
 struct GatherArgs {
   const float* y;          // [rows, H]
@@ -186,6 +213,9 @@ struct FinalizeArgs {
   uint32_t* out_next;
   const uint32_t* row_sequence;  // as in TailNormArgs
   uint32_t capacity;
+  // records per restricted row: row_tiles[r] & ~kRangesUnused (table pass),
+  // or one per `tile` candidates of the list (null)
+  const uint32_t* row_tiles;
   uint32_t rows;
   uint32_t H;
   uint32_t V;
@@ -252,5 +282,31 @@ struct FallbackArgs {
 
 uint32_t fallback_tiles(uint32_t vocab);
 hipError_t launch_fallback(const FallbackArgs& args, hipStream_t stream);
+
+// ---- table pass (mf_pass.hip) ------------------------------------------------
+//
+// One launch over the table in 192-token tiles serves the unrestricted rows
+// (the head above, its records and fb_map) and the restricted candidates
+// whose ids fall in each tile (the range index of the norm kernel), which
+// get one window record per (row, tile) in `records`.
+struct PassArgs {
+  FallbackArgs head;          // m = 0: no unrestricted rows
+  const RowMeta* row_meta;
+  const uint32_t* row_tiles;  // [rows]
+  const uint32_t* range_off;  // [ranges + 1, rows]
+  const uint32_t* range_rec;  // [ranges, rows]
+  const uint32_t* tokens;     // state lists
+  const uint16_t* z_hi;       // [rows, H] FP16 hi of z = x * w
+  const float* row_norm;      // [rows] bound of ||z||
+  const float* row_slack;     // [rows]
+  TileRecord* records;        // [rows, max_recs]
+  uint32_t max_recs;
+  uint32_t rows;
+  uint32_t ranges;
+  float coef;                 // candidate bound: b = ||e|| (coef ||z|| + coef2) + slack
+  float coef2;
+};
+
+hipError_t launch_pass(const PassArgs& args, hipStream_t stream);
 
 } // namespace mf

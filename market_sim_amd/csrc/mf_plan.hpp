@@ -11,12 +11,12 @@
 
 namespace mf {
 
-template <int kThreads>
+template <int kThreads, uint32_t kRows = kPlanRowsMax>
 struct TilePlan {
-  uint32_t prefix[kPlanRowsMax + 1];  // prefix[r] = first tile of row r
-  uint32_t begin[kPlanRowsMax];       // list start in the state lists
-  uint32_t count[kPlanRowsMax];       // gathered candidates (0 = not gathered)
-  uint32_t kind[kPlanRowsMax];
+  uint32_t prefix[kRows + 1];  // prefix[r] = first tile of row r
+  uint32_t begin[kRows];       // list start in the state lists
+  uint32_t count[kRows];       // gathered candidates (0 = not gathered)
+  uint32_t kind[kRows];
   uint32_t wave_total[kThreads / kWave];
 };
 
@@ -26,9 +26,9 @@ __device__ __forceinline__ bool row_gathered(const RowMeta& m, bool lookup) {
 
 // Fills the plan (all threads call; ends with a barrier) and returns W.
 // meta_of(r) gives row r's metadata.
-template <int kThreads, typename MetaOf>
+template <int kThreads, uint32_t kRows, typename MetaOf>
 __device__ uint32_t plan_tiles_by(MetaOf meta_of, uint32_t rows, uint32_t tile, bool lookup,
-                                  TilePlan<kThreads>& p) {
+                                  TilePlan<kThreads, kRows>& p) {
   const uint32_t tid = threadIdx.x;
   for (uint32_t r = tid; r < rows; r += kThreads) {
     const RowMeta m = meta_of(r);
@@ -69,13 +69,13 @@ __device__ uint32_t plan_tiles_by(MetaOf meta_of, uint32_t rows, uint32_t tile, 
 template <int kThreads>
 __device__ uint32_t plan_tiles(const RowMeta* row_meta, uint32_t rows, uint32_t tile,
                                bool lookup, TilePlan<kThreads>& p) {
-  return plan_tiles_by<kThreads>([row_meta](uint32_t r) { return row_meta[r]; }, rows, tile,
-                                 lookup, p);
+  return plan_tiles_by<kThreads, kPlanRowsMax>([row_meta](uint32_t r) { return row_meta[r]; },
+                                               rows, tile, lookup, p);
 }
 
 // The row holding tile w: largest r with prefix[r] <= w < prefix[r + 1].
-template <int kThreads>
-__device__ uint32_t plan_row_of(const TilePlan<kThreads>& p, uint32_t rows, uint32_t w) {
+template <int kThreads, uint32_t kRows>
+__device__ uint32_t plan_row_of(const TilePlan<kThreads, kRows>& p, uint32_t rows, uint32_t w) {
   uint32_t lo = 0u, hi = rows;
   while (lo < hi) {
     const uint32_t mid = (lo + hi) / 2;

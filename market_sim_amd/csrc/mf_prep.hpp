@@ -223,4 +223,203 @@ __device__ inline void prep_item(const TailNormArgs& a, uint32_t item, float* ld
   }
 }
 
+// The range index of row r for the table pass (TailNormArgs range_off,
+// range_rec, row_tiles; range-major, so the pass reads each range's entries
+// of all rows contiguously), built by kWalkWaves waves of the row's
+// workgroup in three phases separated by workgroup barriers:
+//
+//   range_begin  every walk wave finds the row's list [b, b + c); the LDS
+//                table is cleared.
+//   range_walk   wave `part` walks its share of the list's 64-id chunks,
+//                each lane also loading its id's predecessor: an id whose
+//                predecessor lies in an earlier range opens its range, which
+//                records the id's position and its rank among this wave's
+//                openers (tagged with the wave).
+//   range_end    (one wave) ranks become record indices (earlier waves'
+//                opener counts added), ranges without ids start where the
+//                next opened one does (or at the end of the list: a suffix
+//                minimum), and the index is written out coalesced.
+//
+// A list that is not strictly ascending, or holds an id >= V, is not
+// indexed: the row gets one record covering its whole list, "rescore all"
+// (exact, in the finalize) or "invalid".  Ids past the vocabulary never
+// index past range `ranges`.  LDS (RangeLds): 2 (ranges + 1) + 2 kWalkWaves
+// words.
+constexpr uint32_t kWalkWaves = 3;
+constexpr uint32_t kNotOpened = 0xFFFFFFFFu;
+
+struct RangeLds {
+  uint32_t* offs;   // [ranges + 1] position of each opened range's first id
+  uint32_t* recs;   // [ranges + 1] rank | wave << 24 (kNotOpened)
+  uint32_t* count;  // [kWalkWaves] openers per wave
+  uint32_t* flags;  // [kWalkWaves] bit 0: an id >= V, bit 1: not ascending
+  static __device__ RangeLds at(uint32_t* base, uint32_t ranges) {
+    return RangeLds{base, base + ranges + 1u, base + 2u * (ranges + 1u),
+                    base + 2u * (ranges + 1u) + kWalkWaves};
+  }
+};
+
+struct RangeRow {
+  uint32_t b;     // list start
+  uint32_t c;     // list length
+  bool indexed;   // a restricted row
+};
+
+__device__ inline RangeRow range_begin(const TailNormArgs& a, uint32_t r, const RangeLds& L,
+                                       uint32_t part) {
+  const uint32_t lane = threadIdx.x % kWave;
+  RowList l{};
+  if (lane == 0) l = row_list(a, r);
+  RangeRow w;
+  w.b = __shfl(l.b, 0);
+  w.c = __shfl(l.e, 0) - w.b;
+  w.indexed = __shfl(l.meta.kind, 0) == kRowRestricted;
+  if (!w.indexed) {
+    if (part == 0 && lane == 0) a.row_tiles[r] = 0u;
+    return w;
+  }
+  for (uint32_t g = part * kWave + lane; g <= a.ranges; g += kWalkWaves * kWave) {
+    L.offs[g] = w.c;
+    L.recs[g] = kNotOpened;
+  }
+  return w;
+}
+
+__device__ inline void range_walk(const TailNormArgs& a, const RangeRow& w, const RangeLds& L,
+                                  uint32_t part) {
+  const uint32_t lane = threadIdx.x % kWave;
+  const uint32_t G = a.ranges;
+  const uint32_t b = w.b;
+  const uint32_t c = w.c;
+  const uint32_t chunks = (c + kWave - 1) / kWave;
+  const uint32_t lo = chunks * part / kWalkWaves * kWave;        // this wave's positions
+  const uint32_t hi = chunks * (part + 1) / kWalkWaves * kWave;  // [lo, min(hi, c))
+  uint32_t opened = 0u;
+  bool bad = false;
+  bool unsorted = false;
+  // ids in batches of kChunks chunks of 64, two batches in flight, each
+  // handled with compile-time registers; unconditional loads at clamped
+  // positions (a load under a branch makes the compiler wait for every load
+  // in flight at the join)
+  constexpr uint32_t kChunks = 8;
+  constexpr uint32_t kStep = kChunks * kWave;
+  auto load = [&](uint32_t base, uint32_t (&ids)[kChunks], uint32_t (&pre)[kChunks]) {
+#pragma unroll
+    for (uint32_t u = 0; u < kChunks; ++u) {
+      const uint32_t q = base + u * kWave + lane;
+      const uint32_t qi = q < c ? q : c - 1u;
+      ids[u] = a.tokens[b + qi];
+      pre[u] = a.tokens[b + (qi > 0u ? qi - 1u : 0u)];
+    }
+  };
+  auto walk = [&](uint32_t base, const uint32_t (&ids)[kChunks], const uint32_t (&pre)[kChunks]) {
+#pragma unroll
+    for (uint32_t u = 0; u < kChunks; ++u) {
+      const uint32_t p = base + u * kWave + lane;
+      const bool in = p < c && p < hi;
+      const uint32_t t = in ? ids[u] : kInvalidToken;
+      const uint32_t tp = p > 0u ? pre[u] : kInvalidToken;  // no predecessor at p = 0
+      const uint32_t gt = t < a.V ? t / kHeadTileTokens : G;
+      const uint32_t gp = tp < a.V ? tp / kHeadTileTokens : kInvalidToken;
+      bad |= in && t >= a.V;
+      unsorted |= in && p > 0 && t <= tp;
+      const bool opens = in && t < a.V && gt != gp;
+      const uint64_t m = __ballot(opens);
+      if (opens) {  // LDS only: global stores under a branch would stall the loads
+        L.offs[gt] = p;
+        L.recs[gt] = (opened + static_cast<uint32_t>(__popcll(m & ((1ull << lane) - 1ull)))) |
+                     (part << 24);
+      }
+      opened += static_cast<uint32_t>(__popcll(m));
+    }
+  };
+  uint32_t ia[kChunks], pa[kChunks], ib[kChunks], pb[kChunks];
+  load(lo, ia, pa);
+  for (uint32_t base = lo; base < hi && base < c; base += 2u * kStep) {
+    load(base + kStep, ib, pb);
+    walk(base, ia, pa);
+    load(base + 2u * kStep, ia, pa);
+    if (base + kStep < hi && base + kStep < c) walk(base + kStep, ib, pb);
+  }
+  const bool any_bad = __ballot(bad) != 0ull;
+  const bool any_unsorted = __ballot(unsorted) != 0ull;
+  if (lane == 0) {
+    L.count[part] = opened;
+    L.flags[part] = (any_bad ? 1u : 0u) | (any_unsorted ? 2u : 0u);
+  }
+}
+
+__device__ inline void range_end(const TailNormArgs& a, uint32_t r, const RangeRow& w,
+                                 const RangeLds& L) {
+  const uint32_t lane = threadIdx.x % kWave;
+  const uint32_t G = a.ranges;
+  const uint32_t rows = a.rows;
+  const uint32_t c = w.c;
+  uint32_t base[kWalkWaves];
+  uint32_t tiles = 0u;
+  uint32_t flags = 0u;
+#pragma unroll
+  for (uint32_t i = 0; i < kWalkWaves; ++i) {
+    base[i] = tiles;
+    tiles += L.count[i];
+    flags |= L.flags[i];
+  }
+  // offs[g] = min(offs[g .. G]): segment minima, a suffix minimum over the
+  // lanes, then each segment from its right end
+  const uint32_t seg = (G + kWave) / kWave;  // ceil((G + 1) / 64)
+  const uint32_t g0 = lane * seg;
+  uint32_t mine = c;
+  for (uint32_t i = 0; i < seg; ++i) {
+    if (g0 + i <= G) mine = L.offs[g0 + i] < mine ? L.offs[g0 + i] : mine;
+  }
+  uint32_t right = mine;  // minimum over lanes >= this one
+  for (int d = 1; d < kWave; d <<= 1) {
+    const uint32_t o = static_cast<uint32_t>(__shfl_down(static_cast<int>(right), d));
+    if (lane + d < kWave && o < right) right = o;
+  }
+  uint32_t run = static_cast<uint32_t>(__shfl_down(static_cast<int>(right), 1));
+  if (lane == kWave - 1) run = c;
+  for (uint32_t i = seg; i-- > 0;) {
+    if (g0 + i <= G) {
+      run = L.offs[g0 + i] < run ? L.offs[g0 + i] : run;
+      L.offs[g0 + i] = run;
+    }
+  }
+  wave_sync();
+  for (uint32_t g = lane; g <= G; g += kWave) {
+    a.range_off[static_cast<uint64_t>(g) * rows + r] = L.offs[g];
+    const uint32_t q = L.recs[g];
+    if (g < G) {
+      a.range_rec[static_cast<uint64_t>(g) * rows + r] =
+          q == kNotOpened ? 0u : (q & 0xFFFFFFu) + base[(q >> 24) < kWalkWaves ? (q >> 24) : 0u];
+    }
+  }
+  // the whole-list record of a list that is not indexed: its lowest id
+  if (flags != 0u) {
+    uint32_t mt = kInvalidToken;
+    uint32_t mp = 0u;
+    for (uint32_t p = lane; p < c; p += kWave) {
+      const uint32_t t = a.tokens[w.b + p];
+      if (t < mt) {
+        mt = t;
+        mp = p;
+      }
+    }
+    wave_min_token(mt, mp);
+    if (lane == 0) {
+      TileRecord* rec = a.records + static_cast<uint64_t>(r) * a.max_recs;
+      rec->best_lower = -__builtin_huge_valf();
+      rec->flags = (flags & 1u) ? kTileInvalid : kTileRescoreAll;
+      rec->min_token = mt;
+      rec->min_pos = mp;
+      rec->begin = 0u;
+      rec->count = c;
+      rec->n_members = 0u;
+      a.row_tiles[r] = 1u | kRangesUnused;
+    }
+  } else if (lane == 0) {
+    a.row_tiles[r] = tiles;
+  }
+}
+
 }  // namespace mf

@@ -32,11 +32,29 @@ namespace {
 constexpr int kThreads = 256;
 
 // Workgroup i runs prep item i (mf_prep.hpp): row i < rows, else slot
-// i - rows of the MFMA head's panel.
-__global__ __launch_bounds__(kWave) void tail_norm_kernel(TailNormArgs a) {
+// i - rows of the MFMA head's panel.  With a range index the workgroup has
+// kWalkWaves more waves, which index row i's list for the table pass while
+// wave 0 normalizes.
+__global__ __launch_bounds__((1 + kWalkWaves) * kWave) void tail_norm_kernel(TailNormArgs a) {
   extern __shared__ __align__(16) float lds[];
   __shared__ float inverse_shared;
-  prep_item(a, blockIdx.x, lds, &inverse_shared, true);
+  if (a.range_off == nullptr) {  // one wave
+    prep_item(a, blockIdx.x, lds, &inverse_shared, true);
+    return;
+  }
+  const uint32_t wave = threadIdx.x / kWave;
+  const bool row = blockIdx.x < a.rows;
+  const RangeLds L = RangeLds::at(reinterpret_cast<uint32_t*>(lds + 3u * a.H), a.ranges);
+  RangeRow w{};
+  if (wave > 0 && row) w = range_begin(a, blockIdx.x, L, wave - 1);
+  __syncthreads();
+  if (wave == 0) {
+    prep_item(a, blockIdx.x, lds, &inverse_shared, true);
+  } else if (row && w.indexed) {
+    range_walk(a, w, L, wave - 1);
+  }
+  __syncthreads();
+  if (wave == 1 && row && w.indexed) range_end(a, blockIdx.x, w, L);
 }
 
 // ---------------------------------------------------------------------------
@@ -309,9 +327,12 @@ __global__ __launch_bounds__(kWave) void finalize_kernel(FinalizeArgs a) {
 } // namespace
 
 hipError_t launch_tail_norm(const TailNormArgs& args, hipStream_t stream) {
-  const size_t lds = 3u * static_cast<size_t>(args.H) * sizeof(float);
+  const size_t lds =
+      3u * static_cast<size_t>(args.H) * sizeof(float) +
+      (args.range_off != nullptr ? (2u * (args.ranges + 1u) + 2u * kWalkWaves) * sizeof(uint32_t) : 0u);
   const uint32_t slots = args.fb_panel != nullptr ? args.fb_m : 0u;
-  hipLaunchKernelGGL(tail_norm_kernel, dim3(args.rows + slots), dim3(kWave), lds, stream, args);
+  const uint32_t threads = args.range_off != nullptr ? (1u + kWalkWaves) * kWave : kWave;
+  hipLaunchKernelGGL(tail_norm_kernel, dim3(args.rows + slots), dim3(threads), lds, stream, args);
   return hipGetLastError();
 }
 

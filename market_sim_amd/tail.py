@@ -9,7 +9,7 @@ from typing import Optional
 
 import numpy as np
 
-from . import abi, ops
+from . import abi, ops, workloads
 from .workloads import STATE_UNRESTRICTED, Workload
 
 
@@ -30,9 +30,15 @@ class DeviceTail:
 
     def __init__(self, w: Workload, device: str = "cuda", order: int = abi.ORDER_FMA_CHAIN,
                  copies: int = 1, full: bool = False, advance: Optional[str] = None,
-                 unrestricted: Optional[np.ndarray] = None):
+                 unrestricted: Optional[np.ndarray] = None,
+                 sorted_lists: Optional[bool] = None):
         import torch
         self.w = w
+        # MF_TAIL_SORTED_LISTS (the one-pass table kernel): declared when the
+        # lists are strictly ascending (None: checked here), or forced
+        if sorted_lists is None:
+            sorted_lists = workloads.lists_ascending(w.state_offsets, w.state_tokens)
+        self.flags = abi.TAIL_SORTED_LISTS if sorted_lists else 0
         # the rows handed to the MFMA head (default: the rows whose state is
         # MF_STATE_UNRESTRICTED)
         self._unrestricted = unrestricted
@@ -101,7 +107,8 @@ class DeviceTail:
         return ops.decode_tail_args(
             self.buffers(table), rows=w.rows, hidden=w.hidden, vocab=w.vocab,
             states=w.states, nnz=int(w.state_tokens.size), max_count=w.max_count,
-            unrestricted_count=self.n_unrestricted, epsilon=w.epsilon, order=self.order)
+            unrestricted_count=self.n_unrestricted, epsilon=w.epsilon, order=self.order,
+            flags=self.flags)
 
     def launch(self, table: int = 0, args: Optional[abi.DecodeTailArgs] = None) -> None:
         a = args if args is not None else self.args(table)

@@ -127,6 +127,20 @@ def distinct_sorted_ids(rng, vocab: int, k: int) -> np.ndarray:
     return np.sort(rng.choice(vocab, size=k, replace=False)).astype(np.uint32)
 
 
+def lists_ascending(offsets: np.ndarray, tokens: np.ndarray) -> bool:
+    """True when every CSR list tokens[offsets[s]:offsets[s + 1]] is strictly
+    ascending (the layout MF_TAIL_SORTED_LISTS declares)."""
+    t = np.asarray(tokens, dtype=np.int64)
+    if t.size < 2:
+        return True
+    up = np.diff(t) > 0
+    # pairs that straddle two lists are not compared
+    ends = np.asarray(offsets, dtype=np.int64)[1:-1] - 1
+    ends = ends[(ends >= 0) & (ends < up.size)]
+    up[ends] = True
+    return bool(up.all())
+
+
 def _pack(lists: List[Optional[np.ndarray]]):
     """CSR over the restricted rows; None marks an unrestricted row."""
     offsets = [0]

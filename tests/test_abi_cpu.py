@@ -26,7 +26,7 @@ def test_library_exports_every_declared_symbol():
     lib = abi.lib()
     for name in declared_functions():
         assert hasattr(lib, name), name
-    assert lib.mf_abi_version() == 2
+    assert lib.mf_abi_version() == 3
 
 
 def b(addr, n):
@@ -172,4 +172,24 @@ def test_decode_tail_sequence_table_and_flags_validation():
     assert ws_code(out_next_state=rs) == abi.MF_INVALID_ARGUMENT
     assert ws_code(row_state=table, row_sequence=seq, out_token=seq) == abi.MF_INVALID_ARGUMENT
     assert ws_code(flags=abi.TAIL_HOLD_FINISHED) == abi.MF_OK
-    assert ws_code(flags=2) == abi.MF_INVALID_ARGUMENT
+    assert ws_code(flags=abi.TAIL_SORTED_LISTS) == abi.MF_OK
+    assert ws_code(flags=abi.TAIL_HOLD_FINISHED | abi.TAIL_SORTED_LISTS) == abi.MF_OK
+    assert ws_code(flags=4) == abi.MF_INVALID_ARGUMENT
+
+
+def test_sorted_lists_flag_sizes_the_range_index():
+    """MF_TAIL_SORTED_LISTS adds the table pass's range index to the
+    workspace where the pass runs (hidden % 64 == 0, hidden <= 576, rows <=
+    1024) and changes nothing where it does not."""
+    l = abi.lib()
+    n = ctypes.c_uint64()
+
+    def ws(**kw):
+        a = _tail_args(**kw)
+        assert l.mf_decode_tail_workspace_bytes(ctypes.byref(a), ctypes.byref(n)).code == abi.MF_OK
+        return n.value
+
+    assert ws(flags=abi.TAIL_SORTED_LISTS) > ws()
+    wide = dict(hidden=2048, x=b(0x100000, 4 * 2048 * 4), norm_weight=b(0x200000, 2048 * 4),
+                embedding=b(0x300000, 1000 * 2048 * 2))
+    assert ws(flags=abi.TAIL_SORTED_LISTS, **wide) == ws(**wide)

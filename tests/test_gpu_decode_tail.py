@@ -20,6 +20,23 @@ def _lib(hip):
     return hip
 
 
+# Every test runs twice: with MF_TAIL_SORTED_LISTS (the one-pass table
+# kernel; lists that are not ascending are then caught on the device and
+# rescored in full) and without it (the gather and the MFMA head).
+_LISTS = {"sorted": True}
+
+
+@pytest.fixture(params=[True, False], ids=["table_pass", "gather"], autouse=True)
+def _lists_flag(request):
+    _LISTS["sorted"] = request.param
+    yield
+
+
+def _tail(w, **kw):
+    from market_sim_amd.tail import DeviceTail
+    return DeviceTail(w, sorted_lists=_LISTS["sorted"], **kw)
+
+
 def _oracle(w, x=None, order=abi.ORDER_FMA_CHAIN, advance="auto", threads=8):
     sn = w.state_next if advance in ("auto", "arcs") else None
     nt = w.next_table if (advance == "dense" or (advance == "auto" and sn is None)) else None
@@ -43,9 +60,7 @@ def _same(got, exp, check_next=True):
 
 
 def _run(w, order=abi.ORDER_FMA_CHAIN, full=False, advance=None):
-    from market_sim_amd.tail import DeviceTail
-    t = DeviceTail(w, order=order, full=full, advance=advance)
-    return t.run()
+    return _tail(w, order=order, full=full, advance=advance).run()
 
 
 @pytest.mark.parametrize("order", [abi.ORDER_FMA_CHAIN, abi.ORDER_MUL_ADD_CHAIN])
@@ -80,7 +95,7 @@ def test_cfg4_dfa_tail_32_steps(advance):
     carried on the device from one step to the next."""
     from market_sim_amd.tail import DeviceTail
     w = wl.config(4, seed=0)
-    t = DeviceTail(w, advance=advance)
+    t = _tail(w, advance=advance)
     state = w.row_state.copy()
     for step in range(w.steps):
         x = w.step_hidden(step)
@@ -189,7 +204,7 @@ def test_workspace_reuse_across_calls_and_shapes():
     give identical results."""
     from market_sim_amd.tail import DeviceTail
     w = wl.config(3, seed=11, scale_vocab=6000, scale_rows=40)
-    t = DeviceTail(w)
+    t = _tail(w)
     first = t.run()
     for _ in range(5):
         again = t.run()
@@ -212,7 +227,7 @@ def test_market_dfa_real_grammar_walk():
                     epsilon=1e-5, x=rng.standard_normal((rows, hidden)).astype(np.float32),
                     row_state=np.zeros(rows, np.uint32), state_offsets=offsets,
                     state_tokens=tokens, state_next=nxt)
-    t = DeviceTail(w)
+    t = _tail(w)
     state = w.row_state.copy()
     for step in range(6):
         x = rng.standard_normal((rows, hidden)).astype(np.float32)
@@ -249,7 +264,7 @@ def test_decode_tail_equals_its_stages(rows):
     from market_sim_amd.tail import DeviceTail
     w = wl.config(3, seed=21, scale_vocab=8192, scale_rows=rows)
     assert w.unrestricted_rows.size > 0
-    t = DeviceTail(w)
+    t = _tail(w)
     fused = t.run()
     staged = _staged(t)
     for a, b in zip(fused, staged):
@@ -272,7 +287,7 @@ def test_duplicate_and_foreign_unrestricted_rows():
     unr = w.unrestricted_rows
     restricted = np.nonzero(w.row_state < w.states)[0]
     listed = np.concatenate([unr, unr[:1], restricted[:1]]).astype(np.uint32)
-    t = DeviceTail(w, unrestricted=listed)
+    t = _tail(w, unrestricted=listed)
     fused = t.run()
     _same(fused, _oracle(w))
     staged = _staged(t)
