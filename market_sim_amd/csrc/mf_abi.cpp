@@ -484,7 +484,7 @@ constexpr uint32_t kFullTile = 256;  // selection over projected scores
 
 struct TailLayout {
   uint64_t y, row_inv, row_norm, row_slack, row_meta, y_hi, y_lo, fb_map, records, fb_records,
-      fb_panel, fb_slot_row, fb_slot_norm, fb_slot_slack, scores, tok_norm, range_off, range_rec,
+      fb_panel, fb_slot_row, fb_slot_norm, fb_slot_slack, scores, tok_norm, range_index,
       row_tiles, total;
   uint32_t tile, max_tiles, fb_tiles, fb_rows;
   bool pass;  // the table pass serves both kinds of rows
@@ -625,8 +625,7 @@ mf_status validate_tail(const mf_decode_tail_args* a, bool full, TailLayout& L) 
   L.fb_slot_slack = take(fb_rows * 4u);
   L.scores = take(full ? rows * a->vocab * 4u : 0u);
   L.tok_norm = take(full ? a->vocab * 4u : 0u);
-  L.range_off = take(L.pass ? (L.fb_tiles + 1u) * rows * 4u : 0u);
-  L.range_rec = take(L.pass ? L.fb_tiles * rows * 4u : 0u);
+  L.range_index = take(L.pass ? L.fb_tiles * rows * 16u : 0u);
   L.row_tiles = take(L.pass ? rows * 4u : 0u);
   L.total = off;
   return ok();
@@ -691,8 +690,7 @@ mf::TailNormArgs norm_args(const mf_decode_tail_args* a, const TailLayout& L, ch
   }
   if (L.pass) {  // the range index of the table pass
     n.tokens = ptr<const uint32_t>(a->state_tokens.address);
-    n.range_off = reinterpret_cast<uint32_t*>(ws + L.range_off);
-    n.range_rec = reinterpret_cast<uint32_t*>(ws + L.range_rec);
+    n.range_index = reinterpret_cast<uint4*>(ws + L.range_index);
     n.row_tiles = reinterpret_cast<uint32_t*>(ws + L.row_tiles);
     n.ranges = L.fb_tiles;
     n.records = reinterpret_cast<mf::TileRecord*>(ws + L.records);
@@ -777,8 +775,7 @@ mf::PassArgs pass_args(const mf_decode_tail_args* a, const TailLayout& L, char* 
   p.head = fallback_args(a, L, ws);
   p.row_meta = reinterpret_cast<const mf::RowMeta*>(ws + L.row_meta);
   p.row_tiles = reinterpret_cast<const uint32_t*>(ws + L.row_tiles);
-  p.range_off = reinterpret_cast<const uint32_t*>(ws + L.range_off);
-  p.range_rec = reinterpret_cast<const uint32_t*>(ws + L.range_rec);
+  p.range_index = reinterpret_cast<const uint4*>(ws + L.range_index);
   p.tokens = ptr<const uint32_t>(a->state_tokens.address);
   p.z_hi = reinterpret_cast<const uint16_t*>(ws + L.y_hi);
   p.row_norm = reinterpret_cast<const float*>(ws + L.row_norm);

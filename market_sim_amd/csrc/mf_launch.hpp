@@ -117,18 +117,17 @@ struct TailNormArgs {
   uint32_t* fb_slot_row;   // [fb_m]
   float* fb_slot_norm;     // [fb_m]
   float* fb_slot_slack;    // [fb_m]
-  // Range index of the table pass (range_off null: none).  A second wave of
-  // each row's workgroup walks the row's list (ascending ids expected) and
-  // writes, per 192-token range g of the vocabulary, the list position of
-  // the row's first id >= 192 g (range_off[g * rows + r], g <= ranges)
-  // and, for ranges holding ids of the row, their record index among the
-  // row's non-empty ranges (range_rec[g * rows + r]); row_tiles[r] = the row's
-  // record count, with kRangesUnused set when the list is not strictly
-  // ascending or holds an id >= V (the wave then writes the row's single
-  // record itself: rescore the whole list, or the invalid row).
+  // Range index of the table pass (range_index null: none): per 192-token
+  // range g of the vocabulary and row r, range_index[g * rows + r] =
+  // {lo, hi, record, 0}: the positions [lo, hi) of the row's ids in the
+  // range (lo = hi = 0: none) and the range's record index among the row's
+  // non-empty ranges; row_tiles[r] = the row's record count, with
+  // kRangesUnused set when the list is not strictly ascending or holds an
+  // id >= V (the norm kernel then writes the row's single record itself:
+  // rescore the whole list, or the invalid row).  Walk workgroups of the
+  // norm launch build it (mf_prep.hpp).
   const uint32_t* tokens;  // the state lists (range index only)
-  uint32_t* range_off;     // [ranges + 1, rows]
-  uint32_t* range_rec;     // [ranges, rows]
+  uint4* range_index;      // [ranges, rows]
   uint32_t* row_tiles;     // [rows]
   uint32_t ranges;
   TileRecord* records;     // [rows, max_recs]
@@ -293,8 +292,7 @@ struct PassArgs {
   FallbackArgs head;          // m = 0: no unrestricted rows
   const RowMeta* row_meta;
   const uint32_t* row_tiles;  // [rows]
-  const uint32_t* range_off;  // [ranges + 1, rows]
-  const uint32_t* range_rec;  // [ranges, rows]
+  const uint4* range_index;   // [ranges, rows] {lo, hi, record, 0}
   const uint32_t* tokens;     // state lists
   const uint16_t* z_hi;       // [rows, H] FP16 hi of z = x * w
   const float* row_norm;      // [rows] bound of ||z||

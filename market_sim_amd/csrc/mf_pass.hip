@@ -209,9 +209,10 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
     const uint32_t ri = tid < rows ? tid : 0u;
     const RowMeta m = p.row_meta[ri];
     const uint32_t rt = p.row_tiles[ri];
-    const uint32_t lo_r = p.range_off[static_cast<uint64_t>(tile) * rows + ri];
-    const uint32_t hi_r = p.range_off[static_cast<uint64_t>(tile + 1u) * rows + ri];
-    const uint32_t rec_r = p.range_rec[static_cast<uint64_t>(tile) * rows + ri];
+    const uint4 ix = p.range_index[static_cast<uint64_t>(tile) * rows + ri];
+    const uint32_t lo_r = ix.x;
+    const uint32_t hi_r = ix.y;
+    const uint32_t rec_r = ix.z;
     const float norm_r = p.row_norm[ri];
     const float slack_r = p.row_slack[ri];
     {

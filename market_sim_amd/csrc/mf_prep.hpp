@@ -223,39 +223,46 @@ __device__ inline void prep_item(const TailNormArgs& a, uint32_t item, float* ld
   }
 }
 
-// The range index of row r for the table pass (TailNormArgs range_off,
-// range_rec, row_tiles; range-major, so the pass reads each range's entries
-// of all rows contiguously), built by kWalkWaves waves of the row's
-// workgroup in three phases separated by workgroup barriers:
+// The range index of row r for the table pass (TailNormArgs range_index,
+// row_tiles): per 192-token range g of the vocabulary, the positions
+// [lo, hi) of the row's ids in the range and its record index among the
+// row's non-empty ranges (0, 0, 0 for an empty range), range-major so the
+// pass reads one range's entries of all rows contiguously.  Built by the
+// kWalkWaves waves of a workgroup of its own (the norm items run in other
+// workgroups of the same launch), with one workgroup barrier:
 //
-//   range_begin  every walk wave finds the row's list [b, b + c); the LDS
-//                table is cleared.
 //   range_walk   wave `part` walks its share of the list's 64-id chunks,
-//                each lane also loading its id's predecessor: an id whose
-//                predecessor lies in an earlier range opens its range, which
-//                records the id's position and its rank among this wave's
-//                openers (tagged with the wave).
-//   range_end    (one wave) ranks become record indices (earlier waves'
-//                opener counts added), ranges without ids start where the
-//                next opened one does (or at the end of the list: a suffix
-//                minimum), and the index is written out coalesced.
+//                each lane also loading its id's predecessor.  An id whose
+//                predecessor lies in an earlier range opens its range: it
+//                records its position as the range's lo, its rank among this
+//                wave's openers, a bit in this wave's own bitmap (cleared by
+//                the wave itself, so no wave waits for another before
+//                walking), and its position as the hi of the predecessor's
+//                range; the list's last id closes its own range at the end.
+//   range_end    (after the barrier) every range g's entry: opened when a
+//                wave's bit says so, ranks made record indices by adding the
+//                opener counts of earlier waves; written out coalesced.
 //
 // A list that is not strictly ascending, or holds an id >= V, is not
 // indexed: the row gets one record covering its whole list, "rescore all"
-// (exact, in the finalize) or "invalid".  Ids past the vocabulary never
-// index past range `ranges`.  LDS (RangeLds): 2 (ranges + 1) + 2 kWalkWaves
-// words.
-constexpr uint32_t kWalkWaves = 3;
-constexpr uint32_t kNotOpened = 0xFFFFFFFFu;
+// (exact, in the finalize) or "invalid".  LDS: range_lds_words(ranges).
+constexpr uint32_t kWalkWaves = 4;
+
+__host__ __device__ constexpr uint32_t range_bit_words(uint32_t ranges) { return ranges / 32u + 1u; }
+__host__ __device__ constexpr uint32_t range_lds_words(uint32_t ranges) {
+  return 3u * ranges + kWalkWaves * (2u + range_bit_words(ranges));
+}
 
 struct RangeLds {
-  uint32_t* offs;   // [ranges + 1] position of each opened range's first id
-  uint32_t* recs;   // [ranges + 1] rank | wave << 24 (kNotOpened)
+  uint32_t* lo;     // [ranges] position of each opened range's first id
+  uint32_t* hi;     // [ranges] one past its last id
+  uint32_t* rank;   // [ranges] rank of each opened range among its wave's openers
   uint32_t* count;  // [kWalkWaves] openers per wave
   uint32_t* flags;  // [kWalkWaves] bit 0: an id >= V, bit 1: not ascending
+  uint32_t* bits;   // [kWalkWaves][range_bit_words] ranges each wave opened
   static __device__ RangeLds at(uint32_t* base, uint32_t ranges) {
-    return RangeLds{base, base + ranges + 1u, base + 2u * (ranges + 1u),
-                    base + 2u * (ranges + 1u) + kWalkWaves};
+    uint32_t* q = base + 3u * ranges;
+    return RangeLds{base, base + ranges, base + 2u * ranges, q, q + kWalkWaves, q + 2u * kWalkWaves};
   }
 };
 
@@ -265,8 +272,8 @@ struct RangeRow {
   bool indexed;   // a restricted row
 };
 
-__device__ inline RangeRow range_begin(const TailNormArgs& a, uint32_t r, const RangeLds& L,
-                                       uint32_t part) {
+// The row's list (every walk wave finds it itself).
+__device__ inline RangeRow range_row(const TailNormArgs& a, uint32_t r) {
   const uint32_t lane = threadIdx.x % kWave;
   RowList l{};
   if (lane == 0) l = row_list(a, r);
@@ -274,14 +281,6 @@ __device__ inline RangeRow range_begin(const TailNormArgs& a, uint32_t r, const 
   w.b = __shfl(l.b, 0);
   w.c = __shfl(l.e, 0) - w.b;
   w.indexed = __shfl(l.meta.kind, 0) == kRowRestricted;
-  if (!w.indexed) {
-    if (part == 0 && lane == 0) a.row_tiles[r] = 0u;
-    return w;
-  }
-  for (uint32_t g = part * kWave + lane; g <= a.ranges; g += kWalkWaves * kWave) {
-    L.offs[g] = w.c;
-    L.recs[g] = kNotOpened;
-  }
   return w;
 }
 
@@ -291,6 +290,10 @@ __device__ inline void range_walk(const TailNormArgs& a, const RangeRow& w, cons
   const uint32_t G = a.ranges;
   const uint32_t b = w.b;
   const uint32_t c = w.c;
+  const uint32_t words = range_bit_words(G);
+  uint32_t* bits = L.bits + part * words;
+  for (uint32_t i = lane; i < words; i += kWave) bits[i] = 0u;
+  wave_sync();
   const uint32_t chunks = (c + kWave - 1) / kWave;
   const uint32_t lo = chunks * part / kWalkWaves * kWave;        // this wave's positions
   const uint32_t hi = chunks * (part + 1) / kWalkWaves * kWave;  // [lo, min(hi, c))
@@ -320,16 +323,19 @@ __device__ inline void range_walk(const TailNormArgs& a, const RangeRow& w, cons
       const uint32_t t = in ? ids[u] : kInvalidToken;
       const uint32_t tp = p > 0u ? pre[u] : kInvalidToken;  // no predecessor at p = 0
       const uint32_t gt = t < a.V ? t / kHeadTileTokens : G;
-      const uint32_t gp = tp < a.V ? tp / kHeadTileTokens : kInvalidToken;
+      const uint32_t gp = tp < a.V ? tp / kHeadTileTokens : G;
       bad |= in && t >= a.V;
       unsorted |= in && p > 0 && t <= tp;
-      const bool opens = in && t < a.V && gt != gp;
+      const bool opens = in && gt < G && gt != gp;
       const uint64_t m = __ballot(opens);
-      if (opens) {  // LDS only: global stores under a branch would stall the loads
-        L.offs[gt] = p;
-        L.recs[gt] = (opened + static_cast<uint32_t>(__popcll(m & ((1ull << lane) - 1ull)))) |
-                     (part << 24);
+      // LDS only: global stores under a branch would stall the loads
+      if (opens) {
+        L.lo[gt] = p;
+        L.rank[gt] = opened + static_cast<uint32_t>(__popcll(m & ((1ull << lane) - 1ull)));
+        atomicOr(&bits[gt / 32u], 1u << (gt % 32u));
+        if (p > 0u && gp < G) L.hi[gp] = p;
       }
+      if (in && p == c - 1u && gt < G) L.hi[gt] = c;
       opened += static_cast<uint32_t>(__popcll(m));
     }
   };
@@ -349,12 +355,13 @@ __device__ inline void range_walk(const TailNormArgs& a, const RangeRow& w, cons
   }
 }
 
+// All kWalkWaves waves (after the barrier): range g = tid, tid + 256, ...
 __device__ inline void range_end(const TailNormArgs& a, uint32_t r, const RangeRow& w,
                                  const RangeLds& L) {
-  const uint32_t lane = threadIdx.x % kWave;
+  const uint32_t tid = threadIdx.x;
   const uint32_t G = a.ranges;
   const uint32_t rows = a.rows;
-  const uint32_t c = w.c;
+  const uint32_t words = range_bit_words(G);
   uint32_t base[kWalkWaves];
   uint32_t tiles = 0u;
   uint32_t flags = 0u;
@@ -364,61 +371,41 @@ __device__ inline void range_end(const TailNormArgs& a, uint32_t r, const RangeR
     tiles += L.count[i];
     flags |= L.flags[i];
   }
-  // offs[g] = min(offs[g .. G]): segment minima, a suffix minimum over the
-  // lanes, then each segment from its right end
-  const uint32_t seg = (G + kWave) / kWave;  // ceil((G + 1) / 64)
-  const uint32_t g0 = lane * seg;
-  uint32_t mine = c;
-  for (uint32_t i = 0; i < seg; ++i) {
-    if (g0 + i <= G) mine = L.offs[g0 + i] < mine ? L.offs[g0 + i] : mine;
-  }
-  uint32_t right = mine;  // minimum over lanes >= this one
-  for (int d = 1; d < kWave; d <<= 1) {
-    const uint32_t o = static_cast<uint32_t>(__shfl_down(static_cast<int>(right), d));
-    if (lane + d < kWave && o < right) right = o;
-  }
-  uint32_t run = static_cast<uint32_t>(__shfl_down(static_cast<int>(right), 1));
-  if (lane == kWave - 1) run = c;
-  for (uint32_t i = seg; i-- > 0;) {
-    if (g0 + i <= G) {
-      run = L.offs[g0 + i] < run ? L.offs[g0 + i] : run;
-      L.offs[g0 + i] = run;
-    }
-  }
-  wave_sync();
-  for (uint32_t g = lane; g <= G; g += kWave) {
-    a.range_off[static_cast<uint64_t>(g) * rows + r] = L.offs[g];
-    const uint32_t q = L.recs[g];
-    if (g < G) {
-      a.range_rec[static_cast<uint64_t>(g) * rows + r] =
-          q == kNotOpened ? 0u : (q & 0xFFFFFFu) + base[(q >> 24) < kWalkWaves ? (q >> 24) : 0u];
-    }
-  }
-  // the whole-list record of a list that is not indexed: its lowest id
-  if (flags != 0u) {
-    uint32_t mt = kInvalidToken;
-    uint32_t mp = 0u;
-    for (uint32_t p = lane; p < c; p += kWave) {
-      const uint32_t t = a.tokens[w.b + p];
-      if (t < mt) {
-        mt = t;
-        mp = p;
+  if (flags == 0u) {
+    for (uint32_t g = tid; g < G; g += kWalkWaves * kWave) {
+      uint4 e = {0u, 0u, 0u, 0u};
+#pragma unroll
+      for (uint32_t i = 0; i < kWalkWaves; ++i) {
+        if ((L.bits[i * words + g / 32u] >> (g % 32u)) & 1u) e = uint4{L.lo[g], L.hi[g], L.rank[g] + base[i], 0u};
       }
+      a.range_index[static_cast<uint64_t>(g) * rows + r] = e;
     }
-    wave_min_token(mt, mp);
-    if (lane == 0) {
-      TileRecord* rec = a.records + static_cast<uint64_t>(r) * a.max_recs;
-      rec->best_lower = -__builtin_huge_valf();
-      rec->flags = (flags & 1u) ? kTileInvalid : kTileRescoreAll;
-      rec->min_token = mt;
-      rec->min_pos = mp;
-      rec->begin = 0u;
-      rec->count = c;
-      rec->n_members = 0u;
-      a.row_tiles[r] = 1u | kRangesUnused;
+    if (tid == 0) a.row_tiles[r] = tiles;
+    return;
+  }
+  // a list that is not indexed: one whole-list record with its lowest id
+  if (tid >= kWave) return;
+  const uint32_t lane = tid;
+  uint32_t mt = kInvalidToken;
+  uint32_t mp = 0u;
+  for (uint32_t p = lane; p < w.c; p += kWave) {
+    const uint32_t t = a.tokens[w.b + p];
+    if (t < mt) {
+      mt = t;
+      mp = p;
     }
-  } else if (lane == 0) {
-    a.row_tiles[r] = tiles;
+  }
+  wave_min_token(mt, mp);
+  if (lane == 0) {
+    TileRecord* rec = a.records + static_cast<uint64_t>(r) * a.max_recs;
+    rec->best_lower = -__builtin_huge_valf();
+    rec->flags = (flags & 1u) ? kTileInvalid : kTileRescoreAll;
+    rec->min_token = mt;
+    rec->min_pos = mp;
+    rec->begin = 0u;
+    rec->count = w.c;
+    rec->n_members = 0u;
+    a.row_tiles[r] = 1u | kRangesUnused;
   }
 }
 

@@ -31,30 +31,29 @@ namespace {
 
 constexpr int kThreads = 256;
 
-// Workgroup i runs prep item i (mf_prep.hpp): row i < rows, else slot
-// i - rows of the MFMA head's panel.  With a range index the workgroup has
-// kWalkWaves more waves, which index row i's list for the table pass while
-// wave 0 normalizes.
-__global__ __launch_bounds__((1 + kWalkWaves) * kWave) void tail_norm_kernel(TailNormArgs a) {
+// Workgroup i < items runs prep item i (mf_prep.hpp): row i < rows, else
+// slot i - rows of the MFMA head's panel, with its first wave.  With a range
+// index, workgroup items + r indexes row r's list for the table pass with
+// all kWalkWaves waves.
+__global__ __launch_bounds__(kWalkWaves * kWave) void tail_norm_kernel(TailNormArgs a) {
   extern __shared__ __align__(16) float lds[];
   __shared__ float inverse_shared;
-  if (a.range_off == nullptr) {  // one wave
-    prep_item(a, blockIdx.x, lds, &inverse_shared, true);
+  const uint32_t items = a.rows + (a.fb_panel != nullptr ? a.fb_m : 0u);
+  const uint32_t wave = threadIdx.x / kWave;
+  if (blockIdx.x < items) {
+    if (wave == 0) prep_item(a, blockIdx.x, lds, &inverse_shared, true);
     return;
   }
-  const uint32_t wave = threadIdx.x / kWave;
-  const bool row = blockIdx.x < a.rows;
-  const RangeLds L = RangeLds::at(reinterpret_cast<uint32_t*>(lds + 3u * a.H), a.ranges);
-  RangeRow w{};
-  if (wave > 0 && row) w = range_begin(a, blockIdx.x, L, wave - 1);
-  __syncthreads();
-  if (wave == 0) {
-    prep_item(a, blockIdx.x, lds, &inverse_shared, true);
-  } else if (row && w.indexed) {
-    range_walk(a, w, L, wave - 1);
+  const uint32_t r = blockIdx.x - items;
+  const RangeLds L = RangeLds::at(reinterpret_cast<uint32_t*>(lds), a.ranges);
+  const RangeRow w = range_row(a, r);
+  if (!w.indexed) {
+    if (threadIdx.x == 0) a.row_tiles[r] = 0u;
+    return;
   }
+  range_walk(a, w, L, wave);
   __syncthreads();
-  if (wave == 1 && row && w.indexed) range_end(a, blockIdx.x, w, L);
+  range_end(a, r, w, L);
 }
 
 // ---------------------------------------------------------------------------
@@ -327,12 +326,14 @@ __global__ __launch_bounds__(kWave) void finalize_kernel(FinalizeArgs a) {
 } // namespace
 
 hipError_t launch_tail_norm(const TailNormArgs& args, hipStream_t stream) {
-  const size_t lds =
-      3u * static_cast<size_t>(args.H) * sizeof(float) +
-      (args.range_off != nullptr ? (2u * (args.ranges + 1u) + 2u * kWalkWaves) * sizeof(uint32_t) : 0u);
+  const size_t norm_lds = 3u * static_cast<size_t>(args.H) * sizeof(float);
+  const size_t walk_lds =
+      args.range_index != nullptr ? range_lds_words(args.ranges) * sizeof(uint32_t) : 0u;
   const uint32_t slots = args.fb_panel != nullptr ? args.fb_m : 0u;
-  const uint32_t threads = args.range_off != nullptr ? (1u + kWalkWaves) * kWave : kWave;
-  hipLaunchKernelGGL(tail_norm_kernel, dim3(args.rows + slots), dim3(threads), lds, stream, args);
+  const uint32_t walks = args.range_index != nullptr ? args.rows : 0u;
+  const uint32_t threads = walks > 0 ? kWalkWaves * kWave : kWave;
+  hipLaunchKernelGGL(tail_norm_kernel, dim3(args.rows + slots + walks), dim3(threads),
+                     norm_lds > walk_lds ? norm_lds : walk_lds, stream, args);
   return hipGetLastError();
 }
 
