@@ -6,16 +6,17 @@ log-uniform in [1, 4096]; 10% of rows unrestricted (MFMA fallback); hidden
 N(0, 1) through the final RMSNorm.  Synthetic data (seeded), inputs resident
 in HBM before the timed region.
 
-One step = one mf_decode_tail_f16 call over the whole pack: RMSNorm + plan,
-CSR gather head of the restricted rows, MFMA head of the unrestricted rows,
+One step = one mf_decode_tail_f16 call over the whole pack: RMSNorm and the
+range index of each row's (ascending) list, one pass over the table scoring
+the restricted rows' candidates and the unrestricted rows on MFMA,
 DFA/selection outputs.  Eight copies of the embedding (453 MB > the 256 MiB
 Infinity Cache) are rotated so no step finds the table cached by the previous
 one.
 
 Prints one JSON line: metric/value (sequences per second), the roofline of
-the dominant kernel (the CSR gather head) from HIP events on its stream, the
-full-vocabulary comparator ("x vs full head"), and the CPU oracle timed on
-this host's cores.
+the dominant kernel (the table pass) from HIP events on its stream, the same
+step on the gather + MFMA head kernels, the full-vocabulary comparator
+("x vs full head"), and the CPU oracle timed on this host's cores.
 """
 from __future__ import annotations
 
@@ -46,6 +47,8 @@ def parse():
                    help="budget of the CPU oracle baseline sample")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-full", action="store_true")
+    p.add_argument("--no-gather-path", action="store_true",
+                   help="skip timing the same step on the gather + MFMA head kernels")
     p.add_argument("--no-reference-bench", action="store_true",
                    help="skip the reference's 12-cell output-head benchmark")
     p.add_argument("--calibration-copy-mib", type=int, default=0,
@@ -56,8 +59,12 @@ def parse():
 
 def algorithmic_bytes(w) -> dict:
     """Bytes one launch must move:
-    gather  2 H U + 4 N + 4 H B_r + 4 (B_r + 1) + 12 B_r
-    fallback 2 V H + 4 H B_u + 8 B_u, flops 2 B_u H V."""
+    gather   2 H U + 4 N + 4 H B_r + 4 (B_r + 1) + 12 B_r
+    fallback 2 V H + 4 H B_u + 8 B_u, flops 2 B_u H V
+    pass     2 H T + 4 N + 4 H B + 4 (B_r + 1) + 12 B with T = V when there
+             are unrestricted rows (the table is read once for both kinds of
+             rows), else U; flops 2 (B_u H V + N H) (candidates and the
+             unrestricted rows' head, FP16 hi of z)."""
     H, V = w.hidden, w.vocab
     counts = w.row_counts()
     restricted = w.row_state < w.states
@@ -67,9 +74,13 @@ def algorithmic_bytes(w) -> dict:
     U = w.distinct_restricted_ids()
     gather = 2 * H * U + 4 * N + 4 * H * B_r + 4 * (B_r + 1) + 12 * B_r
     logical = 2 * H * N + 4 * N + 4 * H * B_r + 4 * (B_r + 1) + 12 * B_r
+    B = w.rows
+    T = V if B_u > 0 else U
     return dict(gather=gather, gather_logical=logical, N=N, U=U, B_r=B_r, B_u=B_u,
                 fallback_bytes=2 * V * H + 4 * H * B_u + 8 * B_u,
-                fallback_flops=2 * B_u * H * V)
+                fallback_flops=2 * B_u * H * V,
+                pass_bytes=2 * H * T + 4 * N + 4 * H * B + 4 * (B_r + 1) + 12 * B,
+                pass_flops=2 * (B_u * H * V + N * H))
 
 
 def time_loop(tail, stages, steps, warmup, copies):
@@ -277,10 +288,28 @@ def main() -> int:
             torch.mul(src, 1.0, out=dst)
         torch.cuda.synchronize()
         del src, dst
-    gather_ms = kernel_loop(tail, "restricted", args.steps, args.copies)
-    fb_ms = kernel_loop(tail, "unrestricted", args.steps, args.copies)
-    achieved = alg["gather"] / (gather_ms * 1e-3) / 1e9
-    traffic = profiled_traffic("gather_mfma_kernel")
+    # the dominant kernel: the table pass (sorted lists with unrestricted
+    # rows: one kernel for both kinds of rows) or the CSR gather
+    one_pass = tail.table_pass
+    main_ms = kernel_loop(tail, "restricted", args.steps, args.copies)
+    if one_pass:
+        main_bytes, main_name = alg["pass_bytes"], "pass_kernel (one table pass: candidates + unrestricted head)"
+        achieved = main_bytes / (main_ms * 1e-3) / 1e9
+        traffic = profiled_traffic("pass_kernel")
+        fb = {"kernel": "inside pass_kernel (MFMA on the FP16 hi of z)", "rows": alg["B_u"],
+              "mfma_TFLOPs": round(alg["pass_flops"] / (main_ms * 1e-3) / 1e12, 2),
+              "mfma_util": round(alg["pass_flops"] / (main_ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)}
+    else:
+        main_bytes, main_name = alg["gather"], "gather_mfma_kernel (CSR gather)"
+        achieved = main_bytes / (main_ms * 1e-3) / 1e9
+        traffic = profiled_traffic("gather_mfma_kernel")
+        fb_ms = kernel_loop(tail, "unrestricted", args.steps, args.copies)
+        fb = {"kernel": "vocab_head_kernel (MFMA head, unrestricted rows)", "rows": alg["B_u"],
+              "avg_launch_us": round(fb_ms * 1e3, 2),
+              "hbm_GBs": round(alg["fallback_bytes"] / (fb_ms * 1e-3) / 1e9, 1),
+              "hbm_frac": round(alg["fallback_bytes"] / (fb_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+              "mfma_TFLOPs": round(alg["fallback_flops"] / (fb_ms * 1e-3) / 1e12, 2),
+              "mfma_util": round(alg["fallback_flops"] / (fb_ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)}
     result = {
         "metric": METRIC,
         "value": round(w.rows / (total_ms * 1e-3), 1),
@@ -299,23 +328,32 @@ def main() -> int:
                    "unrestricted_rows": alg["B_u"], "candidates": alg["N"],
                    "distinct_ids": alg["U"], "table_copies": args.copies,
                    "order": "fma chain (greedy.cu:171-176)"},
-        "roofline": {"kernel": "gather_mfma_kernel (CSR gather)", "bound": "hbm",
+        "roofline": {"kernel": main_name, "bound": "hbm",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "bytes_per_launch": alg["gather"], "avg_launch_us": round(gather_ms * 1e3, 2),
+                     "bytes_per_launch": main_bytes, "avg_launch_us": round(main_ms * 1e3, 2),
                      "traffic_source": "profiles/decode_tail_cfg3_traffic.md"},
         "stages_us": {k: round(v[0] * 1e3, 2) for k, v in st.items()},
         "stages_serial_ms": round(stages_ms, 5),
-        "effective_gather_GBs": round(alg["gather_logical"] / (gather_ms * 1e-3) / 1e9, 1),
-        "fallback": {"kernel": "vocab_head_kernel (MFMA head, unrestricted rows)", "rows": alg["B_u"],
-                     "avg_launch_us": round(fb_ms * 1e3, 2),
-                     "hbm_GBs": round(alg["fallback_bytes"] / (fb_ms * 1e-3) / 1e9, 1),
-                     "hbm_frac": round(alg["fallback_bytes"] / (fb_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                     "mfma_TFLOPs": round(alg["fallback_flops"] / (fb_ms * 1e-3) / 1e12, 2),
-                     "mfma_util": round(alg["fallback_flops"] / (fb_ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)},
+        "effective_gather_GBs": round(alg["gather_logical"] / (main_ms * 1e-3) / 1e9, 1),
+        "fallback": fb,
         "wall_ms_per_step": round(wall_ms, 4),
         "token_checksum": int(np.bitwise_xor.reduce(tok.astype(np.uint64) * np.arange(1, tok.size + 1, dtype=np.uint64))),
     }
+    if one_pass and not args.no_gather_path:
+        # the same step on the gather + MFMA head kernels (no sorted-lists
+        # declaration), same tokens required
+        g = DeviceTail(w, copies=args.copies, sorted_lists=False)
+        g_ms, _, _ = time_loop(g, ["tail"], args.steps, args.warmup, args.copies)
+        gtok, _, _ = g.results()
+        g_gather = kernel_loop(g, "restricted", args.steps, args.copies)
+        g_head = kernel_loop(g, "unrestricted", args.steps, args.copies)
+        result["gather_path"] = {
+            "ms_per_step": round(g_ms, 5), "token_parity": bool(np.array_equal(gtok, tok)),
+            "gather_us": round(g_gather * 1e3, 2), "head_us": round(g_head * 1e3, 2),
+            "gather_frac": round(alg["gather"] / (g_gather * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "head_frac": round(alg["fallback_bytes"] / (g_head * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        del g
     if not args.no_full:
         full = DeviceTail(w, copies=args.copies, full=True)
         full_ms, _, _ = time_loop(full, ["full"], max(10, args.steps // 4), 5, args.copies)

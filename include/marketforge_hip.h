@@ -202,12 +202,14 @@ mf_status mf_linear_f16(mf_buffer input, mf_buffer weight, mf_buffer output,
  * state is MF_STATE_INVALID, as for every invalid row.
  *
  * flags: MF_TAIL_SORTED_LISTS -- every state's list is strictly ascending,
- * as TokenDfa keeps its arcs (src/grammar/token_dfa.cpp:100-109).  With
- * hidden % 64 == 0, hidden <= 576 and rows <= 256 the tail then scores the
- * restricted and the unrestricted rows in one pass over the table (the
- * restricted-stage entry point runs it; the unrestricted one does nothing).
- * Results are the same with or without the flag; a list that turns out not
- * to be ascending is rescored in full, exactly.
+ * as TokenDfa keeps its arcs (src/grammar/token_dfa.cpp:100-109).  When the
+ * call has unrestricted rows (so the whole table is read anyway), or with
+ * MF_TAIL_TABLE_PASS as well, and hidden % 64 == 0, hidden <= 576 and
+ * rows <= 256, the tail then scores the restricted and the unrestricted
+ * rows in one pass over the table (the restricted-stage entry point runs
+ * it; the unrestricted one does nothing).  Results are the same with or
+ * without the flags; a list that turns out not to be ascending is rescored
+ * in full, exactly.  MF_TAIL_TABLE_PASS alone changes nothing.
  *
  * Workspace: caller-allocated device memory of mf_decode_tail_workspace_bytes
  * bytes, zero-filled once by mf_workspace_init before first use.  Every call
@@ -237,14 +239,24 @@ typedef struct mf_decode_tail_args {
   uint64_t max_count;          /* longest state list (table builder's figure) */
   uint64_t unrestricted_count;
   mf_buffer row_sequence;      /* u32 [rows] or address 0: see "Sequence table" */
-  uint64_t flags;              /* MF_TAIL_HOLD_FINISHED | MF_TAIL_SORTED_LISTS */
+  uint64_t flags;              /* MF_TAIL_HOLD_FINISHED | MF_TAIL_SORTED_LISTS | MF_TAIL_TABLE_PASS */
 } mf_decode_tail_args;
 
 #define MF_TAIL_HOLD_FINISHED 1u
 #define MF_TAIL_SORTED_LISTS 2u
+#define MF_TAIL_TABLE_PASS 4u
 
 mf_status mf_decode_tail_workspace_bytes(const mf_decode_tail_args* args,
                                          uint64_t* bytes);
+
+/* Which kernels mf_decode_tail_f16 runs for these arguments (no reference
+ * counterpart; for benchmarks and tests that report per-kernel figures):
+ * MF_TAIL_PATH_GATHER (restricted stage = CSR gather, unrestricted stage =
+ * MFMA head) or MF_TAIL_PATH_TABLE_PASS (restricted stage = one pass over
+ * the table for both kinds of rows, unrestricted stage empty). */
+#define MF_TAIL_PATH_GATHER 0u
+#define MF_TAIL_PATH_TABLE_PASS 1u
+mf_status mf_decode_tail_path(const mf_decode_tail_args* args, uint32_t* path);
 /* Zero-fills a workspace with a fill kernel (safe under graph capture). */
 mf_status mf_workspace_init(mf_buffer workspace, uintptr_t stream);
 
@@ -256,9 +268,10 @@ mf_status mf_decode_tail_f16(const mf_decode_tail_args* args, uintptr_t stream);
  * (e.g. the unrestricted stage on a second stream once prepare is done).
  * prepare:      final RMSNorm into the workspace, per-row metadata, the FP16
  *               split of unrestricted rows; presets invalid rows' outputs.
- * restricted:   CSR gather of the restricted rows into tile records.
+ * restricted:   CSR gather of the restricted rows into tile records (table
+ *               pass: both kinds of rows, see MF_TAIL_SORTED_LISTS).
  * unrestricted: MFMA full-vocabulary head of unrestricted_rows into tile
- *               records.
+ *               records (table pass: nothing).
  * finalize:     per row, merges the records, rescores the surviving
  *               candidates in the reference order, writes the outputs.
  * restricted and unrestricted need prepare; finalize needs both. */

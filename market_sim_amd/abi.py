@@ -31,6 +31,9 @@ ORDER_FMA_CHAIN = 0
 ORDER_MUL_ADD_CHAIN = 1
 TAIL_HOLD_FINISHED = 1
 TAIL_SORTED_LISTS = 2
+TAIL_TABLE_PASS = 4
+TAIL_PATH_GATHER = 0
+TAIL_PATH_TABLE_PASS = 1
 ABI_VERSION = 3
 
 _U64 = ctypes.c_uint64
@@ -87,6 +90,8 @@ SIGNATURES = {
     "mf_linear_f16": (Status, [Buffer, Buffer, Buffer, _U64, _U64, _U64, _UP]),
     "mf_decode_tail_workspace_bytes": (
         Status, [ctypes.POINTER(DecodeTailArgs), ctypes.POINTER(_U64)]),
+    "mf_decode_tail_path": (
+        Status, [ctypes.POINTER(DecodeTailArgs), ctypes.POINTER(ctypes.c_uint32)]),
     "mf_workspace_init": (Status, [Buffer, _UP]),
     "mf_decode_tail_f16": (Status, [ctypes.POINTER(DecodeTailArgs), _UP]),
     "mf_decode_tail_prepare": (Status, [ctypes.POINTER(DecodeTailArgs), _UP]),

@@ -504,9 +504,11 @@ uint32_t gather_tile(uint64_t H) {
 }
 
 // The table pass (one launch for restricted and unrestricted rows): lists
-// declared ascending, the panel tile of the head in LDS, the row plan in LDS.
+// declared ascending, the whole table read anyway (unrestricted rows) or the
+// pass asked for, a panel tile that fits LDS, the row plan in LDS.
 bool table_pass(const mf_decode_tail_args* a) {
-  return (a->flags & MF_TAIL_SORTED_LISTS) && a->hidden % 64u == 0 &&
+  return (a->flags & MF_TAIL_SORTED_LISTS) &&
+         (a->unrestricted_count > 0 || (a->flags & MF_TAIL_TABLE_PASS)) && a->hidden % 64u == 0 &&
          mf::panel_tile_bytes(a->hidden) <= mf::kPanelLdsMaxBytes && a->rows <= mf::kPassRowsMax;
 }
 
@@ -538,7 +540,8 @@ mf_status validate_tail(const mf_decode_tail_args* a, bool full, TailLayout& L) 
   // the state buffers: one entry per row, or a sequence table of any
   // capacity that row_sequence indexes
   const bool table = a->row_sequence.address != 0;
-  if ((a->flags & ~static_cast<uint64_t>(MF_TAIL_HOLD_FINISHED | MF_TAIL_SORTED_LISTS)) != 0) {
+  if ((a->flags & ~static_cast<uint64_t>(MF_TAIL_HOLD_FINISHED | MF_TAIL_SORTED_LISTS |
+                                         MF_TAIL_TABLE_PASS)) != 0) {
     return status(MF_INVALID_ARGUMENT);
   }
   if (table && (a->row_state.bytes / 4u > kU32Max || a->row_state.bytes == 0 ||
@@ -850,6 +853,15 @@ mf_status mf_decode_tail_workspace_bytes(const mf_decode_tail_args* args, uint64
   const mf_status v = validate_tail(args, false, L);
   if (v.code != MF_OK) return v;
   *bytes = L.total;
+  return ok();
+}
+
+mf_status mf_decode_tail_path(const mf_decode_tail_args* args, uint32_t* path) {
+  if (path == nullptr) return status(MF_INVALID_ARGUMENT);
+  TailLayout L{};
+  const mf_status v = validate_tail(args, false, L);
+  if (v.code != MF_OK) return v;
+  *path = L.pass ? MF_TAIL_PATH_TABLE_PASS : MF_TAIL_PATH_GATHER;
   return ok();
 }
 

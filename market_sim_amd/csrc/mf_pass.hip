@@ -85,10 +85,12 @@ struct PassShared {
   uint32_t slot_row[kPassRowsMax];        // staged slot -> row (batch)
   float rf1[kPassRowsMax];                // coef * ||z|| + coef2, absolute error term
   float rf2[kPassRowsMax];
-  uint32_t ptok[kPairBatch];              // candidate k of the batch: id, window bounds
-  float pupper[kPairBatch];               // g + b (+inf: not scored)
+  uint32_t ptok[kPairBatch];              // candidate k of the batch: id, row, g + b
+  uint16_t prow[kPairBatch];
+  float pupper[kPairBatch];               // (+inf: not scored)
   uint32_t row_lower[kPassRowsMax];       // per row: max of g - b, order-preserving bits
   uint32_t row_all[kPassRowsMax];         // per row: a candidate needs the exact rescore
+  uint32_t row_members[kPassRowsMax];     // per row: candidates with g + b >= the row's lower bound
   PairEntry bent[kBucketSlots];
   uint32_t bcount[kHeadTileBlocks];
   uint32_t bfill[kHeadTileBlocks];
@@ -282,6 +284,7 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
       if (tid < rows) {
         ps.row_lower[tid] = order_bits(-__builtin_huge_valf());
         ps.row_all[tid] = 0u;
+        ps.row_members[tid] = 0u;
       }
       __syncthreads();  // slot rows, cleared counters
       uint32_t tok[2] = {0u, 0u};
@@ -312,6 +315,7 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
         blk[u] = (k < k0 + nb && c < kHeadTileTokens) ? c / 16u : kHeadTileBlocks;
         if (k < k0 + nb) {
           ps.ptok[k - k0] = tok[u];
+          ps.prow[k - k0] = static_cast<uint16_t>(row[u]);
           ps.pupper[k - k0] = __builtin_huge_valf();
           if (blk[u] < kHeadTileBlocks) {
             atomicAdd(&ps.bcount[blk[u]], 1u);
@@ -413,7 +417,8 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
         }
       };
       // one group at a time: its LDS reads complete in order, so each MFMA
-      // waits only for its own operand
+      // waits only for its own operand (a second group in flight costs
+      // register spills)
       for (uint32_t q = 0; q < nq; ++q) {
         Group<kSteps> g;
         load_group(q, g);
@@ -423,33 +428,39 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
       // the first panel tile's hi rows land while the records are written
       if (first && panels > 0u) stage_panel(0u);
 
-      // (4) one window record per (row, tile), thread per row: the best
-      // lower bound came from the scoring, so one pass finds the members;
-      // the list is ascending, so the row's lowest id here is its first
-      for (uint32_t r = r0 + tid; r < r1; r += kThreads) {
-        const uint32_t n = ps.plan.count[r];
-        if (n == 0u) continue;
-        const uint32_t kr = ps.plan.prefix[r] - k0;
-        const float L = from_order_bits(ps.row_lower[r]);
-        TileRecord* rec = p.records + static_cast<uint64_t>(r) * p.max_recs + ps.rec[r];
-        const uint32_t lo = ps.lo[r];
-        uint32_t members = 0u;
-        if (ps.row_all[r] == 0u) {
-          for (uint32_t j = 0; j < n; ++j) {
-            const float up = ps.pupper[kr + j];
-            if (up >= L) {
-              if (members < static_cast<uint32_t>(kTileMembers)) {
-                // g - b of a member is only used against the row's window
-                rec->m[members] = TileMember{ps.ptok[kr + j], lo + j, -__builtin_huge_valf(), up};
-              }
-              ++members;
+      // (4) one window record per (row, tile).  The best lower bound came
+      // from the scoring; each candidate then checks itself against its
+      // row's (members in any order: the finalize only collects them), and
+      // one thread per row writes the header.  The list is ascending, so a
+      // row's lowest id here is its first.
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const uint32_t kk = tid + u * kThreads;
+        if (kk < nb) {
+          const uint32_t r = ps.prow[kk];
+          const float up = ps.pupper[kk];
+          if (ps.row_all[r] == 0u && up >= from_order_bits(ps.row_lower[r])) {
+            const uint32_t i = atomicAdd(&ps.row_members[r], 1u);
+            if (i < static_cast<uint32_t>(kTileMembers)) {
+              const uint32_t j = k0 + kk - ps.plan.prefix[r];
+              TileRecord* rec = p.records + static_cast<uint64_t>(r) * p.max_recs + ps.rec[r];
+              // g - b of a member is only used against the row's window
+              rec->m[i] = TileMember{ps.ptok[kk], ps.lo[r] + j, -__builtin_huge_valf(), up};
             }
           }
         }
+      }
+      __syncthreads();
+      for (uint32_t r = r0 + tid; r < r1; r += kThreads) {
+        const uint32_t n = ps.plan.count[r];
+        if (n == 0u) continue;
+        const uint32_t members = ps.row_members[r];
         const bool ordinary = ps.row_all[r] == 0u && members <= static_cast<uint32_t>(kTileMembers);
-        rec->best_lower = L;
+        TileRecord* rec = p.records + static_cast<uint64_t>(r) * p.max_recs + ps.rec[r];
+        const uint32_t lo = ps.lo[r];
+        rec->best_lower = from_order_bits(ps.row_lower[r]);
         rec->flags = ordinary ? 0u : kTileRescoreAll;
-        rec->min_token = ps.ptok[kr];
+        rec->min_token = ps.ptok[ps.plan.prefix[r] - k0];
         rec->min_pos = lo;
         rec->begin = lo;
         rec->count = n;

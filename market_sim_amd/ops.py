@@ -201,6 +201,14 @@ def decode_tail_workspace_bytes(args: abi.DecodeTailArgs, full: bool = False) ->
     return n.value
 
 
+def decode_tail_path(args: abi.DecodeTailArgs) -> int:
+    """abi.TAIL_PATH_GATHER or abi.TAIL_PATH_TABLE_PASS: the kernels
+    mf_decode_tail_f16 runs for these arguments."""
+    n = ctypes.c_uint32()
+    abi.check("decode_tail_path", abi.lib().mf_decode_tail_path(ctypes.byref(args), ctypes.byref(n)))
+    return n.value
+
+
 def workspace_init(workspace: DeviceBuffer, stream: int) -> Status:
     return abi.lib().mf_workspace_init(workspace.c(), stream)
 

@@ -174,13 +174,15 @@ def test_decode_tail_sequence_table_and_flags_validation():
     assert ws_code(flags=abi.TAIL_HOLD_FINISHED) == abi.MF_OK
     assert ws_code(flags=abi.TAIL_SORTED_LISTS) == abi.MF_OK
     assert ws_code(flags=abi.TAIL_HOLD_FINISHED | abi.TAIL_SORTED_LISTS) == abi.MF_OK
-    assert ws_code(flags=4) == abi.MF_INVALID_ARGUMENT
+    assert ws_code(flags=abi.TAIL_SORTED_LISTS | abi.TAIL_TABLE_PASS) == abi.MF_OK
+    assert ws_code(flags=8) == abi.MF_INVALID_ARGUMENT
 
 
 def test_sorted_lists_flag_sizes_the_range_index():
     """MF_TAIL_SORTED_LISTS adds the table pass's range index to the
-    workspace where the pass runs (hidden % 64 == 0, hidden <= 576, rows <=
-    1024) and changes nothing where it does not."""
+    workspace where the pass runs (unrestricted rows or MF_TAIL_TABLE_PASS,
+    hidden % 64 == 0, hidden <= 576, rows <= 256) and changes nothing where
+    it does not."""
     l = abi.lib()
     n = ctypes.c_uint64()
 
@@ -189,7 +191,24 @@ def test_sorted_lists_flag_sizes_the_range_index():
         assert l.mf_decode_tail_workspace_bytes(ctypes.byref(a), ctypes.byref(n)).code == abi.MF_OK
         return n.value
 
-    assert ws(flags=abi.TAIL_SORTED_LISTS) > ws()
+    sorted_pass = abi.TAIL_SORTED_LISTS | abi.TAIL_TABLE_PASS
+    assert ws(flags=sorted_pass) > ws()
+    path = ctypes.c_uint32()
+
+    def path_of(**kw):
+        a = _tail_args(**kw)
+        assert l.mf_decode_tail_path(ctypes.byref(a), ctypes.byref(path)).code == abi.MF_OK
+        return path.value
+
+    assert path_of(flags=sorted_pass) == abi.TAIL_PATH_TABLE_PASS
+    assert path_of(flags=abi.TAIL_SORTED_LISTS) == abi.TAIL_PATH_GATHER
+    assert path_of() == abi.TAIL_PATH_GATHER
+    assert path_of(flags=abi.TAIL_TABLE_PASS) == abi.TAIL_PATH_GATHER
+    unr = dict(unrestricted_count=1, unrestricted_rows=b(0xC00000, 4))
+    assert path_of(flags=abi.TAIL_SORTED_LISTS, **unr) == abi.TAIL_PATH_TABLE_PASS
+    assert path_of(**unr) == abi.TAIL_PATH_GATHER
+    # without unrestricted rows the pass runs only when asked for
+    assert ws(flags=abi.TAIL_SORTED_LISTS) == ws()
     wide = dict(hidden=2048, x=b(0x100000, 4 * 2048 * 4), norm_weight=b(0x200000, 2048 * 4),
                 embedding=b(0x300000, 1000 * 2048 * 2))
-    assert ws(flags=abi.TAIL_SORTED_LISTS, **wide) == ws(**wide)
+    assert ws(flags=sorted_pass, **wide) == ws(**wide)

@@ -20,9 +20,10 @@ def _lib(hip):
     return hip
 
 
-# Every test runs twice: with MF_TAIL_SORTED_LISTS (the one-pass table
-# kernel; lists that are not ascending are then caught on the device and
-# rescored in full) and without it (the gather and the MFMA head).
+# Every test runs twice: with MF_TAIL_SORTED_LISTS | MF_TAIL_TABLE_PASS (the
+# one-pass table kernel, also for calls without unrestricted rows; lists
+# that are not ascending are then caught on the device and rescored in
+# full) and without them (the gather and the MFMA head).
 _LISTS = {"sorted": True}
 
 
@@ -34,7 +35,7 @@ def _lists_flag(request):
 
 def _tail(w, **kw):
     from market_sim_amd.tail import DeviceTail
-    return DeviceTail(w, sorted_lists=_LISTS["sorted"], **kw)
+    return DeviceTail(w, sorted_lists=_LISTS["sorted"], table_pass=_LISTS["sorted"], **kw)
 
 
 def _oracle(w, x=None, order=abi.ORDER_FMA_CHAIN, advance="auto", threads=8):
@@ -93,7 +94,6 @@ def test_cfg3_full_size_mul_add_order():
 def test_cfg4_dfa_tail_32_steps(advance):
     """128-state DFA, 32 steps, fresh hidden per step, states
     carried on the device from one step to the next."""
-    from market_sim_amd.tail import DeviceTail
     w = wl.config(4, seed=0)
     t = _tail(w, advance=advance)
     state = w.row_state.copy()
@@ -202,7 +202,6 @@ def test_extreme_row_scales_and_near_ties(order):
 def test_workspace_reuse_across_calls_and_shapes():
     """Arrival counters reset themselves: repeated calls on one workspace
     give identical results."""
-    from market_sim_amd.tail import DeviceTail
     w = wl.config(3, seed=11, scale_vocab=6000, scale_rows=40)
     t = _tail(w)
     first = t.run()
@@ -217,7 +216,6 @@ def test_market_dfa_real_grammar_walk():
     """The reference's market-action DFA (3230 states) as the state table:
     rows walk the grammar from the root with random hidden states."""
     from tests import cases
-    from market_sim_amd.tail import DeviceTail
     offsets, tokens, nxt = cases.market_dfa()
     rng = np.random.default_rng(0)
     rows, hidden, vocab = 32, 576, 49152
@@ -261,7 +259,6 @@ def _staged(t):
 def test_decode_tail_equals_its_stages(rows):
     """One mf_decode_tail_f16 call and the four stage calls give the same
     bits, and the oracle's."""
-    from market_sim_amd.tail import DeviceTail
     w = wl.config(3, seed=21, scale_vocab=8192, scale_rows=rows)
     assert w.unrestricted_rows.size > 0
     t = _tail(w)
@@ -282,7 +279,6 @@ def test_decode_tail_without_norm_weight():
 def test_duplicate_and_foreign_unrestricted_rows():
     """The unrestricted list names a row twice and a row whose state is
     restricted: each row is finalized once, from its own kind."""
-    from market_sim_amd.tail import DeviceTail
     w = wl.config(3, seed=23, scale_vocab=6000, scale_rows=48)
     unr = w.unrestricted_rows
     restricted = np.nonzero(w.row_state < w.states)[0]
