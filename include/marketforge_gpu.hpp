@@ -301,6 +301,12 @@ inline constexpr std::uint32_t state_invalid = MF_STATE_INVALID;
 // DecodeTailArgs::flags: a row in a state with an empty list (a finished
 // sequence) keeps that state instead of becoming invalid.
 inline constexpr std::uint64_t tail_hold_finished = MF_TAIL_HOLD_FINISHED;
+// DecodeTailArgs::flags: every state's list is strictly ascending (as
+// TokenDfa keeps its arcs); a call with unrestricted rows then reads the
+// table once for both kinds of rows.  With tail_table_pass as well, so does
+// a call without them.  Results are unchanged.
+inline constexpr std::uint64_t tail_sorted_lists = MF_TAIL_SORTED_LISTS;
+inline constexpr std::uint64_t tail_table_pass = MF_TAIL_TABLE_PASS;
 
 // Buffers and shape of one decode-tail call (see marketforge_hip.h); null
 // pointers are the optional buffers left out.
@@ -330,7 +336,7 @@ struct DecodeTailArgs {
   // next state goes to the same index of out_next_state, which may be
   // row_state itself.  Null: row_state and out_next_state hold one entry per row.
   const DeviceBuffer* row_sequence = nullptr;       // u32 [rows] or null
-  std::uint64_t flags = 0;                          // 0 or tail_hold_finished
+  std::uint64_t flags = 0;                          // tail_hold_finished | tail_sorted_lists | tail_table_pass
 };
 
 namespace detail {
