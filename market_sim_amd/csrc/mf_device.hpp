@@ -307,6 +307,11 @@ constexpr int kTileMembers = 4;
 enum : uint32_t {
   kTileInvalid = 1u,     // an id >= vocabulary: the whole row is invalid
   kTileRescoreAll = 2u,
+  // with kTileRescoreAll: every bound finite, only the members overflowed;
+  // best_lower is valid and upper_max is the tile's max of g + b, so the
+  // finalize rescores the tile only if upper_max reaches the row's best
+  // lower bound
+  kTileCrowded = 4u,
 };
 
 struct alignas(16) TileMember {
@@ -324,7 +329,7 @@ struct alignas(16) TileRecord {
   uint32_t begin;     // list position of the tile's first candidate
   uint32_t count;     // candidates in the tile
   uint32_t n_members;
-  uint32_t pad;
+  float upper_max;    // max of g + b over the tile (kTileCrowded)
   TileMember m[kTileMembers];
 };
 

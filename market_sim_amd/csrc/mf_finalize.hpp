@@ -235,7 +235,10 @@ __device__ inline void finalize_row(const FinalizeArgs& a, uint32_t r, const Row
       const uint32_t flags = h[u].y;
       inv |= (flags & kTileInvalid) ? 1u : 0u;
       any_all |= (flags & kTileRescoreAll) ? 1u : 0u;
-      if (flags == 0u) lg = __builtin_fmaxf(lg, __uint_as_float(h[u].x));
+      // ordinary and crowded tiles carry a valid best lower bound
+      if (flags == 0u || flags == (kTileRescoreAll | kTileCrowded)) {
+        lg = __builtin_fmaxf(lg, __uint_as_float(h[u].x));
+      }
       if (h[u].z < mt) {
         mt = h[u].z;
         mp = h[u].w;
@@ -258,22 +261,46 @@ __device__ inline void finalize_row(const FinalizeArgs& a, uint32_t r, const Row
   wave_min_token(mt, mp);
 
   // tiles that need every candidate rescored (non-finite values, crowded
-  // windows): exact scores, which then also bound the window
+  // windows): exact scores, which then also bound the window.  A crowded
+  // tile whose best upper bound is below the row's best lower bound holds
+  // no winner and is skipped.
+  // The tiles to rescore are found from the headers already in registers
+  // (a ballot per block of tiles), not by reading every record in turn.
   Best best = best_identity();
   if (has_all) {
-    for (uint32_t t = 0; t < ntiles; ++t) {
-      const TileRecord& q = recs[t];
-      if (!(q.flags & kTileRescoreAll)) continue;
-      const uint32_t chunk = L.cand_max < kWave ? L.cand_max : kWave;
-      for (uint32_t c0 = 0; c0 < q.count; c0 += chunk) {
-        const uint32_t n = q.count - c0 < chunk ? q.count - c0 : chunk;
-        wave_sync();
-        if (lane < n) {
-          const uint32_t p = q.begin + c0 + lane;
-          L.cand_token[lane] = virtual_list ? p : a.tokens[meta.list_begin + p];
-          L.cand_pos[lane] = p;
+    const uint32_t chunk = L.cand_max < kWave ? L.cand_max : kWave;
+    for (uint32_t base = 0; base < ntiles; base += kWave * kRecBlock) {
+      if (!resident) {
+#pragma unroll
+        for (uint32_t u = 0; u < kRecBlock; ++u) {
+          const uint32_t t = base + u * kWave + lane;
+          const bool in = t < ntiles;
+          h[u] = in ? *reinterpret_cast<const uint4*>(&recs[t]) : uint4{0u, 0u, 0u, 0u};
+          c[u] = in ? *reinterpret_cast<const uint4*>(&recs[t].begin) : uint4{0u, 0u, 0u, 0u};
         }
-        best = best_of(best, rescore_candidates(a, L, n));
+      }
+#pragma unroll
+      for (uint32_t u = 0; u < kRecBlock; ++u) {
+        const uint32_t t = base + u * kWave + lane;
+        const uint32_t flags = h[u].y;
+        const bool hopeless = (flags & kTileCrowded) && __uint_as_float(c[u].w) < lg;
+        uint64_t need = __ballot(t < ntiles && (flags & kTileRescoreAll) && !hopeless);
+        while (need != 0ull) {
+          const int src = __builtin_ctzll(need);
+          need &= need - 1ull;
+          const uint32_t begin = static_cast<uint32_t>(__shfl(static_cast<int>(c[u].x), src));
+          const uint32_t count = static_cast<uint32_t>(__shfl(static_cast<int>(c[u].y), src));
+          for (uint32_t c0 = 0; c0 < count; c0 += chunk) {
+            const uint32_t n = count - c0 < chunk ? count - c0 : chunk;
+            wave_sync();
+            if (lane < n) {
+              const uint32_t p = begin + c0 + lane;
+              L.cand_token[lane] = virtual_list ? p : a.tokens[meta.list_begin + p];
+              L.cand_pos[lane] = p;
+            }
+            best = best_of(best, rescore_candidates(a, L, n));
+          }
+        }
       }
     }
     if (best.token != kInvalidToken) lg = __builtin_fmaxf(lg, records_lower(a, r, best.score));

@@ -221,6 +221,7 @@ __device__ void mfma_tile(const GatherArgs& a, uint32_t r, uint32_t k, uint32_t 
   uint32_t mt = live ? t : kInvalidToken;
   uint32_t mp = begin + lane;
   wave_min_token(mt, mp);
+  const float U = wave_max(live ? g + b : -__builtin_huge_valf());
   const bool member = all_finite && live && g + b >= L;
   const uint64_t mask = __ballot(member);
   const uint32_t total = static_cast<uint32_t>(__popcll(mask));
@@ -231,12 +232,13 @@ __device__ void mfma_tile(const GatherArgs& a, uint32_t r, uint32_t k, uint32_t 
   }
   if (lane == 0) {
     rec->best_lower = L;
-    rec->flags = ordinary ? 0u : kTileRescoreAll;
+    rec->flags = ordinary ? 0u : (all_finite ? kTileRescoreAll | kTileCrowded : kTileRescoreAll);
     rec->min_token = mt;
     rec->min_pos = mp;
     rec->begin = begin;
     rec->count = n;
     rec->n_members = ordinary ? total : 0u;
+    rec->upper_max = U;
   }
 }
 

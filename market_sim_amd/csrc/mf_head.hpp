@@ -236,8 +236,10 @@ __device__ __forceinline__ void head_records(const FallbackArgs& f, const HeadAc
       }
     }
     if (j8 == 0u) {
+      const bool finite = slot_finite && bs < 0x1p100f;
       rec->best_lower = L;
-      rec->flags = ordinary ? 0u : kTileRescoreAll;
+      rec->flags = ordinary ? 0u : (finite ? kTileRescoreAll | kTileCrowded : kTileRescoreAll);
+      rec->upper_max = G + bs;
       rec->min_token = tok0;
       rec->min_pos = tok0;
       rec->begin = tok0;

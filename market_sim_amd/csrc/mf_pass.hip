@@ -89,6 +89,7 @@ struct PassShared {
   uint16_t prow[kPairBatch];
   float pupper[kPairBatch];               // (+inf: not scored)
   uint32_t row_lower[kPassRowsMax];       // per row: max of g - b, order-preserving bits
+  uint32_t row_upper[kPassRowsMax];       // per row: max of g + b, order-preserving bits
   uint32_t row_all[kPassRowsMax];         // per row: a candidate needs the exact rescore
   uint32_t row_members[kPassRowsMax];     // per row: candidates with g + b >= the row's lower bound
   PairEntry bent[kBucketSlots];
@@ -283,6 +284,7 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
       if (tid >= r0 && tid < r1 && ps.plan.count[tid] > 0u) ps.slot_row[ps.rprefix[tid] - s0] = tid;
       if (tid < rows) {
         ps.row_lower[tid] = order_bits(-__builtin_huge_valf());
+        ps.row_upper[tid] = order_bits(-__builtin_huge_valf());
         ps.row_all[tid] = 0u;
         ps.row_members[tid] = 0u;
       }
@@ -410,6 +412,7 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
           const bool ok = __builtin_isfinite(gs) && __builtin_isfinite(b) && b < 0x1p100f;
           if (ok) {
             atomicMax(&ps.row_lower[r], order_bits(gs - b));
+            atomicMax(&ps.row_upper[r], order_bits(gs + b));
             ps.pupper[k] = gs + b;
           } else {
             ps.row_all[r] = 1u;
@@ -459,7 +462,9 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
         TileRecord* rec = p.records + static_cast<uint64_t>(r) * p.max_recs + ps.rec[r];
         const uint32_t lo = ps.lo[r];
         rec->best_lower = from_order_bits(ps.row_lower[r]);
-        rec->flags = ordinary ? 0u : kTileRescoreAll;
+        rec->flags = ordinary ? 0u
+                              : (ps.row_all[r] == 0u ? kTileRescoreAll | kTileCrowded : kTileRescoreAll);
+        rec->upper_max = from_order_bits(ps.row_upper[r]);
         rec->min_token = ps.ptok[ps.plan.prefix[r] - k0];
         rec->min_pos = lo;
         rec->begin = lo;

@@ -405,6 +405,7 @@ __device__ inline void range_end(const TailNormArgs& a, uint32_t r, const RangeR
     rec->begin = 0u;
     rec->count = w.c;
     rec->n_members = 0u;
+    rec->upper_max = __builtin_huge_valf();
     a.row_tiles[r] = 1u | kRangesUnused;
   }
 }

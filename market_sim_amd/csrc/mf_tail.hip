@@ -209,6 +209,7 @@ __device__ void gather_tile(const GatherArgs& a, uint32_t r, uint32_t k, uint32_
   TileRecord* rec = a.records + static_cast<uint64_t>(r) * a.max_tiles + k;
   uint32_t fin = 1u;
   float lo = -__builtin_huge_valf();
+  float up = -__builtin_huge_valf();
   uint32_t mt = kInvalidToken;
   uint32_t mp = 0u;
   for (uint32_t c = lane; c < n; c += kWave) {
@@ -216,6 +217,7 @@ __device__ void gather_tile(const GatherArgs& a, uint32_t r, uint32_t k, uint32_
     const float b = sh.bd[c];
     fin &= (__builtin_isfinite(g) && __builtin_isfinite(b) && b < 0x1p100f) ? 1u : 0u;
     lo = __builtin_fmaxf(lo, g - b);
+    up = __builtin_fmaxf(up, g + b);
     if (sh.tk[c] < mt) {
       mt = sh.tk[c];
       mp = begin + c;
@@ -223,6 +225,7 @@ __device__ void gather_tile(const GatherArgs& a, uint32_t r, uint32_t k, uint32_
   }
   const bool all_finite = wave_sum_u32(fin ^ 1u) == 0u;
   const float L = wave_max(lo);
+  const float U = wave_max(up);
   wave_min_token(mt, mp);
   // members: candidates with g + b >= L, ranked in list order by ballot
   const bool ordinary = all_finite && !invalid;
@@ -245,7 +248,9 @@ __device__ void gather_tile(const GatherArgs& a, uint32_t r, uint32_t k, uint32_
     uint32_t flags = 0u;
     if (invalid) flags |= kTileInvalid;
     if (!invalid && (!all_finite || total > kTileMembers)) flags |= kTileRescoreAll;
+    if (!invalid && all_finite && total > kTileMembers) flags |= kTileCrowded;
     rec->best_lower = L;
+    rec->upper_max = U;
     rec->flags = flags;
     rec->min_token = mt;
     rec->min_pos = mp;
