@@ -44,6 +44,7 @@ class Workload:
     next_table: Optional[np.ndarray] = None   # int32 [S, V] dense
     steps: int = 1
     seed: int = 0
+    sizes: str = ""                # how the list sizes were drawn
 
     @property
     def rows(self) -> int:
@@ -183,7 +184,8 @@ def ragged_pack(name: str, seed: int, vocab: int, hidden: int, rows: int,
     row_state, offsets, tokens = _pack(lists)
     return Workload(name=name, vocab=vocab, hidden=hidden, embedding=emb,
                     norm_weight=w, epsilon=1e-5, x=x, row_state=row_state,
-                    state_offsets=offsets, state_tokens=tokens, seed=seed)
+                    state_offsets=offsets, state_tokens=tokens, seed=seed,
+                    sizes=f"{'log-' if size_kind == 'log' else ''}uniform [{size_lo}, {size_hi}]")
 
 
 def synthetic_dfa_tail(name: str, seed: int, vocab: int, hidden: int, rows: int,
