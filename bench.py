@@ -142,7 +142,8 @@ def kernel_loop(tail, stage, launches, copies):
     are: they read the normalized rows and write tile records)."""
     import torch
     from market_sim_amd import abi, ops
-    fns = {"restricted": ops.decode_tail_restricted, "unrestricted": ops.decode_tail_unrestricted}
+    fns = {"prepare": ops.decode_tail_prepare, "restricted": ops.decode_tail_restricted,
+           "unrestricted": ops.decode_tail_unrestricted}
     args = [tail.args(i % copies) for i in range(copies)]
     s = tail.stream
     h = s.cuda_stream
@@ -288,11 +289,22 @@ def main() -> int:
             torch.mul(src, 1.0, out=dst)
         torch.cuda.synchronize()
         del src, dst
-    # the dominant kernel: the table pass (sorted lists with unrestricted
-    # rows: one kernel for both kinds of rows) or the CSR gather
+    # the dominant kernel: the one-kernel tail (short lists, no unrestricted
+    # rows: the prepare stage is the whole step), the table pass (sorted
+    # lists with unrestricted rows: one kernel for both kinds of rows) or
+    # the CSR gather
     one_pass = tail.table_pass
-    main_ms = kernel_loop(tail, "restricted", args.steps, args.copies)
-    if one_pass:
+    fused = tail.fused
+    main_ms = kernel_loop(tail, "prepare" if fused else "restricted", args.steps, args.copies)
+    if fused:
+        # the same bytes as the gather: each distinct candidate row, the ids,
+        # the hidden rows, the offsets and the outputs
+        main_bytes = alg["gather"]
+        main_name = "short_tail_kernel (one kernel: norm, exact scores, selection, DFA advance)"
+        achieved = main_bytes / (main_ms * 1e-3) / 1e9
+        traffic = profiled_traffic("short_tail_kernel")
+        fb = {"kernel": "none (no unrestricted rows)", "rows": alg["B_u"]}
+    elif one_pass:
         main_bytes, main_name = alg["pass_bytes"], "pass_kernel (one table pass: candidates + unrestricted head)"
         achieved = main_bytes / (main_ms * 1e-3) / 1e9
         traffic = profiled_traffic("pass_kernel")
@@ -357,6 +369,14 @@ def main() -> int:
             "gather_us": round(g_gather * 1e3, 2), "head_us": round(g_head * 1e3, 2),
             "gather_frac": round(alg["gather"] / (g_gather * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "head_frac": round(alg["fallback_bytes"] / (g_head * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        del g
+    if fused and not args.no_gather_path:
+        # the same step on the separate kernels (MF_TAIL_NO_FUSED)
+        g = DeviceTail(w, copies=args.copies, fused=False)
+        g_ms, _, _ = time_loop(g, ["tail"], args.steps, args.warmup, args.copies)
+        gtok, _, _ = g.results()
+        result["separate_kernels"] = {"ms_per_step": round(g_ms, 5),
+                                      "token_parity": bool(np.array_equal(gtok, tok))}
         del g
     if not args.no_full:
         full = DeviceTail(w, copies=args.copies, full=True)

@@ -307,6 +307,9 @@ inline constexpr std::uint64_t tail_hold_finished = MF_TAIL_HOLD_FINISHED;
 // a call without them.  Results are unchanged.
 inline constexpr std::uint64_t tail_sorted_lists = MF_TAIL_SORTED_LISTS;
 inline constexpr std::uint64_t tail_table_pass = MF_TAIL_TABLE_PASS;
+// DecodeTailArgs::flags: packs of short lists without unrestricted rows
+// still run the separate kernels instead of the one-kernel tail.
+inline constexpr std::uint64_t tail_no_fused = MF_TAIL_NO_FUSED;
 
 // Buffers and shape of one decode-tail call (see marketforge_hip.h); null
 // pointers are the optional buffers left out.
@@ -336,7 +339,7 @@ struct DecodeTailArgs {
   // next state goes to the same index of out_next_state, which may be
   // row_state itself.  Null: row_state and out_next_state hold one entry per row.
   const DeviceBuffer* row_sequence = nullptr;       // u32 [rows] or null
-  std::uint64_t flags = 0;                          // tail_hold_finished | tail_sorted_lists | tail_table_pass
+  std::uint64_t flags = 0;                          // tail_hold_finished | tail_sorted_lists | tail_table_pass | tail_no_fused
 };
 
 namespace detail {
@@ -574,6 +577,8 @@ class RestrictedDecoder {
     std::uint64_t max_steps = 0;
     float epsilon = 1e-5f;
     DotOrder order = DotOrder::fma_chain;
+    // false: the separate kernels even where the one-kernel tail applies
+    bool fused = true;
   };
 
   // embedding, norm_weight (null: hidden rows arrive normalized) and dfa
@@ -618,7 +623,7 @@ class RestrictedDecoder {
       a.states = dfa.tables().states();
       a.nnz = dfa.tables().arcs();
       a.max_count = dfa.tables().max_count;
-      a.flags = MF_TAIL_HOLD_FINISHED;
+      a.flags = MF_TAIL_HOLD_FINISHED | (config.fused ? 0u : MF_TAIL_NO_FUSED);
     }
     std::uint64_t ws = 0;
     Status s = detail::from_c(mf_decode_tail_workspace_bytes(&d.args_[0], &ws));

@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define MF_ABI_VERSION 3u
+#define MF_ABI_VERSION 4u
 
 /* Status: include/marketforge/core/status.hpp:7-49.  The numeric codes equal
  * the reference ErrorCode enumerators so results stay schema-compatible. */
@@ -211,6 +211,14 @@ mf_status mf_linear_f16(mf_buffer input, mf_buffer weight, mf_buffer output,
  * without the flags; a list that turns out not to be ascending is rescored
  * in full, exactly.  MF_TAIL_TABLE_PASS alone changes nothing.
  *
+ * Short lists: a call with no unrestricted rows, max_count <= 128,
+ * hidden % 8 == 0 and max_count within two rounds of one workgroup's LDS
+ * stage of candidate rows (one round at hidden <= 576) runs as
+ * ONE kernel in the prepare stage (norm,
+ * exact reference-order scores of every candidate, selection and DFA
+ * advance; the other three stages do nothing), unless the table pass is
+ * chosen above or flags hold MF_TAIL_NO_FUSED.  The results are the same.
+ *
  * Workspace: caller-allocated device memory of mf_decode_tail_workspace_bytes
  * bytes, zero-filled once by mf_workspace_init before first use.  Every call
  * leaves it ready for the next one; calls that overlap in time on the same
@@ -239,12 +247,14 @@ typedef struct mf_decode_tail_args {
   uint64_t max_count;          /* longest state list (table builder's figure) */
   uint64_t unrestricted_count;
   mf_buffer row_sequence;      /* u32 [rows] or address 0: see "Sequence table" */
-  uint64_t flags;              /* MF_TAIL_HOLD_FINISHED | MF_TAIL_SORTED_LISTS | MF_TAIL_TABLE_PASS */
+  uint64_t flags;              /* MF_TAIL_HOLD_FINISHED | MF_TAIL_SORTED_LISTS | MF_TAIL_TABLE_PASS
+                                  | MF_TAIL_NO_FUSED */
 } mf_decode_tail_args;
 
 #define MF_TAIL_HOLD_FINISHED 1u
 #define MF_TAIL_SORTED_LISTS 2u
 #define MF_TAIL_TABLE_PASS 4u
+#define MF_TAIL_NO_FUSED 8u
 
 mf_status mf_decode_tail_workspace_bytes(const mf_decode_tail_args* args,
                                          uint64_t* bytes);
@@ -253,9 +263,11 @@ mf_status mf_decode_tail_workspace_bytes(const mf_decode_tail_args* args,
  * counterpart; for benchmarks and tests that report per-kernel figures):
  * MF_TAIL_PATH_GATHER (restricted stage = CSR gather, unrestricted stage =
  * MFMA head) or MF_TAIL_PATH_TABLE_PASS (restricted stage = one pass over
- * the table for both kinds of rows, unrestricted stage empty). */
+ * the table for both kinds of rows, unrestricted stage empty) or
+ * MF_TAIL_PATH_FUSED (the whole tail in the prepare stage's one kernel). */
 #define MF_TAIL_PATH_GATHER 0u
 #define MF_TAIL_PATH_TABLE_PASS 1u
+#define MF_TAIL_PATH_FUSED 2u
 mf_status mf_decode_tail_path(const mf_decode_tail_args* args, uint32_t* path);
 /* Zero-fills a workspace with a fill kernel (safe under graph capture). */
 mf_status mf_workspace_init(mf_buffer workspace, uintptr_t stream);

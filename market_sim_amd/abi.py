@@ -32,9 +32,11 @@ ORDER_MUL_ADD_CHAIN = 1
 TAIL_HOLD_FINISHED = 1
 TAIL_SORTED_LISTS = 2
 TAIL_TABLE_PASS = 4
+TAIL_NO_FUSED = 8
 TAIL_PATH_GATHER = 0
 TAIL_PATH_TABLE_PASS = 1
-ABI_VERSION = 3
+TAIL_PATH_FUSED = 2
+ABI_VERSION = 4
 
 _U64 = ctypes.c_uint64
 _UP = ctypes.c_size_t  # uintptr_t

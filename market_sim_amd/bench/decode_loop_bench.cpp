@@ -27,7 +27,7 @@
 // reference_ops rounds the hidden rows to FP16 first, so its tokens may
 // differ (reported, not required).
 //
-// Usage: decode_loop_bench --dfa FILE [--rows B] [--repeats R] [--hidden H]
+// Usage: decode_loop_bench --dfa FILE [--rows B] [--repeats R] [--hidden H] [--no-fused]
 // FILE is the binary table written by market_sim_amd.dfa.write_tables.
 #include <hip/hip_runtime_api.h>
 
@@ -176,14 +176,17 @@ struct Timer {
 int main(int argc, char** argv) {
   const char* dfa_path = nullptr;
   std::uint64_t rows = 256, repeats = 50, hidden = 576;
+  bool fused = true;
   for (int i = 1; i < argc; ++i) {
     const std::string a = argv[i];
     if (a == "--dfa" && i + 1 < argc) dfa_path = argv[++i];
     else if (a == "--rows" && i + 1 < argc) rows = std::strtoull(argv[++i], nullptr, 10);
     else if (a == "--repeats" && i + 1 < argc) repeats = std::strtoull(argv[++i], nullptr, 10);
     else if (a == "--hidden" && i + 1 < argc) hidden = std::strtoull(argv[++i], nullptr, 10);
+    else if (a == "--no-fused") fused = false;
     else {
-      std::fprintf(stderr, "usage: %s --dfa FILE [--rows B] [--repeats R] [--hidden H]\n", argv[0]);
+      std::fprintf(stderr, "usage: %s --dfa FILE [--rows B] [--repeats R] [--hidden H] [--no-fused]\n",
+                   argv[0]);
       return 2;
     }
   }
@@ -223,6 +226,7 @@ int main(int argc, char** argv) {
   cfg.hidden = hidden;
   cfg.vocab = kVocab;
   cfg.max_steps = steps;
+  cfg.fused = fused;
   auto dec_r = mg::RestrictedDecoder::create(d_table.value(), &d_w.value(), dfa.value(), cfg, h);
   if (!dec_r) return 1;
   mg::RestrictedDecoder& dec = dec_r.value();
@@ -418,14 +422,15 @@ int main(int argc, char** argv) {
   };
   std::printf(
       "{\"tool\":\"decode_loop_bench\",\"states\":%llu,\"arcs\":%llu,\"rows\":%llu,"
-      "\"hidden\":%llu,\"vocab\":%llu,\"steps\":%llu,\"repeats\":%llu,\"finished_rows\":%llu,"
+      "\"hidden\":%llu,\"vocab\":%llu,\"steps\":%llu,\"repeats\":%llu,\"fused\":%s,\"finished_rows\":%llu,"
       "\"emitted_tokens\":%llu,\"resident\":%s,\"resident_repeatable\":%s,\"graph\":%s,"
       "\"graph_ok\":%s,\"graph_token_parity\":%s,\"round_trip\":%s,\"round_trip_token_parity\":%s,"
       "\"reference_ops\":%s,\"reference_ops_token_differences\":%llu}\n",
       static_cast<unsigned long long>(tables.states()), static_cast<unsigned long long>(tables.arcs()),
       static_cast<unsigned long long>(rows), static_cast<unsigned long long>(hidden),
       static_cast<unsigned long long>(kVocab), static_cast<unsigned long long>(steps),
-      static_cast<unsigned long long>(repeats), static_cast<unsigned long long>(finished),
+      static_cast<unsigned long long>(repeats), fused ? "true" : "false",
+      static_cast<unsigned long long>(finished),
       static_cast<unsigned long long>(emitted), rates(resident_ms).c_str(),
       resident_stable ? "true" : "false", rates(graph_ms > 0 ? graph_ms : 1e9).c_str(),
       graph_ok ? "true" : "false", graph_match ? "true" : "false", rates(rt_ms).c_str(),

@@ -487,7 +487,8 @@ struct TailLayout {
       fb_panel, fb_slot_row, fb_slot_norm, fb_slot_slack, scores, tok_norm, range_index,
       row_tiles, total;
   uint32_t tile, max_tiles, fb_tiles, fb_rows;
-  bool pass;  // the table pass serves both kinds of rows
+  bool pass;   // the table pass serves both kinds of rows
+  bool fused;  // the one-kernel tail (short lists)
 };
 
 bool buffer_is(const mf_buffer& b, uint64_t bytes) { return b.address != 0 && b.bytes == bytes; }
@@ -510,6 +511,18 @@ bool table_pass(const mf_decode_tail_args* a) {
   return (a->flags & MF_TAIL_SORTED_LISTS) &&
          (a->unrestricted_count > 0 || (a->flags & MF_TAIL_TABLE_PASS)) && a->hidden % 64u == 0 &&
          mf::panel_tile_bytes(a->hidden) <= mf::kPanelLdsMaxBytes && a->rows <= mf::kPassRowsMax;
+}
+
+// The one-kernel tail: short lists (two rounds of the workgroup's stage of
+// candidate rows at most), no unrestricted rows, not switched off.
+bool fused_tail(const mf_decode_tail_args* a) {
+  if ((a->flags & MF_TAIL_NO_FUSED) || a->unrestricted_count > 0 ||
+      a->max_count > mf::kShortListMax || a->hidden % 8u != 0 || a->hidden > 65535u) {
+    return false;
+  }
+  const uint32_t stage = mf::short_stage_rows(static_cast<uint32_t>(a->hidden),
+                                              static_cast<uint32_t>(a->max_count));
+  return stage > 0 && 2u * static_cast<uint64_t>(stage) >= a->max_count;
 }
 
 // Validation common to both decode-tail entry points; fills the layout.
@@ -541,7 +554,7 @@ mf_status validate_tail(const mf_decode_tail_args* a, bool full, TailLayout& L) 
   // capacity that row_sequence indexes
   const bool table = a->row_sequence.address != 0;
   if ((a->flags & ~static_cast<uint64_t>(MF_TAIL_HOLD_FINISHED | MF_TAIL_SORTED_LISTS |
-                                         MF_TAIL_TABLE_PASS)) != 0) {
+                                         MF_TAIL_TABLE_PASS | MF_TAIL_NO_FUSED)) != 0) {
     return status(MF_INVALID_ARGUMENT);
   }
   if (table && (a->row_state.bytes / 4u > kU32Max || a->row_state.bytes == 0 ||
@@ -598,6 +611,7 @@ mf_status validate_tail(const mf_decode_tail_args* a, bool full, TailLayout& L) 
   L.fb_tiles = mf::fallback_tiles(static_cast<uint32_t>(a->vocab));
   // table pass: one record per (row, 192-token range) holding its ids
   L.pass = !full && table_pass(a);
+  L.fused = !full && !L.pass && fused_tail(a);
   if (L.pass) {
     const uint64_t longest = a->max_count == 0 ? 1 : a->max_count;
     L.max_tiles = static_cast<uint32_t>(longest < L.fb_tiles ? longest : L.fb_tiles);
@@ -804,10 +818,15 @@ mf_status decode_tail_stage(const mf_decode_tail_args* args, uintptr_t stream, S
   hipError_t e = hipSuccess;
   switch (stage) {
     case Stage::kPrepare:
+      if (L.fused) {
+        e = mf::launch_short(norm_args(a, L, ws, false, true), finalize_args(a, L, ws, false), s);
+        break;
+      }
       e = mf::launch_tail_norm(
           norm_args(a, L, ws, mfma_gather(a->hidden), L.pass || !defer_chain(a)), s);
       break;
     case Stage::kRestricted: {
+      if (L.fused) break;
       if (L.pass) {
         e = mf::launch_pass(pass_args(a, L, ws), s);
         break;
@@ -834,11 +853,12 @@ mf_status decode_tail_stage(const mf_decode_tail_args* args, uintptr_t stream, S
       break;
     }
     case Stage::kUnrestricted: {
-      if (a->unrestricted_count == 0 || L.pass) break;
+      if (a->unrestricted_count == 0 || L.pass || L.fused) break;
       e = mf::launch_fallback(fallback_args(a, L, ws), s);
       break;
     }
     case Stage::kFinalize:
+      if (L.fused) break;
       e = mf::launch_finalize(finalize_args(a, L, ws, false), s);
       break;
   }
@@ -861,7 +881,7 @@ mf_status mf_decode_tail_path(const mf_decode_tail_args* args, uint32_t* path) {
   TailLayout L{};
   const mf_status v = validate_tail(args, false, L);
   if (v.code != MF_OK) return v;
-  *path = L.pass ? MF_TAIL_PATH_TABLE_PASS : MF_TAIL_PATH_GATHER;
+  *path = L.pass ? MF_TAIL_PATH_TABLE_PASS : L.fused ? MF_TAIL_PATH_FUSED : MF_TAIL_PATH_GATHER;
   return ok();
 }
 

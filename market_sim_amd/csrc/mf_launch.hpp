@@ -156,6 +156,10 @@ __host__ __device__ constexpr uint32_t panel_tiles(uint32_t m) {
 constexpr uint32_t kHeadTileTokens = 192;
 // Rows the table pass plans in LDS (one per thread of its workgroup).
 constexpr uint32_t kPassRowsMax = 256;
+// The one-kernel tail for short lists: longest list, and the LDS its
+// workgroup may take for x, the weight and the staged candidate rows.
+constexpr uint32_t kShortListMax = 128;
+constexpr uint32_t kShortLdsBytes = 156u * 1024u;
 constexpr uint32_t kPanelLdsMaxBytes = 76u * 1024u;
 
 struct GatherArgs {
@@ -306,5 +310,9 @@ struct PassArgs {
 };
 
 hipError_t launch_pass(const PassArgs& args, hipStream_t stream);
+// mf_short.hip: candidate rows one workgroup stages per round (0: H does
+// not fit), and the one-kernel tail
+uint32_t short_stage_rows(uint32_t H, uint32_t max_count);
+hipError_t launch_short(const TailNormArgs& norm, const FinalizeArgs& fin, hipStream_t stream);
 
 } // namespace mf

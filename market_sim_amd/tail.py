@@ -31,17 +31,20 @@ class DeviceTail:
     def __init__(self, w: Workload, device: str = "cuda", order: int = abi.ORDER_FMA_CHAIN,
                  copies: int = 1, full: bool = False, advance: Optional[str] = None,
                  unrestricted: Optional[np.ndarray] = None,
-                 sorted_lists: Optional[bool] = None, table_pass: bool = False):
+                 sorted_lists: Optional[bool] = None, table_pass: bool = False,
+                 fused: bool = True):
         import torch
         self.w = w
         # MF_TAIL_SORTED_LISTS (the one-pass table kernel where it pays):
         # declared when the lists are strictly ascending (None: checked
         # here) or by the caller; table_pass asks for that kernel even
-        # without unrestricted rows
+        # without unrestricted rows.  fused=False keeps packs of short lists
+        # off the one-kernel tail (MF_TAIL_NO_FUSED).
         if sorted_lists is None:
             sorted_lists = workloads.lists_ascending(w.state_offsets, w.state_tokens)
         self.flags = (abi.TAIL_SORTED_LISTS if sorted_lists else 0) | \
-            (abi.TAIL_TABLE_PASS if table_pass else 0)
+            (abi.TAIL_TABLE_PASS if table_pass else 0) | \
+            (0 if fused else abi.TAIL_NO_FUSED)
         # the rows handed to the MFMA head (default: the rows whose state is
         # MF_STATE_UNRESTRICTED)
         self._unrestricted = unrestricted
@@ -117,6 +120,11 @@ class DeviceTail:
     def table_pass(self) -> bool:
         """The library runs the one-pass table kernel for this tail."""
         return not self.full and ops.decode_tail_path(self.args(0)) == abi.TAIL_PATH_TABLE_PASS
+
+    @property
+    def fused(self) -> bool:
+        """The library runs the one-kernel tail (short lists) for this tail."""
+        return not self.full and ops.decode_tail_path(self.args(0)) == abi.TAIL_PATH_FUSED
 
     def launch(self, table: int = 0, args: Optional[abi.DecodeTailArgs] = None) -> None:
         a = args if args is not None else self.args(table)

@@ -216,7 +216,8 @@ def synthetic_dfa_tail(name: str, seed: int, vocab: int, hidden: int, rows: int,
                     state_offsets=offsets,
                     state_tokens=np.concatenate(chunks).astype(np.uint32),
                     state_next=np.concatenate(nexts).astype(np.uint32),
-                    next_table=table, steps=steps, seed=seed)
+                    next_table=table, steps=steps, seed=seed,
+                    sizes=f"uniform [{lo}, {hi}] per DFA state")
 
 
 def single_sequence_f32(seed: int = 0, vocab: int = 49152, hidden: int = 576,

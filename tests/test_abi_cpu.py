@@ -26,7 +26,7 @@ def test_library_exports_every_declared_symbol():
     lib = abi.lib()
     for name in declared_functions():
         assert hasattr(lib, name), name
-    assert lib.mf_abi_version() == 3
+    assert lib.mf_abi_version() == 4
 
 
 def b(addr, n):
@@ -175,7 +175,8 @@ def test_decode_tail_sequence_table_and_flags_validation():
     assert ws_code(flags=abi.TAIL_SORTED_LISTS) == abi.MF_OK
     assert ws_code(flags=abi.TAIL_HOLD_FINISHED | abi.TAIL_SORTED_LISTS) == abi.MF_OK
     assert ws_code(flags=abi.TAIL_SORTED_LISTS | abi.TAIL_TABLE_PASS) == abi.MF_OK
-    assert ws_code(flags=8) == abi.MF_INVALID_ARGUMENT
+    assert ws_code(flags=abi.TAIL_NO_FUSED) == abi.MF_OK
+    assert ws_code(flags=16) == abi.MF_INVALID_ARGUMENT
 
 
 def test_sorted_lists_flag_sizes_the_range_index():
@@ -200,10 +201,17 @@ def test_sorted_lists_flag_sizes_the_range_index():
         assert l.mf_decode_tail_path(ctypes.byref(a), ctypes.byref(path)).code == abi.MF_OK
         return path.value
 
+    nf = abi.TAIL_NO_FUSED
     assert path_of(flags=sorted_pass) == abi.TAIL_PATH_TABLE_PASS
-    assert path_of(flags=abi.TAIL_SORTED_LISTS) == abi.TAIL_PATH_GATHER
-    assert path_of() == abi.TAIL_PATH_GATHER
-    assert path_of(flags=abi.TAIL_TABLE_PASS) == abi.TAIL_PATH_GATHER
+    assert path_of(flags=sorted_pass | nf) == abi.TAIL_PATH_TABLE_PASS
+    assert path_of(flags=abi.TAIL_SORTED_LISTS | nf) == abi.TAIL_PATH_GATHER
+    assert path_of(flags=nf) == abi.TAIL_PATH_GATHER
+    assert path_of(flags=abi.TAIL_TABLE_PASS | nf) == abi.TAIL_PATH_GATHER
+    # short lists and no unrestricted rows: the one-kernel tail
+    assert path_of() == abi.TAIL_PATH_FUSED
+    assert path_of(flags=abi.TAIL_SORTED_LISTS) == abi.TAIL_PATH_FUSED
+    assert path_of(max_count=128) == abi.TAIL_PATH_FUSED
+    assert path_of(max_count=129) == abi.TAIL_PATH_GATHER
     unr = dict(unrestricted_count=1, unrestricted_rows=b(0xC00000, 4))
     assert path_of(flags=abi.TAIL_SORTED_LISTS, **unr) == abi.TAIL_PATH_TABLE_PASS
     assert path_of(**unr) == abi.TAIL_PATH_GATHER

@@ -20,22 +20,26 @@ def _lib(hip):
     return hip
 
 
-# Every test runs twice: with MF_TAIL_SORTED_LISTS | MF_TAIL_TABLE_PASS (the
-# one-pass table kernel, also for calls without unrestricted rows; lists
-# that are not ascending are then caught on the device and rescored in
-# full) and without them (the gather and the MFMA head).
-_LISTS = {"sorted": True}
+# Every test runs three times: with MF_TAIL_SORTED_LISTS | MF_TAIL_TABLE_PASS
+# (the one-pass table kernel, also for calls without unrestricted rows;
+# lists that are not ascending are then caught on the device and rescored
+# in full); with no flags (the one-kernel tail where the lists are short and
+# no row is unrestricted, else the gather and the MFMA head); and with
+# MF_TAIL_NO_FUSED (always the gather and the MFMA head).
+_MODE = {"mode": "table_pass"}
 
 
-@pytest.fixture(params=[True, False], ids=["table_pass", "gather"], autouse=True)
-def _lists_flag(request):
-    _LISTS["sorted"] = request.param
+@pytest.fixture(params=["table_pass", "auto", "separate"], autouse=True)
+def _tail_mode(request):
+    _MODE["mode"] = request.param
     yield
 
 
 def _tail(w, **kw):
     from market_sim_amd.tail import DeviceTail
-    return DeviceTail(w, sorted_lists=_LISTS["sorted"], table_pass=_LISTS["sorted"], **kw)
+    mode = _MODE["mode"]
+    return DeviceTail(w, sorted_lists=mode == "table_pass", table_pass=mode == "table_pass",
+                      fused=mode != "separate", **kw)
 
 
 def _oracle(w, x=None, order=abi.ORDER_FMA_CHAIN, advance="auto", threads=8):
