@@ -10,6 +10,7 @@
 
 #include "mf_device.hpp"
 #include "mf_launch.hpp"
+#include "mf_norm.hpp"
 
 namespace mf {
 namespace {
@@ -24,36 +25,85 @@ constexpr int kWaves = kThreads / kWave;
 // (x * inverse) * weight.  Optionally writes an upper bound of ||y||_2 per
 // row for the MFMA bounds.
 // ---------------------------------------------------------------------------
+// Rows up to this width also stage the weight in LDS (3 H floats in all).
+constexpr uint32_t kNormStagedWeightMax = 8192;
+
 template <bool kHalfIn, bool kHalfW, bool kHalfOut>
 __global__ __launch_bounds__(kWave) void rms_norm_kernel(
     const void* __restrict__ input, const void* __restrict__ weight,
     void* output, float* __restrict__ row_norm, uint32_t H, float epsilon) {
+  // [H] x, [H] x * x, and [H] weight when H <= kNormStagedWeightMax
   extern __shared__ __align__(16) float xs[];
   __shared__ float inverse_shared;
+  const bool stage_w = H <= kNormStagedWeightMax;
+  float* sq = xs + H;
+  float* ws = xs + 2u * H;
   const uint64_t r = blockIdx.x;
   const uint32_t lane = threadIdx.x;
-  for (uint32_t c = lane; c < H; c += kWave) {
-    xs[c] = kHalfIn ? half_to_float(static_cast<const uint16_t*>(input)[r * H + c])
-                    : static_cast<const float*>(input)[r * H + c];
+  // x and the weight staged with four 4-element loads of each per lane in
+  // flight before the LDS stores (one memory round trip per 1024 features)
+  constexpr uint32_t kInBytes = kHalfIn ? 2u : 4u;
+  constexpr uint32_t kWBytes = kHalfW ? 2u : 4u;
+  const bool vec = (H & 3u) == 0 &&
+                   (reinterpret_cast<uintptr_t>(input) & (4u * kInBytes - 1u)) == 0 &&
+                   (reinterpret_cast<uintptr_t>(weight) & (4u * kWBytes - 1u)) == 0;
+  auto load4 = [](const void* base, uint64_t q, auto half) -> float4 {
+    if constexpr (decltype(half)::value) {
+      const uint2 h = static_cast<const uint2*>(base)[q];
+      return float4{half_to_float(static_cast<uint16_t>(h.x)), half_to_float(static_cast<uint16_t>(h.x >> 16)),
+                    half_to_float(static_cast<uint16_t>(h.y)), half_to_float(static_cast<uint16_t>(h.y >> 16))};
+    } else {
+      return static_cast<const float4*>(base)[q];
+    }
+  };
+  using HalfIn = std::integral_constant<bool, kHalfIn>;
+  using HalfW = std::integral_constant<bool, kHalfW>;
+  if (vec) {
+    constexpr uint32_t kBatch = 4;
+    const uint32_t n4 = H / 4u;
+    for (uint32_t base = lane; base < n4; base += kWave * kBatch) {
+      float4 v[kBatch];
+      float4 w4[kBatch];
+#pragma unroll
+      for (uint32_t u = 0; u < kBatch; ++u) {
+        const uint32_t q = base + u * kWave;
+        v[u] = q < n4 ? load4(input, r * n4 + q, HalfIn{}) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+        w4[u] = (stage_w && q < n4) ? load4(weight, q, HalfW{}) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+#pragma unroll
+      for (uint32_t u = 0; u < kBatch; ++u) {
+        const uint32_t q = base + u * kWave;
+        if (q < n4) {
+          reinterpret_cast<float4*>(xs)[q] = v[u];
+          reinterpret_cast<float4*>(sq)[q] =
+              float4{v[u].x * v[u].x, v[u].y * v[u].y, v[u].z * v[u].z, v[u].w * v[u].w};
+          if (stage_w) reinterpret_cast<float4*>(ws)[q] = w4[u];
+        }
+      }
+    }
+  } else {
+    for (uint32_t c = lane; c < H; c += kWave) {
+      const float v = kHalfIn ? half_to_float(static_cast<const uint16_t*>(input)[r * H + c])
+                              : static_cast<const float*>(input)[r * H + c];
+      xs[c] = v;
+      sq[c] = v * v;
+      if (stage_w) {
+        ws[c] = kHalfW ? half_to_float(static_cast<const uint16_t*>(weight)[c])
+                       : static_cast<const float*>(weight)[c];
+      }
+    }
   }
   __syncthreads();
-  if (lane == 0) {
-    float sum_squares = 0.0f;
-#pragma unroll 8
-    for (uint32_t c = 0; c < H; ++c) {
-      const float v = xs[c];
-      const float sq = v * v;
-      sum_squares = sum_squares + sq;
-    }
-    const float mean = div_rn(sum_squares, static_cast<float>(H));
-    inverse_shared = div_rn(1.0f, sqrt_rn(mean + epsilon));
-  }
+  // sum of the squares in feature order, then mean, + epsilon, sqrt and
+  // reciprocal, each rounded once (rms_norm.cu:104-182)
+  if (lane == 0) inverse_shared = norm_inverse(sequential_sum(sq, H), H, epsilon);
   __syncthreads();
   const float inverse = inverse_shared;
   float norm_sq = 0.0f;
   for (uint32_t c = lane; c < H; c += kWave) {
-    const float w = kHalfW ? half_to_float(static_cast<const uint16_t*>(weight)[c])
-                           : static_cast<const float*>(weight)[c];
+    const float w = stage_w ? ws[c]
+                    : kHalfW ? half_to_float(static_cast<const uint16_t*>(weight)[c])
+                             : static_cast<const float*>(weight)[c];
     const float scaled = xs[c] * inverse;
     const float y = scaled * w;
     if constexpr (kHalfOut) {
@@ -585,7 +635,8 @@ hipError_t launch_rms_norm(const void* input, bool half_input, const void* weigh
                            bool half_weight, void* output, bool half_output,
                            float* row_norm, uint32_t rows, uint32_t hidden,
                            float epsilon, hipStream_t stream) {
-  const size_t lds = static_cast<size_t>(hidden) * sizeof(float);
+  const size_t lds = (hidden <= kNormStagedWeightMax ? 3u : 2u) * static_cast<size_t>(hidden) *
+                     sizeof(float);
   const dim3 grid(rows), block(kWave);
   if (half_input && half_weight && half_output) {
     hipLaunchKernelGGL((rms_norm_kernel<true, true, true>), grid, block, lds, stream,
