@@ -112,8 +112,12 @@ class RestrictedDecoder:
 
     def __init__(self, embedding, dfa: DeviceDfa, rows: int, max_steps: int,
                  norm_weight: Optional[np.ndarray] = None, epsilon: float = 1e-5,
-                 order: int = abi.ORDER_FMA_CHAIN, device: str = "cuda", stream=None):
+                 order: int = abi.ORDER_FMA_CHAIN, device: str = "cuda", stream=None,
+                 fused: bool = True):
         import torch
+        # fused=False: the separate kernels even where the one-kernel tail
+        # applies (MF_TAIL_NO_FUSED)
+        self.flags = abi.TAIL_HOLD_FINISHED | (0 if fused else abi.TAIL_NO_FUSED)
         self.dfa = dfa
         self.device = device
         self.rows = rows
@@ -150,7 +154,7 @@ class RestrictedDecoder:
         return ops.decode_tail_args(
             b, rows=self.rows, hidden=self.hidden, vocab=self.vocab, states=self.dfa.states,
             nnz=self.dfa.nnz, max_count=self.dfa.max_count, epsilon=self.epsilon,
-            order=self.order, flags=abi.TAIL_HOLD_FINISHED)
+            order=self.order, flags=self.flags)
 
     def start(self, states: Optional[Sequence[int]] = None) -> None:
         """Every row at the DFA root, or at the given states (one upload)."""

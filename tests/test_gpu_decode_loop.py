@@ -232,3 +232,27 @@ def test_decode_loop_bench_tool(tmp_path, market):
     assert doc["finished_rows"] == 48 and doc["steps"] == market.depth
     assert doc["graph_ok"] and doc["graph_token_parity"]
     assert doc["round_trip_token_parity"] and doc["resident_repeatable"]
+
+
+def test_decoder_one_kernel_tail_equals_separate_kernels(market):
+    """The market grammar's lists take the one-kernel tail; the same steps
+    on the separate kernels (MF_TAIL_NO_FUSED) give the same tokens, scores
+    and states."""
+    import torch
+    from market_sim_amd.decode import DeviceDfa, RestrictedDecoder
+    B, H, steps = 40, 576, 5
+    emb = _table(14, H)
+    rng = np.random.default_rng(15)
+    w = (1.0 + 0.02 * rng.standard_normal(H)).astype(np.float32)
+    xs = [torch.from_numpy(_hidden(rng, B, H)).cuda() for _ in range(steps)]
+    out = []
+    for fused in (True, False):
+        dec = RestrictedDecoder(emb, DeviceDfa(market), B, steps, norm_weight=w, fused=fused)
+        dec.start()
+        for x in xs:
+            dec.step(x)
+        res = dec.result()
+        out.append((res.tokens, res.scores, dec.current_states().cpu().numpy().view(np.uint32)))
+    assert np.array_equal(out[0][0], out[1][0])
+    assert np.array_equal(out[0][1].view(np.uint32), out[1][1].view(np.uint32))
+    assert np.array_equal(out[0][2], out[1][2])
