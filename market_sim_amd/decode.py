@@ -28,18 +28,34 @@ the C ABI.
 """
 from __future__ import annotations
 
+import os
+import re
 from dataclasses import dataclass
-from typing import Dict, Iterable, List, Optional, Sequence
+from typing import Dict, Iterable, List, Optional, Sequence, Tuple
 
 import numpy as np
 
-from . import abi, ops
+from . import abi, ops, schema
 from .dfa import NO_CHOICE, DfaTables
 
 
 def _device_u32(a: np.ndarray, device: str):
     import torch
     return torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint32).view(np.int32)).to(device)
+
+
+def stream_workspace(nbytes: int, stream, device: str):
+    """A decode-tail workspace of ``nbytes`` (256-byte aligned) for work on
+    ``stream``: allocated under that stream, so torch's allocator orders it
+    with the stream's work, and zero-filled there by mf_workspace_init (no
+    fill on another stream can overlap the tail).  Returns (tensor, buffer)."""
+    import torch
+    with torch.cuda.stream(stream):
+        t = torch.empty(nbytes // 4 + 64, dtype=torch.int32, device=device)
+        off = (-t.data_ptr()) % 256
+        ws = ops.DeviceBuffer(t.data_ptr() + off, nbytes)
+        abi.check("workspace_init", ops.workspace_init(ws, stream.cuda_stream))
+    return t, ws
 
 
 def _table_tensor(table, device: str):
@@ -135,12 +151,9 @@ class RestrictedDecoder:
         self._x = torch.empty((rows, self.hidden), dtype=torch.float32, device=device)
         self._args = [self._make_args(k) for k in range(2)]
         nbytes = ops.decode_tail_workspace_bytes(self._args[0])
-        self._ws_t = torch.zeros(nbytes // 4 + 64, dtype=torch.int32, device=device)
-        off = (-self._ws_t.data_ptr()) % 256
-        ws = ops.DeviceBuffer(self._ws_t.data_ptr() + off, nbytes)
+        self._ws_t, ws = stream_workspace(nbytes, self.stream, device)
         for a in self._args:
             a.workspace = ws.c()
-        abi.check("workspace_init", ops.workspace_init(ws, self.stream.cuda_stream))
         self.k = 0
 
     def _make_args(self, parity: int) -> abi.DecodeTailArgs:
@@ -199,6 +212,76 @@ class RestrictedDecoder:
         known = st < self.dfa.states
         choice[known] = self.dfa.tables.choice[st[known]]
         return DecodeResult(tok, sc, st, choice)
+
+
+# ---- the run contract of a decode run ---------------------------------------
+
+def source_identity() -> Tuple[str, str]:
+    """(commit, bundle_sha256) for the run contract's ``source`` block: the
+    git commit of this checkout (or, in a snapshot without git history, the
+    SHA-1 of the library's sources, a 40-hex content id of the same form),
+    and the SHA-256 of the library file that ran."""
+    import hashlib
+    import subprocess
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    commit = ""
+    try:
+        r = subprocess.run(["git", "-C", root, "rev-parse", "HEAD"], capture_output=True,
+                           text=True, timeout=10, check=False)
+        commit = r.stdout.strip() if r.returncode == 0 else ""
+    except (OSError, subprocess.SubprocessError):
+        commit = ""
+    if not re.fullmatch(r"[0-9a-f]{40}", commit):
+        h = hashlib.sha1()
+        csrc = os.path.join(root, "market_sim_amd", "csrc")
+        for name in sorted(os.listdir(csrc)):
+            path = os.path.join(csrc, name)
+            if os.path.isfile(path):
+                h.update(name.encode())
+                with open(path, "rb") as f:
+                    h.update(f.read())
+        commit = h.hexdigest()
+    with open(abi.LIB_PATH, "rb") as f:
+        bundle = hashlib.sha256(f.read()).hexdigest()
+    return commit, bundle
+
+
+def run_record(result: "DecodeResult", prompts: Sequence[Sequence[int]], table: np.ndarray, *,
+               seed: int, inference_seconds: float, model_load_seconds: float,
+               peak_gpu_memory_bytes: int, device_name: str, runtime_version: str,
+               backend_mode: str = "eager", graphs: bool = False,
+               model_id: str = "synthetic-tied-embedding",
+               model_repository: str = "local/synthetic") -> schema.RunRecord:
+    """The run contract (tools/inference/contract.py:85-160) of a decode run:
+    one request per row, its prompt ``prompts[r]`` and the tokens the device
+    generated up to the row's end (``DecodeResult.generated``); the finish
+    reason is "stop" when the row reached a terminal DFA state, else
+    "length".  The model block names the embedding table by content: its
+    SHA-256 as checkpoint digest and its SHA-1 as revision.  Generation is
+    greedy FP16-table decoding with structured (DFA-restricted) output;
+    MI355X (gfx950) reports compute capability 9.5."""
+    import hashlib
+    tbl = np.ascontiguousarray(table)
+    steps, rows = result.tokens.shape
+    if len(prompts) != rows:
+        raise ValueError(f"{rows} rows need {rows} prompts")
+    reqs = tuple(schema.RequestRecord(
+        f"seq-{r}", tuple(int(t) for t in prompts[r]), tuple(result.generated(r)),
+        "stop" if bool(result.finished[r]) else "length") for r in range(rows))
+    commit, bundle = source_identity()
+    return schema.RunRecord(
+        commit=commit, bundle_sha256=bundle, backend_name="market_sim_amd",
+        backend_version=f"abi-{abi.ABI_VERSION}", backend_mode=backend_mode,
+        model_id=model_id, model_repository=model_repository,
+        model_revision=hashlib.sha1(tbl.tobytes()).hexdigest(),
+        checkpoint_sha256=hashlib.sha256(tbl.tobytes()).hexdigest(),
+        vocabulary_size=int(tbl.shape[0]), device_name=device_name,
+        compute_capability="9.5", runtime_version=runtime_version, dtype="float16",
+        seed=int(seed), max_output_tokens=int(steps), requests=reqs,
+        model_load_seconds=float(model_load_seconds),
+        inference_seconds=float(inference_seconds),
+        peak_gpu_memory_bytes=int(peak_gpu_memory_bytes), graphs=graphs,
+        structured_output=True)
 
 
 # ---- continuous batching ----------------------------------------------------
@@ -294,14 +377,16 @@ class SequencePacker:
 
     # -- one pack -------------------------------------------------------------
     def _workspace(self, args: abi.DecodeTailArgs) -> ops.DeviceBuffer:
-        import torch
+        """The pack's workspace, grown when a pack needs more.  Called after
+        the stream has waited for the caller's stream; the replaced tensor
+        is marked as used by the stream, so its memory is not handed out
+        again before a pack still in flight (run(sync=False)) is done."""
         need = ops.decode_tail_workspace_bytes(args)
         if need > self._ws_bytes:
-            self._ws_t = torch.zeros(need // 4 + 64, dtype=torch.int32, device=self.device)
+            if self._ws_t is not None:
+                self._ws_t.record_stream(self.stream)
+            self._ws_t, self._ws = stream_workspace(need, self.stream, self.device)
             self._ws_bytes = need
-            off = (-self._ws_t.data_ptr()) % 256
-            self._ws = ops.DeviceBuffer(self._ws_t.data_ptr() + off, need)
-            abi.check("workspace_init", ops.workspace_init(self._ws, self.stream.cuda_stream))
         return self._ws
 
     def run(self, items: Sequence[BatchItem], hidden, sync: bool = True) -> Optional[PackStep]:

@@ -16,8 +16,13 @@
  *                                          every one of the 65536 halves.
  *   orc_rms_norm_f32     reference operators.cpp compiled into oracle/_ref,
  *                        bit-exact; hand values of cpu_operator_tests.cpp:59-108.
- *   orc_dot_fma          tiny head known answer (cuda_tests.cu:699-800):
- *                        tokens [14, 8, 1] and exact rational scores.
+ *   orc_dot_fma          the ascending single-rounding chain evaluated in
+ *                        exact rational arithmetic on rows spanning many
+ *                        binades, bit for bit (tests/test_oracle_fma_pin.py,
+ *                        which also shows that reversed, unfused, strided and
+ *                        pairwise chains differ on those rows); tiny head
+ *                        known answer (cuda_tests.cu:699-800): tokens
+ *                        [14, 8, 1] and exact rational scores.
  *   orc_dot_mul_add      reference linear_f32 in oracle/_ref, bit-exact;
  *                        linear known answer [-2, 3].
  *   orc_select_*         greedy/restricted tie, NaN and sentinel cases of

@@ -141,6 +141,64 @@ def test_restricted_decoder_generates_market_actions(market):
     assert np.all(res.tokens[-1] == abi.INVALID_TOKEN)
 
 
+def test_decode_run_emits_the_run_contract(market):
+    """A RestrictedDecoder run on the market grammar reports itself in the
+    reference's run contract (tools/inference/contract.py:85-168): the
+    document built from the device tokens passes check_run, survives the
+    strict JSON round trip, and its generated tokens are the oracle's.  The
+    hidden rows are synthetic (no model runs), so each request records one
+    prompt token, 0."""
+    import time
+    import torch
+    from market_sim_amd import schema
+    from market_sim_amd.decode import DeviceDfa, RestrictedDecoder, run_record
+    H, B = 576, 48
+    steps = market.depth + 1
+    emb = _table(8, H)
+    rng = np.random.default_rng(41)
+    w = (1.0 + 0.02 * rng.standard_normal(H)).astype(np.float32)
+    xs = [_hidden(rng, B, H) for _ in range(steps)]
+    torch.cuda.reset_peak_memory_stats()
+    t0 = time.perf_counter()
+    dec = RestrictedDecoder(emb, DeviceDfa(market), B, steps, norm_weight=w)
+    dev_x = [torch.from_numpy(x).cuda() for x in xs]
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    dec.start()
+    for x in dev_x:
+        dec.step(x)
+    res = dec.result()
+    t2 = time.perf_counter()
+    rec = run_record(res, [[0]] * B, emb, seed=41, inference_seconds=t2 - t1,
+                     model_load_seconds=t1 - t0,
+                     peak_gpu_memory_bytes=torch.cuda.max_memory_allocated(),
+                     device_name=torch.cuda.get_device_name(0),
+                     runtime_version=str(torch.version.hip))
+    doc = schema.load_run(rec.to_json())
+    assert doc["hardware"]["compute_capability"] == "9.5"
+    assert doc["features"]["structured_output"] is True
+    assert doc["model"]["vocabulary_size"] == VOCAB
+    # the oracle's tokens, request by request
+    table = np.zeros(B, np.uint32)
+    etoks = []
+    for x in xs:
+        etok, _, table = oracle.decode_tail_sequences(
+            x, w, 1e-5, emb, table, None, market.offsets, market.tokens,
+            state_next=market.next, hold=True, threads=8)
+        etoks.append(etok)
+    etoks = np.array(etoks)
+    language = cases.market_language()
+    for r, req in enumerate(doc["requests"]):
+        col = etoks[:, r]
+        end = np.nonzero(col == abi.INVALID_TOKEN)[0]
+        want = col[: end[0] if end.size else col.size].tolist()
+        assert req["generated_token_ids"] == want
+        assert req["finish_reason"] == "stop"
+        assert want == language[int(res.choice[r])]
+    assert doc["metrics"]["output_tokens"] == sum(len(r["generated_token_ids"])
+                                                  for r in doc["requests"])
+
+
 def test_restricted_decoder_starts_anywhere_and_reuses_buffers(market):
     import torch
     from market_sim_amd.decode import DeviceDfa, RestrictedDecoder
@@ -248,6 +306,10 @@ def test_decoder_one_kernel_tail_equals_separate_kernels(market):
     out = []
     for fused in (True, False):
         dec = RestrictedDecoder(emb, DeviceDfa(market), B, steps, norm_weight=w, fused=fused)
+        # each decoder takes the path it is built for (the comparison is
+        # between two different kernel sets, never one path with itself)
+        want = abi.TAIL_PATH_FUSED if fused else abi.TAIL_PATH_GATHER
+        assert ops.decode_tail_path(dec._args[0]) == want
         dec.start()
         for x in xs:
             dec.step(x)

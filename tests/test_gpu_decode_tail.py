@@ -121,6 +121,57 @@ def test_cfg5_scaled_h2048():
     _same(_run(w), _oracle(w, threads=16))
 
 
+_CFG5 = {}
+
+
+def test_cfg5_full_size_b1024():
+    """configs[4] at its stated size: a 128256 x 2048 FP16 table (525 MB),
+    B = 1024 rows with lists log-uniform in [1, 16384] (about 1.6 M
+    candidates) and 5% of rows unrestricted.  This reaches the largest row
+    plans and the crowded-window records (many near-equal scores per tile).
+    The workload and the oracle's answer are computed once for the three
+    kernel modes."""
+    if "exp" not in _CFG5:
+        w = wl.config(5, seed=0)
+        _CFG5["w"] = w
+        _CFG5["exp"] = _oracle(w, threads=16)
+    w = _CFG5["w"]
+    assert w.rows == 1024 and w.vocab == 128256 and w.hidden == 2048
+    assert w.unrestricted_rows.size == 51 and w.max_count > 8192
+    _same(_run(w), _CFG5["exp"])
+
+
+@pytest.mark.parametrize("order", [abi.ORDER_MUL_ADD_CHAIN, abi.ORDER_FMA_CHAIN])
+def test_cfg1_single_sequence(order):
+    """one sequence, 16 allowed ids, the final RMSNorm; plus the
+    full-vocabulary argmax for comparison (the same row unrestricted).
+
+    The reference's cfg1 table is FP32 and its only implementation is the CPU
+    (rms_norm_f32 -> linear_f32 -> argmax); every device operator of the
+    reference takes an FP16 table (greedy.hpp:35-49, linear.hpp:18-22), and so
+    does this library.  The device path therefore runs on the same seeded
+    table rounded to FP16 and is bit-exact against the oracle on that table.
+    The FP32-table oracle answer is checked beside it: the same tokens (the
+    top-2 margins, 0.065 and 0.18, dwarf the FP16 rounding of the table) and
+    scores within the north star's 1e-3 relative."""
+    w32 = wl.config(1, seed=0)
+    e16 = w32.embedding.astype(np.float16).view(np.uint16)
+    w = wl.Workload(**{**w32.__dict__, "embedding": e16})
+    got = _run(w, order=order)
+    _same(got, _oracle(w, order=order), check_next=False)
+    ref32 = _oracle(w32, order=order)
+    assert got[0][0] == ref32[0][0]
+    assert abs(float(got[1][0]) - float(ref32[1][0])) <= 1e-3 * abs(float(ref32[1][0]))
+    # full-vocabulary argmax: the row unrestricted (MFMA head)
+    unr = np.array([wl.STATE_UNRESTRICTED], np.uint32)
+    wf = wl.Workload(**{**w.__dict__, "row_state": unr})
+    gotf = _run(wf, order=order)
+    _same(gotf, _oracle(wf, order=order), check_next=False)
+    ref32f = _oracle(wl.Workload(**{**w32.__dict__, "row_state": unr}), order=order)
+    assert gotf[0][0] == ref32f[0][0]
+    assert abs(float(gotf[1][0]) - float(ref32f[1][0])) <= 1e-3 * abs(float(ref32f[1][0]))
+
+
 def test_full_projection_comparator_is_identical():
     w = wl.config(3, seed=4, scale_vocab=12000, scale_rows=80)
     exp = _oracle(w)
