@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define MF_ABI_VERSION 4u
+#define MF_ABI_VERSION 5u
 
 /* Status: include/marketforge/core/status.hpp:7-49.  The numeric codes equal
  * the reference ErrorCode enumerators so results stay schema-compatible. */
@@ -275,6 +275,21 @@ mf_status mf_workspace_init(mf_buffer workspace, uintptr_t stream);
 /* The restricted path: CSR gather for restricted rows + MFMA fallback.
  * Equivalent to the four stages below, in order, on one stream. */
 mf_status mf_decode_tail_f16(const mf_decode_tail_args* args, uintptr_t stream);
+
+/* mf_decode_tail_f16 without a caller workspace and without any allocation.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  The workspace is a device array inside
+ * the library, mf_decode_tail_noalloc_max_bytes() bytes (16 MiB) per GPU,
+ * held from library load until the process ends; args->workspace is not
+ * used.  Same kernels, same results as mf_decode_tail_f16.  A call whose
+ * workspace (mf_decode_tail_workspace_bytes) exceeds the array returns
+ * MF_RESOURCE_LIMIT before any launch.  The first call on a device looks up
+ * that device's array and zero-fills it on the call's stream.  Every call on
+ * one GPU shares that GPU's array: calls that overlap in time on one GPU
+ * (two streams, two threads) race and must be ordered by the caller. */
+uint64_t mf_decode_tail_noalloc_max_bytes(void);
+mf_status mf_decode_tail_f16_noalloc(const mf_decode_tail_args* args, uintptr_t stream);
 
 /* Stages of mf_decode_tail_f16 for callers that schedule them separately
  * (e.g. the unrestricted stage on a second stream once prepare is done).

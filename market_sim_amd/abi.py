@@ -36,7 +36,7 @@ TAIL_NO_FUSED = 8
 TAIL_PATH_GATHER = 0
 TAIL_PATH_TABLE_PASS = 1
 TAIL_PATH_FUSED = 2
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _U64 = ctypes.c_uint64
 _UP = ctypes.c_size_t  # uintptr_t
@@ -96,6 +96,8 @@ SIGNATURES = {
         Status, [ctypes.POINTER(DecodeTailArgs), ctypes.POINTER(ctypes.c_uint32)]),
     "mf_workspace_init": (Status, [Buffer, _UP]),
     "mf_decode_tail_f16": (Status, [ctypes.POINTER(DecodeTailArgs), _UP]),
+    "mf_decode_tail_noalloc_max_bytes": (_U64, []),
+    "mf_decode_tail_f16_noalloc": (Status, [ctypes.POINTER(DecodeTailArgs), _UP]),
     "mf_decode_tail_prepare": (Status, [ctypes.POINTER(DecodeTailArgs), _UP]),
     "mf_decode_tail_restricted": (Status, [ctypes.POINTER(DecodeTailArgs), _UP]),
     "mf_decode_tail_unrestricted": (Status, [ctypes.POINTER(DecodeTailArgs), _UP]),

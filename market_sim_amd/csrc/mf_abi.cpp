@@ -929,6 +929,72 @@ mf_status mf_decode_tail_f16(const mf_decode_tail_args* args, uintptr_t stream) 
   return ok();
 }
 
+}  // extern "C"
+
+// ------------------------------------------- decode tail without allocation --
+
+namespace {
+
+// The workspace of mf_decode_tail_f16_noalloc: one array per GPU, held from
+// module load to process end.  Host code never passes the array's name to a
+// kernel or a copy (on the host it is a stand-in, not a device address): it
+// takes the device address from hipGetSymbolAddress, once per device.
+constexpr uint64_t kScratchBytes = 16ull << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+struct ScratchSlot {
+  std::once_flag once;
+  hipError_t error = hipSuccess;
+  void* address = nullptr;
+};
+ScratchSlot g_scratch[64];
+
+// The current device's array: its address, looked up with that device
+// current on the first call there, when the array is also zero-filled on the
+// caller's stream (the state every workspace starts from).
+hipError_t scratch_address(hipStream_t stream, void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+  ScratchSlot& slot = g_scratch[dev];
+  std::call_once(slot.once, [&slot, stream]() {
+    void* p = nullptr;
+    hipError_t r = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (r == hipSuccess && p == nullptr) r = hipErrorInvalidSymbol;
+    if (r == hipSuccess) r = mf::launch_fill_zero(p, kScratchBytes, stream);
+    slot.error = r;
+    slot.address = r == hipSuccess ? p : nullptr;
+  });
+  *out = slot.address;
+  return slot.error;
+}
+
+}  // namespace
+
+extern "C" {
+
+uint64_t mf_decode_tail_noalloc_max_bytes(void) { return kScratchBytes; }
+
+mf_status mf_decode_tail_f16_noalloc(const mf_decode_tail_args* args, uintptr_t stream) {
+  if (args == nullptr || stream == 0) return status(MF_INVALID_ARGUMENT);
+  mf_decode_tail_args a = *args;
+  a.workspace = mf_buffer{0, 0};  // the caller's workspace field is not used
+  TailLayout L{};
+  mf_status v = validate_tail(&a, false, L);
+  if (v.code != MF_OK) return v;
+  if (L.total > kScratchBytes) return status(MF_RESOURCE_LIMIT);
+  void* base = nullptr;
+  const hipError_t e = scratch_address(native(stream), &base);
+  if (e != hipSuccess) return runtime_status(e);
+  a.workspace = mf_buffer{reinterpret_cast<uintptr_t>(base), kScratchBytes};
+  for (Stage st : {Stage::kPrepare, Stage::kUnrestricted, Stage::kRestricted, Stage::kFinalize}) {
+    v = decode_tail_stage(&a, stream, st);
+    if (v.code != MF_OK) return v;
+  }
+  return ok();
+}
+
 mf_status mf_decode_tail_full_f16(const mf_decode_tail_args* args, uintptr_t stream) {
   if (stream == 0) return status(MF_INVALID_ARGUMENT);
   TailLayout L{};

@@ -217,6 +217,16 @@ def decode_tail_f16(args: abi.DecodeTailArgs, stream: int) -> Status:
     return abi.lib().mf_decode_tail_f16(ctypes.byref(args), stream)
 
 
+def decode_tail_f16_noalloc(args: abi.DecodeTailArgs, stream: int) -> Status:
+    """mf_decode_tail_f16 on the library's own per-GPU workspace (no
+    allocation; args.workspace is not used)."""
+    return abi.lib().mf_decode_tail_f16_noalloc(ctypes.byref(args), stream)
+
+
+def decode_tail_noalloc_max_bytes() -> int:
+    return int(abi.lib().mf_decode_tail_noalloc_max_bytes())
+
+
 def decode_tail_prepare(args: abi.DecodeTailArgs, stream: int) -> Status:
     return abi.lib().mf_decode_tail_prepare(ctypes.byref(args), stream)
 

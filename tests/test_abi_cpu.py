@@ -15,7 +15,7 @@ FAKE_STREAM = 0x1000
 
 def declared_functions():
     text = open(os.path.join(ROOT, "include", "marketforge_hip.h")).read()
-    return sorted(set(re.findall(r"^\s*(?:mf_status|uint32_t)\s+(mf_\w+)\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:mf_status|uint32_t|uint64_t)\s+(mf_\w+)\(", text, re.M)))
 
 
 def test_header_declarations_match_binding():
@@ -26,7 +26,7 @@ def test_library_exports_every_declared_symbol():
     lib = abi.lib()
     for name in declared_functions():
         assert hasattr(lib, name), name
-    assert lib.mf_abi_version() == 4
+    assert lib.mf_abi_version() == 5
 
 
 def b(addr, n):
@@ -220,3 +220,34 @@ def test_sorted_lists_flag_sizes_the_range_index():
     wide = dict(hidden=2048, x=b(0x100000, 4 * 2048 * 4), norm_weight=b(0x200000, 2048 * 4),
                 embedding=b(0x300000, 1000 * 2048 * 2))
     assert ws(flags=sorted_pass, **wide) == ws(**wide)
+
+
+def test_decode_tail_noalloc_rejects_before_any_device_call():
+    """mf_decode_tail_f16_noalloc: validation as for mf_decode_tail_f16, and
+    a call whose workspace exceeds the library's per-GPU array is a resource
+    limit, reported before anything touches a device."""
+    l = abi.lib()
+    assert l.mf_decode_tail_noalloc_max_bytes() == 16 << 20
+    a = _tail_args()
+    assert l.mf_decode_tail_f16_noalloc(ctypes.byref(a), 0).code == abi.MF_INVALID_ARGUMENT
+    assert l.mf_decode_tail_f16_noalloc(None, FAKE_STREAM).code == abi.MF_INVALID_ARGUMENT
+    bad = _tail_args(rows=0)
+    assert l.mf_decode_tail_f16_noalloc(ctypes.byref(bad), FAKE_STREAM).code == \
+        abi.MF_INVALID_ARGUMENT
+    # 1024 rows of a 2048-wide hidden with lists up to 16384 ids: a 45 MB workspace
+    rows, hidden, vocab, states, nnz = 1024, 2048, 128256, 1024, 1 << 20
+    big = _tail_args(rows=rows, hidden=hidden, vocab=vocab, states=states, nnz=nnz,
+                     max_count=16384)
+    big.x = b(0x10000000, rows * hidden * 4)
+    big.norm_weight = b(0x20000000, hidden * 4)
+    big.embedding = b(0x30000000, vocab * hidden * 2)
+    big.row_state = b(0x40000000, rows * 4)
+    big.state_offsets = b(0x50000000, (states + 1) * 4)
+    big.state_tokens = b(0x60000000, nnz * 4)
+    big.out_token = b(0x70000000, rows * 4)
+    big.out_score = b(0x80000000, rows * 4)
+    n = ctypes.c_uint64()
+    assert l.mf_decode_tail_workspace_bytes(ctypes.byref(big), ctypes.byref(n)).code == abi.MF_OK
+    assert n.value > l.mf_decode_tail_noalloc_max_bytes()
+    assert l.mf_decode_tail_f16_noalloc(ctypes.byref(big), FAKE_STREAM).code == \
+        abi.MF_RESOURCE_LIMIT
