@@ -793,7 +793,10 @@ mf::PassArgs pass_args(const mf_decode_tail_args* a, const TailLayout& L, char* 
   p.row_meta = reinterpret_cast<const mf::RowMeta*>(ws + L.row_meta);
   p.row_tiles = reinterpret_cast<const uint32_t*>(ws + L.row_tiles);
   p.range_index = reinterpret_cast<const uint4*>(ws + L.range_index);
-  p.tokens = ptr<const uint32_t>(a->state_tokens.address);
+  // the pass reads list entry 0 when a tile has no candidates; without lists
+  // (nnz == 0) that read goes to a word of the workspace instead
+  p.tokens = a->state_tokens.address != 0 ? ptr<const uint32_t>(a->state_tokens.address)
+                                          : reinterpret_cast<const uint32_t*>(ws + L.row_tiles);
   p.z_hi = reinterpret_cast<const uint16_t*>(ws + L.y_hi);
   p.row_norm = reinterpret_cast<const float*>(ws + L.row_norm);
   p.row_slack = reinterpret_cast<const float*>(ws + L.row_slack);

@@ -3,9 +3,8 @@
 // state lists are ascending (MF_TAIL_SORTED_LISTS).
 //
 // A workgroup owns a run of 192-token tiles of the vocabulary.  Per tile its
-// four waves load the tile's 12 blocks of 16 table rows into MFMA B
-// registers, three blocks per wave, the whole K range in flight, and use them
-// for both kinds of rows:
+// four waves hold the tile's 12 blocks of 16 table rows in MFMA B registers,
+// three blocks per wave, and use them for both kinds of rows:
 //
 //   restricted rows    every candidate id of a row that falls in the tile:
 //                      the norm kernel's range index gives, per row, the span
@@ -13,31 +12,45 @@
 //                      candidates are found without a search.  The FP16 hi of
 //                      z (x * w, the normalized row up to its positive factor)
 //                      of every row with candidates in the tile is staged in
-//                      LDS with global-to-LDS copies issued before the table
-//                      rows, so it has landed when they have.  Candidates are
-//                      bucketed by 16-token block; 16 at a time go through
-//                      v_mfma_f32_16x16x32_f16 with A = the candidates' rows
-//                      (one A row per candidate, from LDS) and B = the
-//                      block's table rows, and candidate i's score is
-//                      D[i][its column].  Each (row, tile) with candidates
+//                      LDS.  Candidates are bucketed by 16-token block; 16 at a
+//                      time go through v_mfma_f32_16x16x32_f16 with A = the
+//                      candidates' rows (one A row per candidate, from LDS)
+//                      and B = the block's table rows, and candidate i's score
+//                      is D[i][its column].  Each (row, tile) with candidates
 //                      gets one window record (best lower bound, <= 4
 //                      members, or "rescore all"), the format the finalize
 //                      kernel merges.
 //   unrestricted rows  the head's dense product against the FP16 hi of their
-//                      z (the norm kernel's panel, hi rows staged in LDS),
-//                      one window record per row and tile (mf_head.hpp).
+//                      z (the norm kernel's panel, hi rows staged in LDS), one
+//                      window record per row and tile (mf_head.hpp).
 //
+// Timeline of a tile.  A wave can have 63 vector-memory operations in
+// flight and they complete in issue order; a small load issued behind the
+// table's rows waits in the memory queues behind them, so the small loads
+// go first:
+//   1. the plan's per-row values;
+//   2. (plan landed) scans over the rows; the tile's first block of table
+//      rows, then the rows of z to stage (copies straight into LDS) and
+//      the candidate ids;
+//   3. (block 0, staged rows and ids landed) the second block is issued;
+//      buckets; block 0's token norms and candidates; the third block is
+//      issued; block 1's, then block 2's, each as its rows land;
+//   4. the head's A rows are staged in LDS while the candidates' records
+//      are written; the head runs against the three blocks still in
+//      registers and writes its records.
 // Scores use hi = rne_f16(z) alone: |z - hi| <= 2^-11 |z| (+ 2^-25 below the
 // FP16 normal range), which the bound carries (mf_abi.cpp pass_bound_coefs).
 // The Gram diagonal of each block (an MFMA of the block with itself) gives
 // the token norms of the bounds.  Rows with more candidates in a tile than
-// the LDS holds are taken in batches of whole rows.
+// the LDS holds are taken in batches of whole rows; later batches run after
+// the first with every block in registers.
 #include <hip/hip_runtime.h>
+
+#include <type_traits>
 
 #include "mf_device.hpp"
 #include "mf_head.hpp"
 #include "mf_launch.hpp"
-#include "mf_plan.hpp"
 
 namespace mf {
 namespace {
@@ -51,22 +64,24 @@ static_assert(kPassRowsMax == static_cast<uint32_t>(kThreads), "one plan row per
 constexpr uint32_t kPairBatch = 512;
 // Bucket entries: every block's bucket padded to whole groups of 16.
 constexpr uint32_t kBucketSlots = kPairBatch + kHeadTileBlocks * 16u;
-constexpr uint16_t kNoPair = 0xFFFFu;
+// Bucket entry: staged slot (bits 0-7), candidate index in the batch (8-17,
+// kNoPair: an empty entry), column in the block (18-21), row (22-29).
+constexpr uint32_t kNoPair = 0x3FFu;
+static_assert(kPassRowsMax <= 256u && kPairBatch <= kNoPair, "bucket entry fields");
+__device__ __forceinline__ uint32_t pair_pack(uint32_t slot, uint32_t k, uint32_t c, uint32_t r) {
+  return slot | (k << 8) | (c << 18) | (r << 22);
+}
+// Per-row flags of a batch: bit 31 = the record is rescored in full; the low
+// bits count the members.
+constexpr uint32_t kRowAll = 0x80000000u;
 // Dynamic LDS of the workgroup (one per compute unit), and the slack after
 // the staging area that a wave's last 1 KiB copy may run into.
 constexpr uint32_t kLdsBudget = 160u * 1024u - 1024u;
 constexpr uint32_t kCopySlack = 1024u;
 
-// One candidate in its block's bucket: where its row is staged, which
-// candidate of the batch it is, its column in the block and its row's bound
-// terms, so that scoring a group of 16 needs one LDS read per lane.
-struct alignas(16) PairEntry {
-  uint32_t a_off;  // byte offset of the staged row in the staging area
-  uint32_t kc;     // candidate index (bits 0..15, kNoPair: empty) | column << 16 | row << 20
-  float f1;        // coef * ||z|| + coef2 of the row
-  float f2;        // the row's absolute error term
-};
-static_assert(kPassRowsMax <= 4096u, "row index in 12 bits");
+// s_waitcnt immediate for vmcnt(0) alone (gfx9 encoding: vmcnt in bits 3:0
+// and 15:14, expcnt 6:4, lgkmcnt 11:8; the other counters at their maxima).
+constexpr int kWaitVmcnt0 = 0x0F70;
 
 // Float bits with the float order as unsigned integers (for LDS atomicMax).
 __device__ __forceinline__ uint32_t order_bits(float v) {
@@ -77,53 +92,59 @@ __device__ __forceinline__ float from_order_bits(uint32_t o) {
   return __uint_as_float((o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o);
 }
 
-struct PassShared {
-  TilePlan<kThreads, kPassRowsMax> plan;  // per row: list index of its first id in the tile
-  uint32_t lo[kPassRowsMax];              // list position of that id
-  uint32_t rec[kPassRowsMax];             // record index of (row, tile)
-  uint32_t rprefix[kPassRowsMax + 1];     // rows with candidates before row r
-  uint32_t slot_row[kPassRowsMax];        // staged slot -> row (batch)
-  float rf1[kPassRowsMax];                // coef * ||z|| + coef2, absolute error term
-  float rf2[kPassRowsMax];
-  uint32_t ptok[kPairBatch];              // candidate k of the batch: id, row, g + b
+// 16-byte aligned size: the staging area after it is read in 16-byte pieces
+// (a misaligned ds_read_b128 is split and several times slower).
+struct alignas(16) PassShared {
+  uint32_t begin[kPassRowsMax];         // list index of the row's first id in the tile
+  uint32_t count[kPassRowsMax];         // its ids in the tile
+  uint32_t prefix[kPassRowsMax + 1];    // candidates before row r
+  uint32_t rprefix[kPassRowsMax + 1];   // rows with candidates before row r
+  uint32_t lo[kPassRowsMax];            // list position of the row's first id in the tile
+  uint32_t rec[kPassRowsMax];           // record index of (row, tile)
+  uint32_t slot_row[kPassRowsMax];      // staged slot -> row (batch)
+  float rf1[kPassRowsMax];              // coef * ||z|| + coef2 of the row
+  float rf2[kPassRowsMax];              // its absolute error term
+  uint32_t row_lower[kPassRowsMax];     // per row: max of g - b, order-preserving bits
+  uint32_t row_upper[kPassRowsMax];     // per row: max of g + b, order-preserving bits
+  uint32_t row_flags[kPassRowsMax];     // kRowAll | members
+  uint32_t ptok[kPairBatch];            // candidate k of the batch: id, g + b, row
+  float pupper[kPairBatch];             // (+inf: not scored)
   uint16_t prow[kPairBatch];
-  float pupper[kPairBatch];               // (+inf: not scored)
-  uint32_t row_lower[kPassRowsMax];       // per row: max of g - b, order-preserving bits
-  uint32_t row_upper[kPassRowsMax];       // per row: max of g + b, order-preserving bits
-  uint32_t row_all[kPassRowsMax];         // per row: a candidate needs the exact rescore
-  uint32_t row_members[kPassRowsMax];     // per row: candidates with g + b >= the row's lower bound
-  PairEntry bent[kBucketSlots];
+  uint32_t bent[kBucketSlots];
   uint32_t bcount[kHeadTileBlocks];
   uint32_t bfill[kHeadTileBlocks];
-  uint32_t bstart[kHeadTileBlocks + 1];   // padded bucket starts (multiples of 16)
-  uint32_t wave_sum[kWaves];
-  float tn[kHeadTileTokens];              // token norm bounds of the tile
+  uint32_t bstart[kHeadTileBlocks + 1];  // padded bucket starts (multiples of 16)
+  uint32_t wave_n[kWaves];
+  uint32_t wave_h[kWaves];
+  float tn[kHeadTileTokens];            // token norm bounds of the tile
 };
 
-// LDS image of one FP16 row of z (or of a panel slot's hi row): H halves and
-// a 16-byte pad, the panel's own row format; the 1168-byte stride at
-// H = 576 puts the 16 rows of one A read on distinct banks.
+// LDS image of one FP16 row of z: H halves and a 16-byte pad (the panel's
+// own row format); the 1168-byte stride at H = 576 puts the 16 rows of one
+// A read on distinct banks.
 __host__ __device__ constexpr uint32_t slot_bytes(uint32_t H) { return 2u * (H + kPanelPad); }
 
 // Layout: [PassShared][staging area].  The staging area holds the rows of
-// z while candidates are scored, then the hi rows of a panel tile followed
-// by the head's epilogue scratch (HeadEpi).  The panel part is rounded up to
-// whole 1 KiB copies so that its last copy stays inside it.
-__host__ __device__ constexpr uint32_t panel_part(uint32_t H) {
-  return (kPanelRows * slot_bytes(H) + 1023u) / 1024u * 1024u;
-}
+// z while candidates are scored, then a panel tile's hi rows and the head's
+// epilogue scratch (HeadEpi).
 __host__ __device__ constexpr uint32_t stage_slots(uint32_t H) {
   const uint32_t room = kLdsBudget - static_cast<uint32_t>(sizeof(PassShared)) - kCopySlack;
   const uint32_t n = room / slot_bytes(H);
   return n < kPassRowsMax ? n : kPassRowsMax;
+}
+// The panel part is rounded up to whole 1 KiB copies so that its last copy
+// stays inside it.
+__host__ __device__ constexpr uint32_t panel_part(uint32_t H) {
+  return (kPanelRows * slot_bytes(H) + 1023u) / 1024u * 1024u;
 }
 __host__ __device__ constexpr uint32_t pass_lds_bytes(uint32_t H) {
   const uint32_t rows = stage_slots(H) * slot_bytes(H);
   const uint32_t head = panel_part(H) + static_cast<uint32_t>(sizeof(HeadEpi));
   return static_cast<uint32_t>(sizeof(PassShared)) + (rows > head ? rows : head) + kCopySlack;
 }
-static_assert(stage_slots(576) >= 96 && pass_lds_bytes(576) <= kLdsBudget,
-              "the pass fits one workgroup per CU at H = 576");
+static_assert(sizeof(PassShared) % 16 == 0, "the staging area starts 16-byte aligned");
+static_assert(stage_slots(576) >= 112 && pass_lds_bytes(576) <= kLdsBudget,
+              "the pass stages 112 rows of z at H = 576, one workgroup per CU");
 
 // Largest r1 in [r0, rows] with v[r1] - v[r0] <= limit (v nondecreasing).
 __device__ __forceinline__ uint32_t last_within(const uint32_t* v, uint32_t rows, uint32_t r0,
@@ -154,19 +175,46 @@ __device__ __forceinline__ void stage_rows(unsigned char* area, uint32_t n, Src 
   }
 }
 
-// One group of 16 candidates: its bucket entries (lane l < 16 holds
-// candidate l's) and A rows from the staged slots.
-template <int kSteps>
-struct Group {
-  PairEntry e;
-  half8_t a[kSteps];
-};
+// stage_rows for rows of z given by a slot -> row map in LDS, eight copies
+// per round: the eight map reads are issued together, then the eight
+// copies (a loop of single copies pays an LDS round trip per copy).
+template <uint32_t H>
+__device__ __forceinline__ void stage_rows_batched(unsigned char* area, uint32_t n,
+                                                   const uint32_t* slot_row, const uint16_t* z) {
+  constexpr uint32_t per = slot_bytes(H) / 16u;
+  constexpr uint32_t kRound = 8;
+  const uint32_t lane = threadIdx.x % kWave;
+  const uint32_t wave = threadIdx.x / kWave;
+  const uint32_t pieces = n * per;
+  const uint32_t copies = (pieces + kWave - 1u) / kWave;  // over the workgroup
+  for (uint32_t c0 = wave; c0 < copies; c0 += kWaves * kRound) {
+    uint32_t i[kRound];
+    uint32_t pp[kRound];
+    uint32_t rr[kRound];
+#pragma unroll
+    for (uint32_t u = 0; u < kRound; ++u) {
+      const uint32_t q = (c0 + u * kWaves) * kWave + lane;
+      i[u] = q < pieces ? q / per : 0u;
+      pp[u] = q < pieces ? q % per : 0u;
+      rr[u] = slot_row[i[u]];
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < kRound; ++u) {
+      const uint32_t c = c0 + u * kWaves;
+      if (c < copies) {
+        burst_to_lds(z + static_cast<uint64_t>(rr[u]) * H + (pp[u] < per - 1u ? pp[u] : 0u) * 8u,
+                     area + c * kWave * 16u);
+      }
+    }
+  }
+}
 
 template <int kSteps>
 __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
   constexpr uint32_t H = 32u * kSteps;
   constexpr uint32_t kSlot = slot_bytes(H);
   constexpr uint32_t kTileHalves = static_cast<uint32_t>(panel_tile_bytes(H) / 2u);
+  constexpr uint32_t kPanelSlotHalves = 2u * (H + kPanelPad);  // one panel slot's [hi | lo]
   extern __shared__ __align__(16) unsigned char dyn[];
   __shared__ uint32_t src_row[kPanelRows];
   __shared__ float src_norm[kPanelRows];
@@ -175,7 +223,8 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
   const uint32_t panels = f.m > 0 ? panel_tiles(f.m) : 0u;
   PassShared& ps = *reinterpret_cast<PassShared*>(dyn);
   unsigned char* stage = dyn + sizeof(PassShared);
-  // after the candidates: a panel tile's hi rows, then the head's epilogue
+  // after the candidates: a panel tile's hi rows (tiles past the first),
+  // then the head's epilogue
   unsigned char* panel = stage;
   HeadEpi& epi = *reinterpret_cast<HeadEpi*>(stage + panel_part(H));
   const uint32_t slots = stage_slots(H);
@@ -190,48 +239,97 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
   const uint32_t kb = lane / 16;
 
   half8_t bt[kBlocks][kSteps];
-  auto load_tile = [&](uint32_t t) {
+  auto load_block = [&](uint32_t t, int tb) {
+    const uint32_t token = t * kHeadTileTokens + (wave * kBlocks + tb) * 16u + col;
+    const uint16_t* src = f.emb + static_cast<uint64_t>(token < f.V ? token : 0u) * H + kb * 8u;
 #pragma unroll
-    for (int tb = 0; tb < kBlocks; ++tb) {
-      const uint32_t token = t * kHeadTileTokens + (wave * kBlocks + tb) * 16u + col;
-      const uint16_t* src = f.emb + static_cast<uint64_t>(token < f.V ? token : 0u) * H + kb * 8u;
-#pragma unroll
-      for (int s = 0; s < kSteps; ++s) bt[tb][s] = *reinterpret_cast<const half8_t*>(src + s * 32);
-    }
+    for (int s = 0; s < kSteps; ++s) bt[tb][s] = *reinterpret_cast<const half8_t*>(src + s * 32);
   };
-  // the hi rows of panel tile pt (slot j's hi row leads its [hi | lo] pair)
+  // The head's A operand: a panel tile's hi rows staged in LDS (slot j in
+  // LDS slot j); its MFMAs against every block of the tile
   auto stage_panel = [&](uint32_t pt) {
     const uint16_t* base = f.panel + static_cast<uint64_t>(pt) * kTileHalves;
-    stage_rows<H>(panel, kPanelRows, [&](uint32_t j) { return base + j * 2u * (H + kPanelPad); });
+    stage_rows<H>(panel, kPanelRows, [&](uint32_t j) { return base + j * kPanelSlotHalves; });
   };
+  auto head_lds = [&](HeadAcc<kBlocks>& h) {
+#pragma unroll
+    for (int tb = 0; tb < kBlocks; ++tb) {
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb) h.acc[rb][tb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    const unsigned char* a_lane = panel + col * kSlot + kb * 16u;
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) {
+      half8_t a[2];
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb) a[rb] = *reinterpret_cast<const half8_t*>(a_lane + rb * 16u * kSlot + s * 64);
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb) {
+#pragma unroll
+        for (int tb = 0; tb < kBlocks; ++tb) {
+          h.acc[rb][tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[rb], bt[tb][s], h.acc[rb][tb], 0, 0, 0);
+        }
+      }
+    }
+  };
+
+  constexpr int kWarm = 4;  // 16-byte loads per lane and array (16 KiB of each per workgroup)
+  uint32_t warm[2][kWarm] = {};
 
   for (uint32_t tile = t_begin; tile < t_end; ++tile) {
     const uint32_t t0 = tile * kHeadTileTokens;
-    // (1) the tile's candidates: per row (one per thread) the span [lo, hi)
-    // of its list (range index of the norm kernel, range-major).
+    // (1) the small loads first, ahead of the table's: the plan's per-row
+    // values (one row per thread; the range index is range-major, so
+    // contiguous)
     const uint32_t ri = tid < rows ? tid : 0u;
     const RowMeta m = p.row_meta[ri];
     const uint32_t rt = p.row_tiles[ri];
     const uint4 ix = p.range_index[static_cast<uint64_t>(tile) * rows + ri];
-    const uint32_t lo_r = ix.x;
-    const uint32_t hi_r = ix.y;
-    const uint32_t rec_r = ix.z;
     const float norm_r = p.row_norm[ri];
     const float slack_r = p.row_slack[ri];
+    __builtin_amdgcn_sched_barrier(0);
     {
+      // Warm this XCD's L2 with the rows of z and the head's panel, which
+      // the norm kernel wrote just before (from every XCD): workgroup i
+      // runs on XCD i % 8, and the 32 workgroups of an XCD each touch a
+      // 32nd of both, so that the staging copies below hit L2 instead of
+      // queueing 32 misses per line at the last-level cache.  Issued after
+      // the plan's loads (which do not wait for them), every tile (no
+      // branch around loads); the values are not used.
+      const uint32_t share = (blockIdx.x / 8u) % 32u;
+      auto touch = [&](const uint16_t* base, uint64_t bytes, uint32_t (&w)[kWarm]) {
+        const uint64_t part = (bytes / 32u + 1023u) & ~uint64_t{1023u};
+        const unsigned char* b = reinterpret_cast<const unsigned char*>(base);
+#pragma unroll
+        for (int u = 0; u < kWarm; ++u) {
+          const uint64_t o = share * part + (static_cast<uint64_t>(u) * kThreads + tid) * 16u;
+          w[u] = *reinterpret_cast<const uint32_t*>(b + (o + 16u <= bytes ? o : 0u));
+        }
+      };
+      touch(p.z_hi, static_cast<uint64_t>(rows) * H * 2u, warm[0]);
+      touch(panels > 0u ? f.panel : p.z_hi,
+            panels > 0u ? static_cast<uint64_t>(panels) * panel_tile_bytes(H) : 16u, warm[1]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // (2) per row its span [lo, hi) in the tile; exclusive scans over the
+    // rows: candidates and rows with candidates
+    {
+      const uint32_t lo_r = ix.x;
+      const uint32_t hi_r = ix.y;
+      const uint32_t rec_r = ix.z;
       const bool use = tid < rows && (m.kind & kRowRestricted) && !(rt & kRangesUnused) &&
                        hi_r > lo_r && hi_r <= m.count && rec_r < p.max_recs;
       const uint32_t n = use ? hi_r - lo_r : 0u;
       const uint32_t has = n > 0u ? 1u : 0u;
       if (tid < rows) {
-        ps.plan.begin[tid] = m.list_begin + lo_r;
-        ps.plan.count[tid] = n;
+        ps.begin[tid] = m.list_begin + lo_r;
+        ps.count[tid] = n;
         ps.lo[tid] = lo_r;
         ps.rec[tid] = rec_r;
         ps.rf1[tid] = __builtin_fmaf(p.coef, norm_r, p.coef2);
         ps.rf2[tid] = slack_r;
       }
-      // exclusive scans over the rows: candidates and rows with candidates
       uint32_t in_n = n;
       uint32_t in_h = has;
 #pragma unroll
@@ -244,71 +342,115 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
         }
       }
       if (lane == kWave - 1) {
-        ps.plan.wave_total[wave] = in_n;
-        ps.wave_sum[wave] = in_h;
+        ps.wave_n[wave] = in_n;
+        ps.wave_h[wave] = in_h;
       }
       __syncthreads();
       uint32_t bn = in_n - n;
       uint32_t bh = in_h - has;
       for (uint32_t w = 0; w < wave; ++w) {
-        bn += ps.plan.wave_total[w];
-        bh += ps.wave_sum[w];
+        bn += ps.wave_n[w];
+        bh += ps.wave_h[w];
       }
       if (tid <= rows) {  // tid == rows: the totals
-        ps.plan.prefix[tid] = bn;
+        ps.prefix[tid] = bn;
         ps.rprefix[tid] = bh;
       }
       if (tid == kThreads - 1 && rows == kPassRowsMax) {
-        ps.plan.prefix[rows] = bn + n;
+        ps.prefix[rows] = bn + n;
         ps.rprefix[rows] = bh + has;
       }
       __syncthreads();
     }
 
-    // (2) per batch of whole rows: stage, ids, buckets, scores, records.
-    // The first batch's staging and ids are issued before the table rows.
+    // (3) batches of whole rows.  The first is scored block by block as the
+    // table rows land; the others (rows past the LDS stage) afterwards.
+    HeadAcc<kBlocks> h;
     uint32_t r0 = 0u;
-    bool first = true;
-    while (first || r0 < rows) {
-      const uint32_t r1a = last_within(ps.plan.prefix, rows, r0, kPairBatch);
-      const uint32_t r1b = last_within(ps.rprefix, rows, r0, slots);
-      const uint32_t r1 = r1a < r1b ? r1a : r1b;
-      const uint32_t k0 = ps.plan.prefix[r0];
-      const uint32_t nb = ps.plan.prefix[r1] - k0;
+    // the batch body, compiled separately for the first batch (which issues
+    // the table rows) and the others, so that no control-flow join makes
+    // the compiler's memory waits conservative
+    auto run_batch = [&](auto first_c) -> bool {
+      constexpr bool first = decltype(first_c)::value;
+      // (the common case, every remaining row in one batch, without the
+      // searches)
+      const bool fits = ps.prefix[rows] - ps.prefix[r0] <= kPairBatch &&
+                        ps.rprefix[rows] - ps.rprefix[r0] <= slots;
+      uint32_t r1 = rows;
+      if (!fits) {
+        const uint32_t r1a = last_within(ps.prefix, rows, r0, kPairBatch);
+        const uint32_t r1b = last_within(ps.rprefix, rows, r0, slots);
+        r1 = r1a < r1b ? r1a : r1b;
+      }
+      const uint32_t k0 = ps.prefix[r0];
+      const uint32_t nb = ps.prefix[r1] - k0;
       const uint32_t s0 = ps.rprefix[r0];
       const uint32_t nz = ps.rprefix[r1] - s0;
       if (tid < kHeadTileBlocks) {
         ps.bcount[tid] = 0u;
         ps.bfill[tid] = 0u;
       }
-      if (tid >= r0 && tid < r1 && ps.plan.count[tid] > 0u) ps.slot_row[ps.rprefix[tid] - s0] = tid;
+      if (tid >= r0 && tid < r1 && ps.count[tid] > 0u) ps.slot_row[ps.rprefix[tid] - s0] = tid;
       if (tid < rows) {
         ps.row_lower[tid] = order_bits(-__builtin_huge_valf());
         ps.row_upper[tid] = order_bits(-__builtin_huge_valf());
-        ps.row_all[tid] = 0u;
-        ps.row_members[tid] = 0u;
+        ps.row_flags[tid] = 0u;
       }
       __syncthreads();  // slot rows, cleared counters
-      uint32_t tok[2] = {0u, 0u};
-      uint32_t row[2] = {0u, 0u};
-      if (nb > 0u) {
-        // lanes past the batch load candidate k0 again (a valid list
-        // position) instead of branching around their loads
+      // the rows of the batch's candidates (LDS only), the batch's rows of z
+      // straight into LDS, then its candidate ids (lanes past the batch
+      // load candidate k0 again, a valid list position, instead of
+      // branching around their loads; a batch without candidates reads list
+      // entry 0, which the host guarantees readable), then -- first batch
+      // -- the first two blocks of table rows
+      uint32_t row[2];
+      uint32_t at[2];
+      {
+        uint32_t kk[2], lo2[2] = {0u, 0u}, hi2[2] = {rows, rows};
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
           const uint32_t k = k0 + tid + u * kThreads;
-          const uint32_t kk = k < k0 + nb ? k : k0;
-          row[u] = plan_row_of(ps.plan, rows, kk);
-          tok[u] = p.tokens[ps.plan.begin[row[u]] + (kk - ps.plan.prefix[row[u]])];
+          kk[u] = k < k0 + nb ? k : k0;
+        }
+        // the row holding candidate kk: the largest r with prefix[r] <= kk
+        // < prefix[r + 1] (two binary searches side by side)
+        while (lo2[0] < hi2[0] || lo2[1] < hi2[1]) {
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            if (lo2[u] < hi2[u]) {
+              const uint32_t mid = (lo2[u] + hi2[u]) / 2;
+              if (ps.prefix[mid + 1] <= kk[u]) lo2[u] = mid + 1; else hi2[u] = mid;
+            }
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          row[u] = lo2[u] < rows ? lo2[u] : rows - 1u;
+          at[u] = nb > 0u ? ps.begin[row[u]] + (kk[u] - ps.prefix[row[u]]) : 0u;
         }
       }
       __builtin_amdgcn_sched_barrier(0);
-      stage_rows<H>(stage, nz, [&](uint32_t i) { return p.z_hi + static_cast<uint64_t>(ps.slot_row[i]) * H; });
+      // first batch: block 0 of the table rows streams while the rows of z
+      // are copied (the copies are issued at a limited rate)
+      if constexpr (first) load_block(tile, 0);
       __builtin_amdgcn_sched_barrier(0);
-      if (first) load_tile(tile);
+      stage_rows_batched<H>(stage, nz, ps.slot_row, p.z_hi);
       __builtin_amdgcn_sched_barrier(0);
-      if (first && panels == 1u && tile == t_begin) head_slots(f, 0u, src_row, src_norm, src_slack);
+      uint32_t tok[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) tok[u] = p.tokens[at[u]];
       __builtin_amdgcn_sched_barrier(0);
+      if constexpr (first) {
+        // block 0, the rows of z and the ids landed (a wait the compiler
+        // sees, so that it counts the later table loads in order again),
+        // then block 1 (a wave keeps about 32 loads in flight; block 2 is
+        // issued once block 0 is scored)
+        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+        __builtin_amdgcn_sched_barrier(0);
+        load_block(tile, 1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      // buckets: each candidate in its 16-token block's bucket
       uint32_t blk[2];
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
@@ -322,7 +464,7 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
           if (blk[u] < kHeadTileBlocks) {
             atomicAdd(&ps.bcount[blk[u]], 1u);
           } else {
-            ps.row_all[row[u]] = 1u;  // an id outside the tile: rescore the record in full
+            atomicOr(&ps.row_flags[row[u]], kRowAll);  // an id outside the tile: rescore in full
           }
         }
       }
@@ -335,103 +477,116 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
         }
         ps.bstart[kHeadTileBlocks] = run;
       }
-      for (uint32_t e = tid; e < kBucketSlots; e += kThreads) {
-        ps.bent[e] = PairEntry{0u, static_cast<uint32_t>(kNoPair), 0.0f, 0.0f};
-      }
+      for (uint32_t e = tid; e < kBucketSlots; e += kThreads) ps.bent[e] = pair_pack(0u, kNoPair, 0u, 0u);
       __syncthreads();
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         if (blk[u] < kHeadTileBlocks) {
           const uint32_t at = ps.bstart[blk[u]] + atomicAdd(&ps.bfill[blk[u]], 1u);
           const uint32_t r = row[u];
-          ps.bent[at] = PairEntry{(ps.rprefix[r] - s0) * kSlot,
-                                  (tid + u * kThreads) | (((tok[u] - t0) % 16u) << 16) | (r << 20),
-                                  ps.rf1[r], ps.rf2[r]};
+          ps.bent[at] = pair_pack(ps.rprefix[r] - s0, tid + u * kThreads, (tok[u] - t0) % 16u, r);
         }
       }
-      wait_vector_memory();  // table rows (first batch), staged rows
-      floatx4 gram[kBlocks];
-      if (first) {
-        // Gram diagonal: token norm bounds of the tile
-#pragma unroll
-        for (int tb = 0; tb < kBlocks; ++tb) {
-          gram[tb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-          for (int s = 0; s < kSteps; ++s) {
-            gram[tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bt[tb][s], bt[tb][s], gram[tb], 0, 0, 0);
-          }
-          const uint32_t e = col % 4u;
-          const float d = e == 0u ? gram[tb][0]
-                                  : (e == 1u ? gram[tb][1] : (e == 2u ? gram[tb][2] : gram[tb][3]));
-          if (col / 4u == kb) ps.tn[(wave * kBlocks + tb) * 16u + col] = __fsqrt_rn(d) * (1.0f + 0x1p-7f);
-        }
-      }
-      __syncthreads();  // buckets, staged rows and token norms visible
+      if constexpr (!first) wait_vector_memory();  // the staged rows have landed
+      __syncthreads();  // buckets and staged rows visible
 
-      // (3) this wave's groups: its three blocks' buckets, 16 candidates
-      // per group, two accumulators per group (even and odd steps)
-      const uint32_t qb = __builtin_amdgcn_readfirstlane(ps.bstart[wave * kBlocks] / 16u);
-      const uint32_t q1 = __builtin_amdgcn_readfirstlane(ps.bstart[wave * kBlocks + 1] / 16u) - qb;
-      const uint32_t q2 = __builtin_amdgcn_readfirstlane(ps.bstart[wave * kBlocks + 2] / 16u) - qb;
-      const uint32_t nq = __builtin_amdgcn_readfirstlane(ps.bstart[wave * kBlocks + 3] / 16u) - qb;
-      auto load_group = [&](uint32_t q, Group<kSteps>& g) {
-        g.e = ps.bent[(qb + (q < nq ? q : 0u)) * 16u + col];
-        const unsigned char* src = stage + g.e.a_off + kb * 16u;
-#pragma unroll
-        for (int s = 0; s < kSteps; ++s) g.a[s] = *reinterpret_cast<const half8_t*>(src + s * 64);
-      };
-      auto score_group = [&](uint32_t q, const Group<kSteps>& g) {
+      // (4) this wave's blocks in landing order: token norms (first batch),
+      // the candidates 16 at a time (two accumulators per group, even and
+      // odd steps), the head of panel tile 0 (first batch)
+      // A rows in two halves of the K range (half the registers of a
+      // whole group in flight); every read of a half is issued before its
+      // MFMAs (the scheduler would otherwise sink each read next to its
+      // MFMA and pay the LDS latency per step)
+      constexpr int kHalf = (kSteps + 1) / 2;
+      auto score_group = [&](uint32_t q, const half8_t(&b)[kSteps], uint32_t blk_id) {
+        const uint32_t ge = ps.bent[q * 16u + col];
+        const unsigned char* a_src = stage + (ge & 0xFFu) * kSlot + kb * 16u;
         floatx4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f};
         floatx4 acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
-        auto chain = [&](const half8_t(&b)[kSteps]) {
 #pragma unroll
-          for (int s = 0; s < kSteps; s += 2) {
-            acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(g.a[s], b[s], acc0, 0, 0, 0);
-            if (s + 1 < kSteps) acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(g.a[s + 1], b[s + 1], acc1, 0, 0, 0);
+        for (int h0 = 0; h0 < kSteps; h0 += kHalf) {
+          half8_t a[kHalf];
+#pragma unroll
+          for (int s = 0; s < kHalf; ++s) {
+            if (h0 + s < kSteps) a[s] = *reinterpret_cast<const half8_t*>(a_src + (h0 + s) * 64);
           }
-        };
-        if (q < q1) chain(bt[0]); else if (q < q2) chain(bt[1]); else chain(bt[2]);
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int s = 0; s < kHalf; ++s) {
+            if (h0 + s < kSteps) {
+              if (s % 2 == 0) {
+                acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[s], b[h0 + s], acc0, 0, 0, 0);
+              } else {
+                acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[s], b[h0 + s], acc1, 0, 0, 0);
+              }
+            }
+          }
+        }
         const floatx4 acc = acc0 + acc1;
         // candidate i = lane (lanes 0..15): D[i][c] sits in lane
         // 16 (i / 4) + c, element i % 4
-        const uint32_t k = g.e.kc & 0xFFFFu;
-        const uint32_t c = (g.e.kc >> 16) & 15u;
-        const uint32_t r = g.e.kc >> 20;
+        const uint32_t k = (ge >> 8) & 0x3FFu;
+        const uint32_t c = (ge >> 18) & 15u;
+        const uint32_t r = ge >> 22;
         const bool mine = lane < 16u && k != kNoPair;
         const int src = lane < 16u ? static_cast<int>(16u * (lane / 4u) + c) : static_cast<int>(lane);
         const float v0 = __shfl(acc[0], src);
         const float v1 = __shfl(acc[1], src);
         const float v2 = __shfl(acc[2], src);
         const float v3 = __shfl(acc[3], src);
-        const uint32_t blk = q < q1 ? 0u : (q < q2 ? 1u : 2u);
-        const float tnv = ps.tn[(wave * kBlocks + blk) * 16u + c];
+        const float tnv = ps.tn[blk_id * 16u + c];
         if (mine) {
           const uint32_t e = lane % 4u;
           const float gs = e == 0u ? v0 : (e == 1u ? v1 : (e == 2u ? v2 : v3));
-          const float b = __builtin_fmaf(tnv, g.e.f1, g.e.f2);
-          const bool ok = __builtin_isfinite(gs) && __builtin_isfinite(b) && b < 0x1p100f;
+          const float bnd = __builtin_fmaf(tnv, ps.rf1[r], ps.rf2[r]);
+          const bool ok = __builtin_isfinite(gs) && __builtin_isfinite(bnd) && bnd < 0x1p100f;
           if (ok) {
-            atomicMax(&ps.row_lower[r], order_bits(gs - b));
-            atomicMax(&ps.row_upper[r], order_bits(gs + b));
-            ps.pupper[k] = gs + b;
+            atomicMax(&ps.row_lower[r], order_bits(gs - bnd));
+            atomicMax(&ps.row_upper[r], order_bits(gs + bnd));
+            ps.pupper[k] = gs + bnd;
           } else {
-            ps.row_all[r] = 1u;
+            atomicOr(&ps.row_flags[r], kRowAll);
           }
         }
       };
-      // one group at a time: its LDS reads complete in order, so each MFMA
-      // waits only for its own operand (a second group in flight costs
-      // register spills)
-      for (uint32_t q = 0; q < nq; ++q) {
-        Group<kSteps> g;
-        load_group(q, g);
-        score_group(q, g);
+#pragma unroll
+      for (int tb = 0; tb < kBlocks; ++tb) {
+        const uint32_t blk_id = wave * kBlocks + tb;
+        if constexpr (first) {
+          // Gram diagonal: token norm bounds of the block (this wave's own)
+          h.gram[tb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int s = 0; s < kSteps; ++s) {
+            h.gram[tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bt[tb][s], bt[tb][s], h.gram[tb], 0, 0, 0);
+          }
+          const uint32_t e = col % 4u;
+          const float d = e == 0u ? h.gram[tb][0]
+                                  : (e == 1u ? h.gram[tb][1] : (e == 2u ? h.gram[tb][2] : h.gram[tb][3]));
+          if (col / 4u == kb) ps.tn[blk_id * 16u + col] = __fsqrt_rn(d) * (1.0f + 0x1p-7f);
+          wave_sync();
+        }
+        const uint32_t qa = __builtin_amdgcn_readfirstlane(ps.bstart[blk_id] / 16u);
+        const uint32_t qz = __builtin_amdgcn_readfirstlane(ps.bstart[blk_id + 1] / 16u);
+        // one group at a time: its LDS reads complete in order, so each
+        // MFMA waits only for its own operand
+        for (uint32_t q = qa; q < qz; ++q) {
+          score_group(q, bt[tb], blk_id);
+        }
+        if constexpr (first) {
+          if (tb == 0) {
+            __builtin_amdgcn_sched_barrier(0);
+            load_block(tile, 2);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
       }
       __syncthreads();  // every candidate scored; the staging area is free
-      // the first panel tile's hi rows land while the records are written
-      if (first && panels > 0u) stage_panel(0u);
+      // the last batch: panel tile 0's hi rows land while the records are
+      // written
+      const bool last = r1 >= rows || nb == 0u;
+      if (last && panels > 0u) stage_panel(0u);
 
-      // (4) one window record per (row, tile).  The best lower bound came
+      // (5) one window record per (row, tile).  The best lower bound came
       // from the scoring; each candidate then checks itself against its
       // row's (members in any order: the finalize only collects them), and
       // one thread per row writes the header.  The list is ascending, so a
@@ -442,10 +597,10 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
         if (kk < nb) {
           const uint32_t r = ps.prow[kk];
           const float up = ps.pupper[kk];
-          if (ps.row_all[r] == 0u && up >= from_order_bits(ps.row_lower[r])) {
-            const uint32_t i = atomicAdd(&ps.row_members[r], 1u);
+          if (!(ps.row_flags[r] & kRowAll) && up >= from_order_bits(ps.row_lower[r])) {
+            const uint32_t i = atomicAdd(&ps.row_flags[r], 1u) & ~kRowAll;
             if (i < static_cast<uint32_t>(kTileMembers)) {
-              const uint32_t j = k0 + kk - ps.plan.prefix[r];
+              const uint32_t j = k0 + kk - ps.prefix[r];
               TileRecord* rec = p.records + static_cast<uint64_t>(r) * p.max_recs + ps.rec[r];
               // g - b of a member is only used against the row's window
               rec->m[i] = TileMember{ps.ptok[kk], ps.lo[r] + j, -__builtin_huge_valf(), up};
@@ -455,65 +610,48 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
       }
       __syncthreads();
       for (uint32_t r = r0 + tid; r < r1; r += kThreads) {
-        const uint32_t n = ps.plan.count[r];
+        const uint32_t n = ps.count[r];
         if (n == 0u) continue;
-        const uint32_t members = ps.row_members[r];
-        const bool ordinary = ps.row_all[r] == 0u && members <= static_cast<uint32_t>(kTileMembers);
+        const uint32_t fl = ps.row_flags[r];
+        const bool all = (fl & kRowAll) != 0u;
+        const uint32_t members = fl & ~kRowAll;
+        const bool ordinary = !all && members <= static_cast<uint32_t>(kTileMembers);
         TileRecord* rec = p.records + static_cast<uint64_t>(r) * p.max_recs + ps.rec[r];
         const uint32_t lo = ps.lo[r];
         rec->best_lower = from_order_bits(ps.row_lower[r]);
-        rec->flags = ordinary ? 0u
-                              : (ps.row_all[r] == 0u ? kTileRescoreAll | kTileCrowded : kTileRescoreAll);
+        rec->flags = ordinary ? 0u : (all ? kTileRescoreAll : kTileRescoreAll | kTileCrowded);
         rec->upper_max = from_order_bits(ps.row_upper[r]);
-        rec->min_token = ps.ptok[ps.plan.prefix[r] - k0];
+        rec->min_token = ps.ptok[ps.prefix[r] - k0];
         rec->min_pos = lo;
         rec->begin = lo;
         rec->count = n;
         rec->n_members = ordinary ? members : 0u;
       }
-
-      // (5) the unrestricted rows (first batch): the head against the panel
-      // tiles' hi rows
-      if (first) {
-        for (uint32_t pt = 0; pt < panels; ++pt) {
-          if (pt > 0u) {
-            __syncthreads();  // the previous panel tile's readers are done
-            stage_panel(pt);
-          }
-          if (panels > 1u) head_slots(f, pt * kPanelRows, src_row, src_norm, src_slack);
-          wait_vector_memory();
-          __syncthreads();
-          HeadAcc<kBlocks> h;
-#pragma unroll
-          for (int tb = 0; tb < kBlocks; ++tb) {
-            h.gram[tb] = gram[tb];
-#pragma unroll
-            for (int rb = 0; rb < 4; ++rb) h.acc[rb][tb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-          }
-          const unsigned char* a_lane = panel + col * kSlot + kb * 16u;
-#pragma unroll
-          for (int s = 0; s < kSteps; ++s) {
-            half8_t a[2];
-#pragma unroll
-            for (int rb = 0; rb < 2; ++rb) a[rb] = *reinterpret_cast<const half8_t*>(a_lane + rb * 16u * kSlot + s * 64);
-#pragma unroll
-            for (int rb = 0; rb < 2; ++rb) {
-#pragma unroll
-              for (int tb = 0; tb < kBlocks; ++tb) {
-                h.acc[rb][tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[rb], bt[tb][s], h.acc[rb][tb], 0, 0, 0);
-              }
-            }
-          }
-          head_records<kWaves, kBlocks, true>(f, h, epi, src_row, src_norm, src_slack,
-                                              pt * kPanelRows, tile, tiles);
-        }
-      }
       __syncthreads();  // the batch's LDS is free again
-      first = false;
       r0 = r1;
-      if (nb == 0u) break;
+      return r0 < rows && nb > 0u;
+    };
+    if (run_batch(std::true_type{})) {
+      while (run_batch(std::false_type{})) {
+      }
+    }
+
+    // (6) the unrestricted rows: the head against each panel tile's hi rows
+    // (panel tile 0 was staged by the last batch) and its records
+    for (uint32_t pt = 0; pt < panels; ++pt) {
+      if (pt > 0u) stage_panel(pt);  // the previous tile's readers are done
+      head_slots(f, pt * kPanelRows, src_row, src_norm, src_slack);
+      wait_vector_memory();
+      __syncthreads();
+      head_lds(h);
+      head_records<kWaves, kBlocks, true>(f, h, epi, src_row, src_norm, src_slack,
+                                          pt * kPanelRows, tile, tiles);
     }
   }
+  uint32_t warm_all = 0u;
+#pragma unroll
+  for (int u = 0; u < kWarm; ++u) warm_all ^= warm[0][u] ^ warm[1][u];
+  asm volatile("" ::"v"(warm_all));  // keeps the warming loads
 }
 
 template <int kSteps>
