@@ -24,20 +24,23 @@
 //                      z (the norm kernel's panel, hi rows staged in LDS), one
 //                      window record per row and tile (mf_head.hpp).
 //
-// Timeline of a tile.  A wave can have 63 vector-memory operations in
-// flight and they complete in issue order; a small load issued behind the
-// table's rows waits in the memory queues behind them, so the small loads
-// go first:
-//   1. the plan's per-row values;
-//   2. (plan landed) scans over the rows; the tile's first block of table
-//      rows, then the rows of z to stage (copies straight into LDS) and
-//      the candidate ids;
-//   3. (block 0, staged rows and ids landed) the second block is issued;
-//      buckets; block 0's token norms and candidates; the third block is
-//      issued; block 1's, then block 2's, each as its rows land;
+// Timeline of a tile.  The compute unit's vector memory pipeline is the
+// bottleneck: loads complete in issue order, and a wave issuing more than
+// the pipeline holds stalls until earlier loads drain, so the order of the
+// loads is the schedule:
+//   1. the plan's per-row values, then the tile's first block of table
+//      rows (it streams while the plan is scanned);
+//   2. (plan landed) scans over the rows, each candidate's row, then the
+//      rows of z to stage (copies straight into LDS) and the candidate ids;
+//   3. (all landed) the second block; buckets; block 0's token norms and
+//      candidates; the third block is issued; block 1's, then block 2's
+//      candidates, each as its rows land;
 //   4. the head's A rows are staged in LDS while the candidates' records
 //      are written; the head runs against the three blocks still in
 //      registers and writes its records.
+// A block's candidates run as a software pipeline (A rows of the next group
+// read from LDS while the MFMAs of this one run); candidate scoring is
+// bound by LDS bandwidth (one 1152-byte A row per candidate).
 // Scores use hi = rne_f16(z) alone: |z - hi| <= 2^-11 |z| (+ 2^-25 below the
 // FP16 normal range), which the bound carries (mf_abi.cpp pass_bound_coefs).
 // The Gram diagonal of each block (an MFMA of the block with itself) gives
@@ -78,7 +81,6 @@ constexpr uint32_t kRowAll = 0x80000000u;
 // the staging area that a wave's last 1 KiB copy may run into.
 constexpr uint32_t kLdsBudget = 160u * 1024u - 1024u;
 constexpr uint32_t kCopySlack = 1024u;
-
 // s_waitcnt immediate for vmcnt(0) alone (gfx9 encoding: vmcnt in bits 3:0
 // and 15:14, expcnt 6:4, lgkmcnt 11:8; the other counters at their maxima).
 constexpr int kWaitVmcnt0 = 0x0F70;
@@ -257,19 +259,32 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
 #pragma unroll
       for (int rb = 0; rb < 2; ++rb) h.acc[rb][tb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     }
+    // A reads kAhead steps ahead of their MFMAs (a step's six MFMAs do not
+    // cover the LDS latency of its own reads)
+    constexpr int kAhead = 2;
     const unsigned char* a_lane = panel + col * kSlot + kb * 16u;
+    half8_t a[kAhead + 1][2];
+    auto read_step = [&](int s) {
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb) {
+        a[s % (kAhead + 1)][rb] = *reinterpret_cast<const half8_t*>(a_lane + rb * 16u * kSlot + s * 64);
+      }
+    };
+#pragma unroll
+    for (int s = 0; s < kAhead; ++s) read_step(s);
 #pragma unroll
     for (int s = 0; s < kSteps; ++s) {
-      half8_t a[2];
-#pragma unroll
-      for (int rb = 0; rb < 2; ++rb) a[rb] = *reinterpret_cast<const half8_t*>(a_lane + rb * 16u * kSlot + s * 64);
+      if (s + kAhead < kSteps) read_step(s + kAhead);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int rb = 0; rb < 2; ++rb) {
 #pragma unroll
         for (int tb = 0; tb < kBlocks; ++tb) {
-          h.acc[rb][tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[rb], bt[tb][s], h.acc[rb][tb], 0, 0, 0);
+          h.acc[rb][tb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[s % (kAhead + 1)][rb], bt[tb][s],
+                                                                 h.acc[rb][tb], 0, 0, 0);
         }
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
 
@@ -310,6 +325,10 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
       touch(panels > 0u ? f.panel : p.z_hi,
             panels > 0u ? static_cast<uint64_t>(panels) * panel_tile_bytes(H) : 16u, warm[1]);
     }
+    __builtin_amdgcn_sched_barrier(0);
+    // the tile's first block of table rows, behind the small loads: it
+    // streams while the plan is scanned and the rows of z are staged
+    load_block(tile, 0);
     __builtin_amdgcn_sched_barrier(0);
 
     // (2) per row its span [lo, hi) in the tile; exclusive scans over the
@@ -390,49 +409,38 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
         ps.bcount[tid] = 0u;
         ps.bfill[tid] = 0u;
       }
-      if (tid >= r0 && tid < r1 && ps.count[tid] > 0u) ps.slot_row[ps.rprefix[tid] - s0] = tid;
+      if (tid >= r0 && tid < r1) {
+        const uint32_t n = ps.count[tid];
+        if (n > 0u) {
+          ps.slot_row[ps.rprefix[tid] - s0] = tid;
+          // the row of each of its candidates (a row has at most one
+          // tile's worth)
+          const uint32_t base = ps.prefix[tid] - k0;
+          for (uint32_t j = 0; j < n; ++j) ps.prow[base + j] = static_cast<uint16_t>(tid);
+        }
+      }
       if (tid < rows) {
         ps.row_lower[tid] = order_bits(-__builtin_huge_valf());
         ps.row_upper[tid] = order_bits(-__builtin_huge_valf());
         ps.row_flags[tid] = 0u;
       }
-      __syncthreads();  // slot rows, cleared counters
-      // the rows of the batch's candidates (LDS only), the batch's rows of z
-      // straight into LDS, then its candidate ids (lanes past the batch
-      // load candidate k0 again, a valid list position, instead of
+      __syncthreads();  // slot rows, candidate rows, cleared counters
+      // the batch's rows of z straight into LDS (block 0 of the table rows
+      // streams ahead of them), then its candidate ids (lanes past the
+      // batch load candidate k0 again, a valid list position, instead of
       // branching around their loads; a batch without candidates reads list
       // entry 0, which the host guarantees readable), then -- first batch
-      // -- the first two blocks of table rows
+      // -- the second block of table rows
       uint32_t row[2];
       uint32_t at[2];
-      {
-        uint32_t kk[2], lo2[2] = {0u, 0u}, hi2[2] = {rows, rows};
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const uint32_t k = k0 + tid + u * kThreads;
-          kk[u] = k < k0 + nb ? k : k0;
-        }
-        // the row holding candidate kk: the largest r with prefix[r] <= kk
-        // < prefix[r + 1] (two binary searches side by side)
-        while (lo2[0] < hi2[0] || lo2[1] < hi2[1]) {
-#pragma unroll
-          for (int u = 0; u < 2; ++u) {
-            if (lo2[u] < hi2[u]) {
-              const uint32_t mid = (lo2[u] + hi2[u]) / 2;
-              if (ps.prefix[mid + 1] <= kk[u]) lo2[u] = mid + 1; else hi2[u] = mid;
-            }
-          }
-        }
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          row[u] = lo2[u] < rows ? lo2[u] : rows - 1u;
-          at[u] = nb > 0u ? ps.begin[row[u]] + (kk[u] - ps.prefix[row[u]]) : 0u;
-        }
+      for (int u = 0; u < 2; ++u) {
+        const uint32_t k = tid + u * kThreads;
+        const uint32_t kk = k < nb ? k : 0u;
+        const uint32_t r = ps.prow[kk];
+        row[u] = r < rows ? r : rows - 1u;
+        at[u] = nb > 0u ? ps.begin[row[u]] + (k0 + kk - ps.prefix[row[u]]) : 0u;
       }
-      __builtin_amdgcn_sched_barrier(0);
-      // first batch: block 0 of the table rows streams while the rows of z
-      // are copied (the copies are issued at a limited rate)
-      if constexpr (first) load_block(tile, 0);
       __builtin_amdgcn_sched_barrier(0);
       stage_rows_batched<H>(stage, nz, ps.slot_row, p.z_hi);
       __builtin_amdgcn_sched_barrier(0);
@@ -440,15 +448,13 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
 #pragma unroll
       for (int u = 0; u < 2; ++u) tok[u] = p.tokens[at[u]];
       __builtin_amdgcn_sched_barrier(0);
-      if constexpr (first) {
-        // block 0, the rows of z and the ids landed (a wait the compiler
-        // sees, so that it counts the later table loads in order again),
-        // then block 1 (a wave keeps about 32 loads in flight; block 2 is
-        // issued once block 0 is scored)
-        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-        __builtin_amdgcn_sched_barrier(0);
-        load_block(tile, 1);
-      }
+      // every load has landed (block 0, the staged rows, the ids: a wait the
+      // compiler sees, so that it counts the later table loads in order);
+      // first batch: block 1 (it streams while block 0 is scored; block 2 is
+      // issued once block 0 is scored)
+      __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (first) load_block(tile, 1);
       __builtin_amdgcn_sched_barrier(0);
       // buckets: each candidate in its 16-token block's bucket
       uint32_t blk[2];
@@ -459,7 +465,6 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
         blk[u] = (k < k0 + nb && c < kHeadTileTokens) ? c / 16u : kHeadTileBlocks;
         if (k < k0 + nb) {
           ps.ptok[k - k0] = tok[u];
-          ps.prow[k - k0] = static_cast<uint16_t>(row[u]);
           ps.pupper[k - k0] = __builtin_huge_valf();
           if (blk[u] < kHeadTileBlocks) {
             atomicAdd(&ps.bcount[blk[u]], 1u);
@@ -487,58 +492,42 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
           ps.bent[at] = pair_pack(ps.rprefix[r] - s0, tid + u * kThreads, (tok[u] - t0) % 16u, r);
         }
       }
-      if constexpr (!first) wait_vector_memory();  // the staged rows have landed
       __syncthreads();  // buckets and staged rows visible
 
       // (4) this wave's blocks in landing order: token norms (first batch),
-      // the candidates 16 at a time (two accumulators per group, even and
-      // odd steps), the head of panel tile 0 (first batch)
-      // A rows in two halves of the K range (half the registers of a
-      // whole group in flight); every read of a half is issued before its
-      // MFMAs (the scheduler would otherwise sink each read next to its
-      // MFMA and pay the LDS latency per step)
+      // the candidates 16 at a time, the next block's rows (first batch)
+      //
+      // A block's groups run as a software pipeline over two halves of the
+      // K range: while the MFMAs of one half run, the other half's A rows
+      // (the next group's first half, or this group's second) are read from
+      // LDS, and the previous group's epilogue (its candidates' scores out
+      // of the accumulators, bounds, LDS atomics) runs between this group's
+      // halves, after its MFMAs had a whole half to finish.  Reads of a group
+      // past the block's last re-read the last group (no branch around LDS
+      // reads, whose waits the compiler counts in order).
       constexpr int kHalf = (kSteps + 1) / 2;
-      auto score_group = [&](uint32_t q, const half8_t(&b)[kSteps], uint32_t blk_id) {
-        const uint32_t ge = ps.bent[q * 16u + col];
-        const unsigned char* a_src = stage + (ge & 0xFFu) * kSlot + kb * 16u;
-        floatx4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f};
-        floatx4 acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int h0 = 0; h0 < kSteps; h0 += kHalf) {
-          half8_t a[kHalf];
-#pragma unroll
-          for (int s = 0; s < kHalf; ++s) {
-            if (h0 + s < kSteps) a[s] = *reinterpret_cast<const half8_t*>(a_src + (h0 + s) * 64);
-          }
-          __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-          for (int s = 0; s < kHalf; ++s) {
-            if (h0 + s < kSteps) {
-              if (s % 2 == 0) {
-                acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[s], b[h0 + s], acc0, 0, 0, 0);
-              } else {
-                acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[s], b[h0 + s], acc1, 0, 0, 0);
-              }
-            }
-          }
-        }
-        const floatx4 acc = acc0 + acc1;
-        // candidate i = lane (lanes 0..15): D[i][c] sits in lane
-        // 16 (i / 4) + c, element i % 4
-        const uint32_t k = (ge >> 8) & 0x3FFu;
-        const uint32_t c = (ge >> 18) & 15u;
-        const uint32_t r = ge >> 22;
+      struct Pending {
+        floatx4 acc;
+        uint32_t ge;
+        float tnv, f1, f2;
+      };
+      // candidate i = lane (lanes 0..15): D[i][c] sits in lane
+      // 16 (i / 4) + c, element i % 4
+      auto epilogue = [&](const Pending& pd) {
+        const floatx4 acc = pd.acc;
+        const uint32_t k = (pd.ge >> 8) & 0x3FFu;
+        const uint32_t c = (pd.ge >> 18) & 15u;
+        const uint32_t r = pd.ge >> 22;
         const bool mine = lane < 16u && k != kNoPair;
         const int src = lane < 16u ? static_cast<int>(16u * (lane / 4u) + c) : static_cast<int>(lane);
         const float v0 = __shfl(acc[0], src);
         const float v1 = __shfl(acc[1], src);
         const float v2 = __shfl(acc[2], src);
         const float v3 = __shfl(acc[3], src);
-        const float tnv = ps.tn[blk_id * 16u + c];
         if (mine) {
           const uint32_t e = lane % 4u;
           const float gs = e == 0u ? v0 : (e == 1u ? v1 : (e == 2u ? v2 : v3));
-          const float bnd = __builtin_fmaf(tnv, ps.rf1[r], ps.rf2[r]);
+          const float bnd = __builtin_fmaf(pd.tnv, pd.f1, pd.f2);
           const bool ok = __builtin_isfinite(gs) && __builtin_isfinite(bnd) && bnd < 0x1p100f;
           if (ok) {
             atomicMax(&ps.row_lower[r], order_bits(gs - bnd));
@@ -549,11 +538,60 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
           }
         }
       };
+      auto score_block = [&](const half8_t(&b)[kSteps], uint32_t blk_id, uint32_t qa, uint32_t qz) {
+        half8_t a0[kHalf];
+        half8_t a1[kHalf];
+        auto a_src = [&](uint32_t ge) { return stage + (ge & 0xFFu) * kSlot + kb * 16u; };
+        auto read_half = [&](half8_t(&dst)[kHalf], const unsigned char* from, int h0) {
+#pragma unroll
+          for (int s = 0; s < kHalf; ++s) {
+            if (h0 + s < kSteps) dst[s] = *reinterpret_cast<const half8_t*>(from + (h0 + s) * 64);
+          }
+        };
+        auto mfma_half = [&](const half8_t(&a)[kHalf], int h0, floatx4& acc) {
+#pragma unroll
+          for (int s = 0; s < kHalf; ++s) {
+            if (h0 + s < kSteps) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[s], b[h0 + s], acc, 0, 0, 0);
+          }
+        };
+        uint32_t ge = ps.bent[qa * 16u + col];
+        const unsigned char* from = a_src(ge);
+        read_half(a0, from, 0);
+        // nothing pending yet: an entry without a candidate
+        Pending pd{{0.0f, 0.0f, 0.0f, 0.0f}, pair_pack(0u, kNoPair, 0u, 0u), 0.0f, 0.0f, 0.0f};
+        for (uint32_t q = qa; q < qz; ++q) {
+          const uint32_t qn = q + 1u < qz ? q + 1u : q;
+          const uint32_t ge_n = ps.bent[qn * 16u + col];
+          const uint32_t c = (ge >> 18) & 15u;
+          const uint32_t r = ge >> 22;
+          const float tnv = ps.tn[blk_id * 16u + c];
+          const float f1 = ps.rf1[r];
+          const float f2 = ps.rf2[r];
+          read_half(a1, from, kHalf);
+          __builtin_amdgcn_sched_barrier(0);
+          floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+          mfma_half(a0, 0, acc);
+          __builtin_amdgcn_sched_barrier(0);
+          epilogue(pd);
+          __builtin_amdgcn_sched_barrier(0);
+          const unsigned char* from_n = a_src(ge_n);
+          read_half(a0, from_n, 0);
+          __builtin_amdgcn_sched_barrier(0);
+          mfma_half(a1, kHalf, acc);
+          __builtin_amdgcn_sched_barrier(0);
+          pd = Pending{acc, ge, tnv, f1, f2};
+          ge = ge_n;
+          from = from_n;
+        }
+        epilogue(pd);
+      };
 #pragma unroll
       for (int tb = 0; tb < kBlocks; ++tb) {
         const uint32_t blk_id = wave * kBlocks + tb;
         if constexpr (first) {
           // Gram diagonal: token norm bounds of the block (this wave's own)
+          // (one chain: a dependent MFMA on the same accumulator issues
+          // back to back)
           h.gram[tb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
           for (int s = 0; s < kSteps; ++s) {
@@ -567,11 +605,7 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
         }
         const uint32_t qa = __builtin_amdgcn_readfirstlane(ps.bstart[blk_id] / 16u);
         const uint32_t qz = __builtin_amdgcn_readfirstlane(ps.bstart[blk_id + 1] / 16u);
-        // one group at a time: its LDS reads complete in order, so each
-        // MFMA waits only for its own operand
-        for (uint32_t q = qa; q < qz; ++q) {
-          score_group(q, bt[tb], blk_id);
-        }
+        if (qa < qz) score_block(bt[tb], blk_id, qa, qz);
         if constexpr (first) {
           if (tb == 0) {
             __builtin_amdgcn_sched_barrier(0);
