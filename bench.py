@@ -135,11 +135,48 @@ def time_loop(tail, stages, steps, warmup, copies):
                             for k, v in per_stage.items()}
 
 
+def back_to_back_ms(s, launch, launches: int) -> float:
+    """Average ms of one launch among `launches` back-to-back launches on
+    stream `s`, between two HIP events.  The launches are captured once into
+    a HIP graph and the graph replayed, so that the host's per-call cost
+    (a ctypes call per launch, more than a 10 us kernel) does not starve the
+    GPU between launches; if capture is refused, an eager loop."""
+    import torch
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    per = min(launches, 64)
+    try:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            for i in range(per):
+                launch(i)
+        reps = max(1, (launches + per - 1) // per)
+        with torch.cuda.stream(s):  # a replay runs on the current stream
+            g.replay()
+            torch.cuda.synchronize()
+            start.record(s)
+            for _ in range(reps):
+                g.replay()
+            stop.record(s)
+        torch.cuda.synchronize()
+        ms = start.elapsed_time(stop) / (reps * per)
+        del g
+        return ms
+    except RuntimeError:
+        torch.cuda.synchronize()
+    start.record(s)
+    for i in range(launches):
+        launch(i)
+    stop.record(s)
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / launches
+
+
 def kernel_loop(tail, stage, launches, copies):
-    """Average duration of one stage's kernel: `launches` back-to-back launches
-    (rotating table copies) between two HIP events on the launch stream.  The
-    stage must be idempotent given the prepare stage's outputs (both heads
-    are: they read the normalized rows and write tile records)."""
+    """Average duration of one stage's kernel: back-to-back launches (rotating
+    table copies) on the launch stream.  The stage must be idempotent given
+    the prepare stage's outputs (both heads are: they read the normalized
+    rows and write tile records)."""
     import torch
     from market_sim_amd import abi, ops
     fns = {"prepare": ops.decode_tail_prepare, "restricted": ops.decode_tail_restricted,
@@ -150,29 +187,63 @@ def kernel_loop(tail, stage, launches, copies):
     abi.check("prepare", ops.decode_tail_prepare(args[0], h))
     for i in range(10):
         abi.check(stage, fns[stage](args[i % copies], h))
-    start = torch.cuda.Event(enable_timing=True)
-    stop = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    start.record(s)
-    for i in range(launches):
-        abi.check(stage, fns[stage](args[i % copies], h))
-    stop.record(s)
-    torch.cuda.synchronize()
-    return start.elapsed_time(stop) / launches
+    return back_to_back_ms(s, lambda i: abi.check(stage, fns[stage](args[i % copies], h)), launches)
 
 
-def profiled_traffic(kernel: str):
-    """HBM-side bytes per launch of `kernel` from the committed rocprofv3 PMC
-    summary (FETCH_SIZE and WRITE_SIZE passes scaled by a copy kernel of known
-    size); None when the summary is absent."""
-    path = os.path.join(ROOT, "profiles", "decode_tail_cfg3_traffic.md")
+def profiled_traffic(kernel: str, workload: str):
+    """HBM-side bytes per launch of `kernel` on `workload` from that
+    workload's committed rocprofv3 PMC summary (FETCH_SIZE and WRITE_SIZE
+    passes scaled by a copy kernel of known size).  Returns (bytes, path of
+    the summary), or (None, None) when no summary of this workload names the
+    kernel."""
+    rel = os.path.join("profiles", f"decode_tail_{workload}_traffic.md")
     try:
-        for line in open(path):
+        for line in open(os.path.join(ROOT, rel)):
             if line.startswith("traffic_bytes_per_launch") and kernel in line:
-                return int(line.split("=", 1)[1].split()[0])
+                return int(line.split("=", 1)[1].split()[0]), rel
     except OSError:
         pass
-    return None
+    return None, None
+
+
+def fallback_summary(alg: dict, fb_ms) -> dict:
+    """The MFMA head's line on the gather path: its rows, launch time and
+    roofline fractions; only when there are unrestricted rows (with none, the
+    unrestricted stage launches nothing and a fraction would divide the head's
+    bytes by an empty launch)."""
+    if alg["B_u"] == 0 or fb_ms is None:
+        return {"kernel": "none (no unrestricted rows)", "rows": 0}
+    return {"kernel": "vocab_head_kernel (MFMA head, unrestricted rows)", "rows": alg["B_u"],
+            "avg_launch_us": round(fb_ms * 1e3, 2),
+            "hbm_GBs": round(alg["fallback_bytes"] / (fb_ms * 1e-3) / 1e9, 1),
+            "hbm_frac": round(alg["fallback_bytes"] / (fb_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "mfma_TFLOPs": round(alg["fallback_flops"] / (fb_ms * 1e-3) / 1e12, 2),
+            "mfma_util": round(alg["fallback_flops"] / (fb_ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)}
+
+
+def read_floor(tail, launches: int, copies: int) -> dict:
+    """The same run's read floor: mf_read_floor over the rotated table copies
+    (every byte once, 16-byte loads, contiguous chunks), `launches` back to
+    back on the tail's stream."""
+    import torch
+    from market_sim_amd import abi, ops
+    bufs = [ops.DeviceBuffer.of(t) for t in tail.tables[:copies]]
+    sink_t = torch.zeros(4, dtype=torch.int32, device=tail.tables[0].device)
+    sink = ops.DeviceBuffer.of(sink_t)
+    s = tail.stream
+    h = s.cuda_stream
+    for i in range(10):
+        abi.check("mf_read_floor", ops.read_floor(bufs[i % len(bufs)], sink, h))
+    torch.cuda.synchronize()
+    ms = back_to_back_ms(
+        s, lambda i: abi.check("mf_read_floor", ops.read_floor(bufs[i % len(bufs)], sink, h)),
+        launches)
+    nbytes = bufs[0].size_bytes
+    return {"kernel": "read_floor_kernel (mf_read_floor: the table, read once)",
+            "bytes": nbytes, "avg_launch_us": round(ms * 1e3, 2),
+            "GBs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
 def cpu_baseline(w, budget_s: float) -> dict:
@@ -302,30 +373,22 @@ def main() -> int:
         main_bytes = alg["gather"]
         main_name = "short_tail_kernel (one kernel: norm, exact scores, selection, DFA advance)"
         achieved = main_bytes / (main_ms * 1e-3) / 1e9
-        traffic = profiled_traffic("short_tail_kernel")
+        traffic, traffic_source = profiled_traffic("short_tail_kernel", w.name)
         fb = {"kernel": "none (no unrestricted rows)", "rows": alg["B_u"]}
     elif one_pass:
         main_bytes, main_name = alg["pass_bytes"], "pass_kernel (one table pass: candidates + unrestricted head)"
         achieved = main_bytes / (main_ms * 1e-3) / 1e9
-        traffic = profiled_traffic("pass_kernel")
+        traffic, traffic_source = profiled_traffic("pass_kernel", w.name)
         fb = {"kernel": "inside pass_kernel (MFMA on the FP16 hi of z)", "rows": alg["B_u"],
               "mfma_TFLOPs": round(alg["pass_flops"] / (main_ms * 1e-3) / 1e12, 2),
               "mfma_util": round(alg["pass_flops"] / (main_ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)}
     else:
         main_bytes, main_name = alg["gather"], "gather_mfma_kernel (CSR gather)"
         achieved = main_bytes / (main_ms * 1e-3) / 1e9
-        traffic = profiled_traffic("gather_mfma_kernel")
-        fb_ms = kernel_loop(tail, "unrestricted", args.steps, args.copies)
-        fb = {"kernel": "vocab_head_kernel (MFMA head, unrestricted rows)", "rows": alg["B_u"],
-              "avg_launch_us": round(fb_ms * 1e3, 2),
-              "hbm_GBs": round(alg["fallback_bytes"] / (fb_ms * 1e-3) / 1e9, 1),
-              "hbm_frac": round(alg["fallback_bytes"] / (fb_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-              "mfma_TFLOPs": round(alg["fallback_flops"] / (fb_ms * 1e-3) / 1e12, 2),
-              "mfma_util": round(alg["fallback_flops"] / (fb_ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)}
-    # the committed counter summary was taken on cfg3 only
-    traffic_source = "profiles/decode_tail_cfg3_traffic.md" if w.name == "cfg3" else None
-    if traffic_source is None:
-        traffic = None
+        traffic, traffic_source = profiled_traffic("gather_mfma_kernel", w.name)
+        fb_ms = kernel_loop(tail, "unrestricted", args.steps, args.copies) if alg["B_u"] > 0 else None
+        fb = fallback_summary(alg, fb_ms)
+    floor = read_floor(tail, args.steps, args.copies)
     result = {
         "metric": METRIC,
         "value": round(w.rows / (total_ms * 1e-3), 1),
@@ -353,9 +416,13 @@ def main() -> int:
         "stages_serial_ms": round(stages_ms, 5),
         "effective_gather_GBs": round(alg["gather_logical"] / (main_ms * 1e-3) / 1e9, 1),
         "fallback": fb,
+        "read_floor": floor,
         "wall_ms_per_step": round(wall_ms, 4),
         "token_checksum": int(np.bitwise_xor.reduce(tok.astype(np.uint64) * np.arange(1, tok.size + 1, dtype=np.uint64))),
     }
+    if one_pass:
+        # the table pass against a plain read of the same table
+        result["roofline"]["vs_read_floor"] = round(floor["avg_launch_us"] / (main_ms * 1e3), 4)
     if one_pass and not args.no_gather_path:
         # the same step on the gather + MFMA head kernels (no sorted-lists
         # declaration), same tokens required
@@ -363,12 +430,15 @@ def main() -> int:
         g_ms, _, _ = time_loop(g, ["tail"], args.steps, args.warmup, args.copies)
         gtok, _, _ = g.results()
         g_gather = kernel_loop(g, "restricted", args.steps, args.copies)
-        g_head = kernel_loop(g, "unrestricted", args.steps, args.copies)
+        g_head = kernel_loop(g, "unrestricted", args.steps, args.copies) if alg["B_u"] > 0 else None
+        head = fallback_summary(alg, g_head)
         result["gather_path"] = {
             "ms_per_step": round(g_ms, 5), "token_parity": bool(np.array_equal(gtok, tok)),
-            "gather_us": round(g_gather * 1e3, 2), "head_us": round(g_head * 1e3, 2),
-            "gather_frac": round(alg["gather"] / (g_gather * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "head_frac": round(alg["fallback_bytes"] / (g_head * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+            "gather_us": round(g_gather * 1e3, 2),
+            "gather_frac": round(alg["gather"] / (g_gather * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        if g_head is not None:
+            result["gather_path"]["head_us"] = head["avg_launch_us"]
+            result["gather_path"]["head_frac"] = head["hbm_frac"]
         del g
     if fused and not args.no_gather_path:
         # the same step on the separate kernels (MF_TAIL_NO_FUSED)

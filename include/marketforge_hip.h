@@ -271,6 +271,12 @@ mf_status mf_decode_tail_workspace_bytes(const mf_decode_tail_args* args,
 mf_status mf_decode_tail_path(const mf_decode_tail_args* args, uint32_t* path);
 /* Zero-fills a workspace with a fill kernel (safe under graph capture). */
 mf_status mf_workspace_init(mf_buffer workspace, uintptr_t stream);
+/* Reads every byte of `data` once (16-byte loads, whole 16-byte words; the
+ * address 16-byte aligned) and writes nothing but, in practice never, one
+ * word of `sink`.  No counterpart in the reference: the read-bandwidth floor
+ * a benchmark times next to a kernel that streams the same bytes (e.g. the
+ * table pass over the embedding). */
+mf_status mf_read_floor(mf_buffer data, mf_buffer sink, uintptr_t stream);
 
 /* The restricted path: CSR gather for restricted rows + MFMA fallback.
  * Equivalent to the four stages below, in order, on one stream. */

@@ -95,6 +95,7 @@ SIGNATURES = {
     "mf_decode_tail_path": (
         Status, [ctypes.POINTER(DecodeTailArgs), ctypes.POINTER(ctypes.c_uint32)]),
     "mf_workspace_init": (Status, [Buffer, _UP]),
+    "mf_read_floor": (Status, [Buffer, Buffer, _UP]),
     "mf_decode_tail_f16": (Status, [ctypes.POINTER(DecodeTailArgs), _UP]),
     "mf_decode_tail_noalloc_max_bytes": (_U64, []),
     "mf_decode_tail_f16_noalloc": (Status, [ctypes.POINTER(DecodeTailArgs), _UP]),

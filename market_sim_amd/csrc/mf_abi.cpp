@@ -905,6 +905,15 @@ mf_status mf_workspace_init(mf_buffer workspace, uintptr_t stream) {
                                             workspace.bytes & ~uint64_t{15u}, native(stream)));
 }
 
+mf_status mf_read_floor(mf_buffer data, mf_buffer sink, uintptr_t stream) {
+  if (data.address == 0 || stream == 0 || (data.address % 16u) != 0 || sink.address == 0 ||
+      sink.bytes < 4u || (sink.address % 4u) != 0) {
+    return status(MF_INVALID_ARGUMENT);
+  }
+  return launch_status(mf::launch_read_floor(ptr<const void>(data.address), data.bytes & ~uint64_t{15u},
+                                             ptr<uint32_t>(sink.address), native(stream)));
+}
+
 mf_status mf_decode_tail_prepare(const mf_decode_tail_args* args, uintptr_t stream) {
   return decode_tail_stage(args, stream, Stage::kPrepare);
 }

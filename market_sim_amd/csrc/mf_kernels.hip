@@ -629,7 +629,38 @@ __global__ __launch_bounds__(kThreads) void fill_zero_kernel(uint4* p, uint64_t 
   }
 }
 
+// Read floor: every 16 bytes of [p, p + 16 n16) read once, kReadBatch
+// loads per thread issued before any is used, each workgroup on one
+// contiguous chunk; the XOR of the words goes to *sink only if it equals a
+// value that never occurs in practice (the loads must not be optimized away).
+constexpr uint32_t kReadBatch = 8;
+__global__ __launch_bounds__(kThreads) void read_floor_kernel(const uint4* p, uint64_t n16,
+                                                              uint32_t* sink) {
+  const uint64_t base = static_cast<uint64_t>(blockIdx.x) * kReadBatch * kThreads + threadIdx.x;
+  uint4 v[kReadBatch];
+#pragma unroll
+  for (uint32_t u = 0; u < kReadBatch; ++u) {
+    const uint64_t q = base + u * kThreads;
+    v[u] = q < n16 ? p[q] : uint4{0u, 0u, 0u, 0u};
+  }
+  uint32_t x = 0u;
+#pragma unroll
+  for (uint32_t u = 0; u < kReadBatch; ++u) x ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+  if (x == 0x9E3779B9u && threadIdx.x == 0) *sink = x;
+}
+
 } // namespace
+
+hipError_t launch_read_floor(const void* address, uint64_t bytes, uint32_t* sink,
+                             hipStream_t stream) {
+  const uint64_t n16 = bytes / 16;
+  if (n16 == 0) return hipSuccess;
+  const uint64_t blocks = (n16 + kReadBatch * kThreads - 1) / (kReadBatch * kThreads);
+  if (blocks > 0xFFFFFFFFull) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(read_floor_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0,
+                     stream, static_cast<const uint4*>(address), n16, sink);
+  return hipGetLastError();
+}
 
 hipError_t launch_rms_norm(const void* input, bool half_input, const void* weight,
                            bool half_weight, void* output, bool half_output,

@@ -66,6 +66,8 @@ hipError_t launch_restricted_greedy(const void* logits, bool half,
 hipError_t launch_token_norms(const uint16_t* emb, uint32_t V, uint32_t H, float* out,
                               hipStream_t stream);
 hipError_t launch_fill_zero(void* address, uint64_t bytes, hipStream_t stream);
+hipError_t launch_read_floor(const void* address, uint64_t bytes, uint32_t* sink,
+                             hipStream_t stream);
 
 // ---- decode tail (mf_tail.hip) ----------------------------------------------
 

@@ -213,6 +213,10 @@ def workspace_init(workspace: DeviceBuffer, stream: int) -> Status:
     return abi.lib().mf_workspace_init(workspace.c(), stream)
 
 
+def read_floor(data: DeviceBuffer, sink: DeviceBuffer, stream: int) -> Status:
+    return abi.lib().mf_read_floor(data.c(), sink.c(), stream)
+
+
 def decode_tail_f16(args: abi.DecodeTailArgs, stream: int) -> Status:
     return abi.lib().mf_decode_tail_f16(ctypes.byref(args), stream)
 
