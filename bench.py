@@ -246,6 +246,36 @@ def read_floor(tail, launches: int, copies: int) -> dict:
             "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
+def vendor_gemm(w, tail, launches: int) -> dict:
+    """For scale beside the full-vocabulary comparator (which scores on this
+    library's own MFMA projection kernel): the vendor FP16 GEMM of the
+    reference's full path (linear.cu:92-102, FP16 inputs and logits) for the
+    same shape, torch.matmul on hipBLASLt, timed back to back."""
+    import torch
+    dev = tail.tables[0].device
+    a = torch.randn(w.rows, w.hidden, device=dev, dtype=torch.float32).to(torch.float16)
+    e = tail.tables[0].view(torch.float16).reshape(w.vocab, w.hidden)
+    out = torch.empty(w.rows, w.vocab, device=dev, dtype=torch.float16)
+    s = tail.stream
+    with torch.cuda.stream(s):
+        for _ in range(5):
+            torch.matmul(a, e.t(), out=out)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    n = max(10, launches // 4)
+    with torch.cuda.stream(s):
+        start.record(s)
+        for _ in range(n):
+            torch.matmul(a, e.t(), out=out)
+        stop.record(s)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(stop) / n
+    return {"op": f"torch.matmul FP16 [{w.rows}x{w.hidden}] x [{w.hidden}x{w.vocab}] -> FP16 logits",
+            "ms": round(ms, 4),
+            "TFLOPs": round(2.0 * w.rows * w.hidden * w.vocab / (ms * 1e-3) / 1e12, 1)}
+
+
 def cpu_baseline(w, budget_s: float) -> dict:
     """The CPU oracle (a plain-C port of the reference loops) on a bounded
     sample of the same pack: whole batches, all host threads, until the time
@@ -456,6 +486,8 @@ def main() -> int:
         result["full_head_ms"] = round(full_ms, 4)
         result["full_head_token_parity"] = bool(np.array_equal(ftok, tok))
         del full
+        result["vendor_gemm"] = vendor_gemm(w, tail, args.steps)
+        result["vs_vendor_gemm"] = round(result["vendor_gemm"]["ms"] / total_ms, 3)
     if not args.no_reference_bench:
         result["reference_bench"] = reference_bench()
     if not args.no_cpu:

@@ -14,7 +14,6 @@
 #include <mutex>
 
 #include <hip/hip_runtime.h>
-#include <rocblas/rocblas.h>
 
 #include "marketforge_hip.h"
 #include "mf_device.hpp"
@@ -142,23 +141,6 @@ uint32_t device_cus() {
   return static_cast<uint32_t>(n);
 }
 
-// rocBLAS handle per device for the full-vocabulary comparator's GEMMs
-// (created on first use, kept for the process).
-hipError_t blas_handle(rocblas_handle& out) {
-  static std::mutex m;
-  static rocblas_handle handles[64] = {};
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) return e;
-  if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
-  std::lock_guard<std::mutex> lock(m);
-  if (handles[dev] == nullptr && rocblas_create_handle(&handles[dev]) != rocblas_status_success) {
-    handles[dev] = nullptr;
-    return hipErrorNotInitialized;
-  }
-  out = handles[dev];
-  return hipSuccess;
-}
 
 uint32_t head_chunk(uint64_t H, uint64_t max_count) {
   uint32_t c = H == 576 ? 128u : 64u;
@@ -1023,36 +1005,23 @@ mf_status mf_decode_tail_full_f16(const mf_decode_tail_args* args, uintptr_t str
   // 1. final RMSNorm (and its FP16 split for the MFMA projection)
   hipError_t e = mf::launch_tail_norm(norm_args(a, L, ws, true, true), s);
   if (e != hipSuccess) return launch_status(e);
-  // 2. full output projection of every row: FP32 scores [rows, V] as two
-  // FP16 GEMMs of the hidden split (hi, then lo accumulated) on rocBLAS --
-  // the library GEMM of the reference's full path (linear.cu:92-102) -- and
-  // the token norm bounds the exact selection needs
+  // 2. full output projection of every row: FP32 scores [rows, V] of the
+  // FP16 hi/lo split of z on the MFMA projection kernel (the hand-written
+  // replacement of the reference's library GEMM, linear.cu:92-102), and the
+  // token norm bounds the exact selection needs
   {
-    rocblas_handle h = nullptr;
-    e = blas_handle(h);
-    if (e != hipSuccess) return runtime_status(e);
-    if (rocblas_set_stream(h, s) != rocblas_status_success) {
-      return status(MF_DEVICE_BACKEND_FAILURE);
-    }
-    // column-major: scores^T [V x rows] = E [V x H] * y16^T [H x rows]
-    const int V = static_cast<int>(a->vocab);
-    const int R = static_cast<int>(a->rows);
-    const int K = static_cast<int>(a->hidden);
-    const float one = 1.0f;
-    const float zero = 0.0f;
-    const void* emb = ptr<const void>(a->embedding.address);
-    const void* parts[2] = {ws + L.y_hi, ws + L.y_lo};
-    for (int i = 0; i < 2; ++i) {
-      const rocblas_status st = rocblas_gemm_ex(
-          h, rocblas_operation_transpose, rocblas_operation_none, V, R, K, &one, emb,
-          rocblas_datatype_f16_r, K, parts[i], rocblas_datatype_f16_r, K, i == 0 ? &zero : &one,
-          scores, rocblas_datatype_f32_r, V, scores, rocblas_datatype_f32_r, V,
-          rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
-      if (st != rocblas_status_success) return status(MF_DEVICE_BACKEND_FAILURE, st);
-    }
-    e = mf::launch_token_norms(ptr<const uint16_t>(a->embedding.address),
-                               static_cast<uint32_t>(a->vocab), static_cast<uint32_t>(a->hidden),
-                               tok_norm, s);
+    mf::ProjArgs pj{};
+    pj.a16 = reinterpret_cast<const uint16_t*>(ws + L.y_hi);
+    pj.a16_lo = reinterpret_cast<const uint16_t*>(ws + L.y_lo);
+    pj.m = static_cast<uint32_t>(a->rows);
+    pj.rows = static_cast<uint32_t>(a->rows);
+    pj.emb = ptr<const uint16_t>(a->embedding.address);
+    pj.H = static_cast<uint32_t>(a->hidden);
+    pj.V = static_cast<uint32_t>(a->vocab);
+    pj.out_f32 = scores;
+    pj.tok_norm = tok_norm;
+    e = mf::launch_projection(pj, s);
+    if (e != hipSuccess) return launch_status(e);
   }
   // 3. restricted selection over the scores (unrestricted rows: every id)
   mf::GatherArgs g = gather_args(a, L, ws);

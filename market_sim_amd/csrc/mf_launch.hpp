@@ -251,6 +251,7 @@ struct ProjArgs {
   // input rows used as they are (a16).
   const float* y;
   const uint16_t* a16;
+  const uint16_t* a16_lo;  // with a16: FP16 lo parts of a split pair (a16 = hi)
   const uint32_t* row_index;
   uint32_t m;          // number of A rows
   uint32_t rows;       // bound of row_index entries (out-of-range rows read as 0)

@@ -213,7 +213,7 @@ __global__ __launch_bounds__(kThreads) void projection_kernel(ProjArgs p) {
   const int wave = threadIdx.x / 64;
   const uint32_t tok0 = blockIdx.x * kTileTokens;
   const uint32_t token = tok0 + wave * 32 + (lane % 32);
-  const AView A{p.y, p.a16, nullptr, p.row_index, p.m, p.rows, p.H};
+  const AView A{p.y, p.a16, p.a16_lo, p.row_index, p.m, p.rows, p.H};
   float tok_sq;
   const floatx16 acc = project_block<kA>(A, p.emb, p.V, m0, tok0, sh, tok_sq);
   if (token >= p.V) return;
@@ -471,7 +471,9 @@ uint32_t fallback_tiles(uint32_t vocab) {
 hipError_t launch_projection(const ProjArgs& args, hipStream_t stream) {
   if (args.H % kKC != 0) return hipErrorInvalidValue;
   const dim3 grid((args.V + kTileTokens - 1) / kTileTokens, (args.m + kMTile - 1) / kMTile);
-  if (args.a16 != nullptr) {
+  if (args.a16 != nullptr && args.a16_lo != nullptr) {
+    hipLaunchKernelGGL((projection_kernel<ASrc::kF16Pair>), grid, dim3(kThreads), 0, stream, args);
+  } else if (args.a16 != nullptr) {
     hipLaunchKernelGGL((projection_kernel<ASrc::kF16>), grid, dim3(kThreads), 0, stream, args);
   } else {
     hipLaunchKernelGGL((projection_kernel<ASrc::kF32Split>), grid, dim3(kThreads), 0, stream, args);

@@ -83,9 +83,12 @@ def test_cfg3_small_vocab_with_unrestricted_rows():
 
 def test_cfg3_full_size_b256():
     """configs[2] at full size: 256 rows, log-uniform [1, 4096], 10% rows
-    unrestricted (MFMA fallback)."""
+    unrestricted (MFMA fallback); also through the full-vocabulary
+    comparator (every row's scores from the MFMA projection kernel)."""
     w = wl.config(3, seed=0)
-    _same(_run(w), _oracle(w, threads=16))
+    exp = _oracle(w, threads=16)
+    _same(_run(w), exp)
+    _same(_run(w, full=True), exp)
 
 
 def test_cfg3_full_size_mul_add_order():
