@@ -253,8 +253,7 @@ static mf_status rms_norm(mf_buffer input, mf_buffer weight, mf_buffer output, u
     return status(MF_INVALID_ARGUMENT);
   }
   if (rows > kIntMax) return status(MF_RESOURCE_LIMIT);
-  // this build stages one row in LDS: hidden <= 16384
-  if (hidden > 16384) return status(MF_RESOURCE_LIMIT);
+  if (hidden > kU32Max) return status(MF_RESOURCE_LIMIT);
   return launch_status(mf::launch_rms_norm(
       ptr<const void>(input.address), half, ptr<const void>(weight.address), half,
       ptr<void>(output.address), half, nullptr, static_cast<uint32_t>(rows),
@@ -384,12 +383,6 @@ mf_status mf_restricted_output_head_f16(mf_buffer hidden, mf_buffer embedding,
       !distinct_valid({hidden.address, embedding.address, allowed_token_ids.address,
                        allowed_token_counts.address, token_ids.address})) {
     return status(MF_INVALID_ARGUMENT);
-  }
-  // limits of this build: one workgroup per row stages the row in LDS and
-  // keeps at most 256 block records
-  if (hidden_size > mf::kHeadMaxHidden ||
-      maximum_allowed_tokens > static_cast<uint64_t>(mf::kHeadChunkMax) * mf::kHeadMaxRecords) {
-    return status(MF_RESOURCE_LIMIT);
   }
   HeadArgs a{};
   a.hidden16 = ptr<const uint16_t>(hidden.address);
@@ -522,7 +515,7 @@ mf_status validate_tail(const mf_decode_tail_args* a, bool full, TailLayout& L) 
   // limits of this build: the hidden row is staged in LDS (H <= 8192), the
   // MFMA heads take K in chunks of 64 features, lists are at most the
   // vocabulary
-  if (a->hidden > mf::kHeadMaxHidden || a->max_count > a->vocab || a->rows > 65535u ||
+  if (a->hidden > mf::kHeadMaxHidden || a->max_count > a->vocab ||
       ((a->unrestricted_count > 0 || full) && (a->hidden % 64u) != 0)) {
     return status(MF_RESOURCE_LIMIT);
   }
@@ -598,6 +591,8 @@ mf_status validate_tail(const mf_decode_tail_args* a, bool full, TailLayout& L) 
     const uint64_t longest = a->max_count == 0 ? 1 : a->max_count;
     L.max_tiles = static_cast<uint32_t>(longest < L.fb_tiles ? longest : L.fb_tiles);
   }
+  // the unplanned gather launches one workgroup per (row, tile)
+  if (rows * L.max_tiles > kU32Max) return status(MF_RESOURCE_LIMIT);
   const uint64_t fb_rows = full ? 0 : a->unrestricted_count;
   L.fb_rows = static_cast<uint32_t>(fb_rows);
   uint64_t off = 0;

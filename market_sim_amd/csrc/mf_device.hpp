@@ -104,12 +104,19 @@ __device__ __forceinline__ float order_step(float s, float h, float e) {
   }
 }
 
+// A hidden row read as FP32 values from FP16 storage in global memory (for
+// rows too wide to stage in LDS); y[f] as for a float pointer.
+struct HalfRow {
+  const uint16_t* h;
+  __device__ __forceinline__ float operator[](uint32_t f) const { return half_to_float(h[f]); }
+};
+
 // Score of one embedding row in a reference order, f = 0..H-1 ascending.
-// y: FP32 hidden (LDS or global); row: FP16 embedding row (global).  When the
-// row is 16-byte aligned and H % 8 == 0 the loads are 16-byte vectors; the
-// arithmetic order is identical either way.
-template <bool kMulAdd>
-__device__ float canonical_dot(const float* y, const uint16_t* row, uint32_t H) {
+// y: FP32 hidden (a float pointer to LDS or global, or a HalfRow); row: FP16
+// embedding row (global).  When the row is 16-byte aligned and H % 8 == 0 the
+// loads are 16-byte vectors; the arithmetic order is identical either way.
+template <bool kMulAdd, typename Y = const float*>
+__device__ float canonical_dot(Y y, const uint16_t* row, uint32_t H) {
   float s = 0.0f;
   uint32_t f = 0;
   if ((reinterpret_cast<uintptr_t>(row) & 15u) == 0 && (H & 7u) == 0) {
@@ -131,11 +138,11 @@ __device__ float canonical_dot(const float* y, const uint16_t* row, uint32_t H) 
   return s;
 }
 
-__device__ __forceinline__ float canonical_dot_order(int order, const float* y,
-                                                     const uint16_t* row,
+template <typename Y = const float*>
+__device__ __forceinline__ float canonical_dot_order(int order, Y y, const uint16_t* row,
                                                      uint32_t H) {
-  return order == 1 ? canonical_dot<true>(y, row, H)
-                    : canonical_dot<false>(y, row, H);
+  return order == 1 ? canonical_dot<true, Y>(y, row, H)
+                    : canonical_dot<false, Y>(y, row, H);
 }
 
 // The reference selection order (greedy.cu:96-100): higher score wins, equal

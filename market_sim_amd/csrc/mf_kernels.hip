@@ -127,6 +127,63 @@ __global__ __launch_bounds__(kWave) void rms_norm_kernel(
   }
 }
 
+// Rows too wide to stage whole in LDS (H > kNormStagedMax): the squares are
+// staged kNormChunk features at a time and lane 0 adds them in feature order
+// (one running sum across the chunks: the same chain as the staged kernel),
+// then y = (x * inverse) * weight with x and the weight read again from
+// global memory.
+constexpr uint32_t kNormStagedMax = 16384;
+constexpr uint32_t kNormChunk = 4096;
+
+template <bool kHalfIn, bool kHalfW, bool kHalfOut>
+__global__ __launch_bounds__(kWave) void rms_norm_wide_kernel(
+    const void* __restrict__ input, const void* __restrict__ weight,
+    void* output, float* __restrict__ row_norm, uint32_t H, float epsilon) {
+  __shared__ float sq[kNormChunk];
+  __shared__ float inverse_shared;
+  const uint64_t r = blockIdx.x;
+  const uint32_t lane = threadIdx.x;
+  auto x_at = [&](uint64_t c) -> float {
+    return kHalfIn ? half_to_float(static_cast<const uint16_t*>(input)[r * H + c])
+                   : static_cast<const float*>(input)[r * H + c];
+  };
+  auto w_at = [&](uint64_t c) -> float {
+    return kHalfW ? half_to_float(static_cast<const uint16_t*>(weight)[c])
+                  : static_cast<const float*>(weight)[c];
+  };
+  float sum = 0.0f;  // lane 0's chain
+  for (uint32_t base = 0; base < H; base += kNormChunk) {
+    const uint32_t n = H - base < kNormChunk ? H - base : kNormChunk;
+    for (uint32_t c = lane; c < n; c += kWave) {
+      const float v = x_at(base + c);
+      sq[c] = v * v;
+    }
+    __syncthreads();
+    if (lane == 0) {
+      for (uint32_t c = 0; c < n; ++c) sum = sum + sq[c];
+    }
+    __syncthreads();
+  }
+  if (lane == 0) inverse_shared = norm_inverse(sum, H, epsilon);
+  __syncthreads();
+  const float inverse = inverse_shared;
+  float norm_sq = 0.0f;
+  for (uint32_t c = lane; c < H; c += kWave) {
+    const float y = (x_at(c) * inverse) * w_at(c);
+    if constexpr (kHalfOut) {
+      static_cast<uint16_t*>(output)[r * H + c] = float_to_half_rne(y);
+    } else {
+      static_cast<float*>(output)[r * H + c] = y;
+      norm_sq = __builtin_fmaf(y, y, norm_sq);
+    }
+  }
+  if (row_norm != nullptr) {
+#pragma unroll
+    for (int m = kWave / 2; m > 0; m >>= 1) norm_sq += __shfl_xor(norm_sq, m);
+    if (lane == 0) row_norm[r] = __fsqrt_rn(norm_sq) * (1.0f + 0x1p-7f);
+  }
+}
+
 // Reference linear_f16 arithmetic on shapes the MFMA tiling does not cover:
 // one output per thread, sequential fma over the input features
 // (tests/cuda/cuda_tests.cu:170-181 order), rounded to FP16.
@@ -319,8 +376,8 @@ __device__ void fast_scores_vec(const HeadArgs& a, const float* ys,
 }
 
 // Fast scores for any H: one wave per candidate, element-strided.
-__device__ void fast_scores_generic(const HeadArgs& a, const float* ys,
-                                    HeadShared& sh, uint32_t n) {
+template <typename Y>
+__device__ void fast_scores_generic(const HeadArgs& a, Y ys, HeadShared& sh, uint32_t n) {
   const int lane = threadIdx.x % kWave;
   const int w = threadIdx.x / kWave;
   for (uint32_t c = w; c < n; c += kWaves) {
@@ -344,8 +401,8 @@ __device__ void fast_scores_generic(const HeadArgs& a, const float* ys,
   }
 }
 
-template <int kH, int kG>
-__device__ void fast_scores(const HeadArgs& a, const float* ys, HeadShared& sh, uint32_t n) {
+template <int kH, int kG, typename Y>
+__device__ void fast_scores(const HeadArgs& a, Y ys, HeadShared& sh, uint32_t n) {
   if constexpr (kH > 0) {
     fast_scores_vec<kH, kG, 2>(a, ys, sh, n);
   } else {
@@ -355,9 +412,9 @@ __device__ void fast_scores(const HeadArgs& a, const float* ys, HeadShared& sh, 
 
 // Summarises one block of n candidates (scores in sh.sc / sh.bd, ids in
 // sh.tk, list positions pos0 + c) into sh.rec.  All threads must call.
-__device__ void summarize_block(const HeadArgs& a, const float* ys,
-                                HeadShared& sh, uint32_t n, uint32_t pos0,
-                                bool invalid) {
+template <typename Y>
+__device__ void summarize_block(const HeadArgs& a, Y ys, HeadShared& sh, uint32_t n,
+                                uint32_t pos0, bool invalid) {
   const int tid = threadIdx.x;
   if (invalid) {
     if (tid == 0) {
@@ -429,9 +486,15 @@ __device__ void summarize_block(const HeadArgs& a, const float* ys,
   __syncthreads();
 }
 
-// Merges n records of one row (in sh.recs) and writes the row's outputs.
-__device__ void finalize_row(const HeadArgs& a, uint32_t r, const RowList& rl,
-                             const float* ys, HeadShared& sh, uint32_t n) {
+// Merges n records of one row (in sh.recs) into one: invalid when any is;
+// otherwise the exact best (reference-order score) of the records whose
+// window reaches the best lower bound L (fast records rescored), or "all
+// NaN" when none has a finite score; the lowest id of all of them rides
+// along.  Merging in stages gives the same record as merging all at once:
+// L never exceeds the row's best exact score, so no stage drops the winner.
+// All threads must call; every thread gets the record.
+template <typename Y>
+__device__ Record merge_records(const HeadArgs& a, Y ys, HeadShared& sh, uint32_t n) {
   const int tid = threadIdx.x;
   uint32_t inv = 0u;
   float lo = -__builtin_huge_valf();
@@ -449,31 +512,38 @@ __device__ void finalize_row(const HeadArgs& a, uint32_t r, const RowList& rl,
   const bool invalid = block_sum(sh, inv) != 0u;
   const float L = block_max(sh, lo);
   block_min_token(sh, mt, mp);
+  const float nan = __builtin_nanf("");
+  if (invalid) return Record{nan, nan, nan, kInvalidToken, 0u, kRecInvalid, mt, mp};
   Best best = best_identity();
-  if (!invalid) {
-    for (uint32_t i = tid; i < n; i += kThreads) {
-      const Record& q = sh.recs[i];
-      if ((q.kind & (kRecFast | kRecExact)) && q.upper >= L) {
-        const float s = (q.kind & kRecExact)
-                            ? q.value
-                            : canonical_dot_order(a.order, ys,
-                                                  a.emb + static_cast<uint64_t>(q.token) * a.H, a.H);
-        best = best_of(best, best_leaf(s, q.token, q.pos));
-      }
+  for (uint32_t i = tid; i < n; i += kThreads) {
+    const Record& q = sh.recs[i];
+    if ((q.kind & (kRecFast | kRecExact)) && q.upper >= L) {
+      const float s = (q.kind & kRecExact)
+                          ? q.value
+                          : canonical_dot_order(a.order, ys,
+                                                a.emb + static_cast<uint64_t>(q.token) * a.H, a.H);
+      best = best_of(best, best_leaf(s, q.token, q.pos));
     }
   }
   best = block_best(sh, best);
-  if (tid == 0) {
+  if (best.token == kInvalidToken) return Record{nan, nan, nan, kInvalidToken, 0u, kRecAllNan, mt, mp};
+  return Record{best.score, best.score, best.score, best.token, best.pos, kRecExact, mt, mp};
+}
+
+// Merges the row's records (sh.recs[0, n)) and writes its outputs.
+template <typename Y>
+__device__ void finalize_row(const HeadArgs& a, uint32_t r, Y ys, HeadShared& sh, uint32_t n) {
+  const Record m = merge_records(a, ys, sh, n);
+  if (threadIdx.x == 0) {
     uint32_t token = kInvalidToken;
     float score = __builtin_nanf("");
-    if (!invalid) {
-      if (best.token == kInvalidToken) {
-        token = mt;
-        score = canonical_dot_order(a.order, ys, a.emb + static_cast<uint64_t>(mt) * a.H, a.H);
-      } else {
-        token = best.token;
-        score = best.score;
-      }
+    if (m.kind & kRecExact) {
+      token = m.token;
+      score = m.value;
+    } else if (m.kind & kRecAllNan) {
+      // every score NaN: the lowest id (greedy.cu:205-207)
+      token = m.min_token;
+      score = canonical_dot_order(a.order, ys, a.emb + static_cast<uint64_t>(m.min_token) * a.H, a.H);
     }
     a.out_token[r] = token;
     if (a.out_score != nullptr) a.out_score[r] = score;
@@ -494,10 +564,14 @@ __device__ bool load_block_ids(const HeadArgs& a, const RowList& rl,
 }
 
 // One workgroup per row: the row's candidates in blocks of a.chunk, each
-// block summarized into a record in LDS, then merged (finalize_row).
-template <int kH, int kG>
+// block summarized into a record in LDS, then merged (finalize_row); when
+// the records fill their LDS array, they are merged into its first entry
+// and the row goes on (lists of any length).  kGlobalHidden: the hidden row
+// is read from global memory in place of an FP32 copy in LDS (rows too wide
+// for LDS).
+template <int kH, int kG, bool kGlobalHidden>
 __global__ __launch_bounds__(kThreads) void head_kernel(HeadArgs a) {
-  extern __shared__ __align__(16) float ys[];
+  extern __shared__ __align__(16) float ys_lds[];
   __shared__ HeadShared sh;
   const uint32_t r = blockIdx.x;
   const RowList rl = resolve_row(a, r);
@@ -508,22 +582,38 @@ __global__ __launch_bounds__(kThreads) void head_kernel(HeadArgs a) {
     }
     return;
   }
-  for (uint32_t f = threadIdx.x; f < a.H; f += kThreads) {
-    ys[f] = half_to_float(a.hidden16[static_cast<uint64_t>(r) * a.H + f]);
-  }
-  __syncthreads();
-  const uint32_t nblocks = (rl.count + a.chunk - 1) / a.chunk;
-  for (uint32_t blk = 0; blk < nblocks; ++blk) {
-    const uint32_t begin = blk * a.chunk;
-    const uint32_t n = rl.count - begin < a.chunk ? rl.count - begin : a.chunk;
-    const bool invalid = load_block_ids(a, rl, sh, begin, n);
-    if (!invalid) fast_scores<kH, kG>(a, ys, sh, n);
+  auto body = [&](auto ys) {
+    const uint32_t nblocks = (rl.count + a.chunk - 1) / a.chunk;
+    uint32_t nrec = 0;
+    for (uint32_t blk = 0; blk < nblocks; ++blk) {
+      const uint32_t begin = blk * a.chunk;
+      const uint32_t n = rl.count - begin < a.chunk ? rl.count - begin : a.chunk;
+      const bool invalid = load_block_ids(a, rl, sh, begin, n);
+      if (!invalid) fast_scores<kH, kG>(a, ys, sh, n);
+      __syncthreads();
+      summarize_block(a, ys, sh, n, begin, invalid);
+      if (threadIdx.x == 0) sh.recs[nrec] = sh.rec;
+      __syncthreads();
+      ++nrec;
+      if (nrec == kHeadMaxRecords && blk + 1 < nblocks) {
+        const Record m = merge_records(a, ys, sh, nrec);
+        __syncthreads();
+        if (threadIdx.x == 0) sh.recs[0] = m;
+        __syncthreads();
+        nrec = 1;
+      }
+    }
+    finalize_row(a, r, ys, sh, nrec);
+  };
+  if constexpr (kGlobalHidden) {
+    body(HalfRow{a.hidden16 + static_cast<uint64_t>(r) * a.H});
+  } else {
+    for (uint32_t f = threadIdx.x; f < a.H; f += kThreads) {
+      ys_lds[f] = half_to_float(a.hidden16[static_cast<uint64_t>(r) * a.H + f]);
+    }
     __syncthreads();
-    summarize_block(a, ys, sh, n, begin, invalid);
-    if (threadIdx.x == 0) sh.recs[blk] = sh.rec;
-    __syncthreads();
+    body(static_cast<const float*>(ys_lds));
   }
-  finalize_row(a, r, rl, ys, sh, nblocks);
 }
 
 // ---------------------------------------------------------------------------
@@ -666,9 +756,22 @@ hipError_t launch_rms_norm(const void* input, bool half_input, const void* weigh
                            bool half_weight, void* output, bool half_output,
                            float* row_norm, uint32_t rows, uint32_t hidden,
                            float epsilon, hipStream_t stream) {
+  const dim3 grid(rows), block(kWave);
+  if (hidden > kNormStagedMax) {
+    if (row_norm != nullptr && hidden > 65536u) return hipErrorInvalidValue;  // bound's margin
+    if (half_input && half_weight && half_output) {
+      hipLaunchKernelGGL((rms_norm_wide_kernel<true, true, true>), grid, block, 0, stream,
+                         input, weight, output, nullptr, hidden, epsilon);
+    } else if (!half_input && !half_weight && !half_output) {
+      hipLaunchKernelGGL((rms_norm_wide_kernel<false, false, false>), grid, block, 0, stream,
+                         input, weight, output, row_norm, hidden, epsilon);
+    } else {
+      return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+  }
   const size_t lds = (hidden <= kNormStagedWeightMax ? 3u : 2u) * static_cast<size_t>(hidden) *
                      sizeof(float);
-  const dim3 grid(rows), block(kWave);
   if (half_input && half_weight && half_output) {
     hipLaunchKernelGGL((rms_norm_kernel<true, true, true>), grid, block, lds, stream,
                        input, weight, output, nullptr, hidden, epsilon);
@@ -685,9 +788,11 @@ hipError_t launch_head(const HeadArgs& args, hipStream_t stream) {
   const bool aligned = (reinterpret_cast<uintptr_t>(args.emb) & 15u) == 0;
   const size_t lds = static_cast<size_t>(args.H) * sizeof(float);
   if (args.H == 576 && aligned) {
-    hipLaunchKernelGGL((head_kernel<576, 8>), dim3(args.rows), dim3(kThreads), lds, stream, args);
+    hipLaunchKernelGGL((head_kernel<576, 8, false>), dim3(args.rows), dim3(kThreads), lds, stream, args);
+  } else if (args.H <= kHeadLdsHidden) {
+    hipLaunchKernelGGL((head_kernel<0, 64, false>), dim3(args.rows), dim3(kThreads), lds, stream, args);
   } else {
-    hipLaunchKernelGGL((head_kernel<0, 64>), dim3(args.rows), dim3(kThreads), lds, stream, args);
+    hipLaunchKernelGGL((head_kernel<0, 64, true>), dim3(args.rows), dim3(kThreads), 0, stream, args);
   }
   return hipGetLastError();
 }

@@ -40,7 +40,11 @@ struct HeadArgs {
 
 constexpr uint32_t kHeadChunkMax = 1024;
 constexpr uint32_t kHeadMaxRecords = 256;
+// decode tail: rows staged in LDS by the norm and finalize kernels
 constexpr uint32_t kHeadMaxHidden = 8192;
+// restricted_output_head: hidden rows up to this width are staged in LDS as
+// FP32; wider ones are read from global memory
+constexpr uint32_t kHeadLdsHidden = 16384;
 
 hipError_t launch_rms_norm(const void* input, bool half_input,
                            const void* weight, bool half_weight, void* output,

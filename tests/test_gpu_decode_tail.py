@@ -327,6 +327,14 @@ def test_decode_tail_equals_its_stages(rows):
     _same(fused, _oracle(w))
 
 
+def test_decode_tail_more_rows_than_16_bits():
+    """A pack of 70,000 rows (past 65,535: the unplanned gather, one
+    workgroup per row and tile), 1% unrestricted, tiny shapes so the oracle
+    finishes in seconds."""
+    w = wl.ragged_pack("rows70k", 31, 512, 64, 70_000, "uniform", 24, 0.01)
+    _same(_run(w), _oracle(w, threads=16))
+
+
 def test_decode_tail_without_norm_weight():
     """norm_weight absent: x is taken as already normalized."""
     w = wl.config(3, seed=22, scale_vocab=6000, scale_rows=48)

@@ -132,6 +132,37 @@ def test_restricted_output_head_matches_reference_fma_chain(hidden, vocab, rows,
     assert _run_head(c).tolist() == expected.tolist()
 
 
+def test_restricted_output_head_wide_hidden_and_long_lists():
+    """Shapes past the LDS staging of the hidden row (H > 16384: read from
+    global memory) and past one LDS array of block records (more than
+    256 x 1024 candidates: the records are merged in stages); the reference
+    runs both (greedy.cu:355-399 caps only at 32-bit sizes)."""
+    rng = np.random.default_rng(23)
+    # wide hidden: 16448 features, a few hundred candidates per row
+    hidden, vocab, rows, max_allowed = 16448, 700, 3, 400
+    h = rng.standard_normal((rows, hidden)).astype(np.float16).view(np.uint16)
+    e = (rng.standard_normal((vocab, hidden)) * 0.02).astype(np.float16).view(np.uint16)
+    allowed = np.zeros((rows, max_allowed), np.uint32)
+    counts = np.array([400, 1, 257], np.uint32)
+    for r in range(rows):
+        allowed[r, :counts[r]] = rng.choice(vocab, counts[r], replace=False)
+    c = dict(hidden=h, embedding=e, allowed=allowed, counts=counts, rows=rows,
+             hidden_size=hidden, vocab=vocab, max_allowed=max_allowed)
+    expected, _ = oracle.restricted_output_head_f16(h, e, allowed, counts, max_allowed)
+    assert _run_head(c).tolist() == expected.tolist()
+    # long lists: 300,000 candidates (ids repeat) over a small vocabulary,
+    # one row with the best id near the end of its list
+    hidden, vocab, rows, max_allowed = 64, 4096, 2, 300_000
+    h = rng.standard_normal((rows, hidden)).astype(np.float16).view(np.uint16)
+    e = (rng.standard_normal((vocab, hidden)) * 0.02).astype(np.float16).view(np.uint16)
+    allowed = rng.integers(0, vocab, (rows, max_allowed)).astype(np.uint32)
+    counts = np.array([max_allowed, 270_001], np.uint32)
+    c = dict(hidden=h, embedding=e, allowed=allowed, counts=counts, rows=rows,
+             hidden_size=hidden, vocab=vocab, max_allowed=max_allowed)
+    expected, _ = oracle.restricted_output_head_f16(h, e, allowed, counts, max_allowed)
+    assert _run_head(c).tolist() == expected.tolist()
+
+
 def test_restricted_output_head_near_ties_are_exact():
     """Candidates whose scores differ only in the last bits: embedding rows
     that are permutations of one another give equal exact sums, so only the
@@ -177,6 +208,28 @@ def test_rms_norm_f32_random_bit_exact():
         ok(ops.rms_norm_f32(B(xd), B(wd), B(out), 9, hidden, 1e-5, stream()))
         got = host(out, np.float32).reshape(9, hidden)
         assert np.array_equal(got, oracle.rms_norm_f32(x, w, 1e-5))
+
+
+def test_rms_norm_wide_rows_bit_exact():
+    """Rows wider than the LDS staging (H > 16384): the squares are staged in
+    chunks with one feature-order chain; the reference has no width limit."""
+    from market_sim_amd import ops
+    rng = np.random.default_rng(5)
+    for hidden in (16385, 40000):
+        x = (rng.standard_normal((3, hidden)) * 2).astype(np.float32)
+        w = (1 + 0.02 * rng.standard_normal(hidden)).astype(np.float32)
+        out = empty(3 * hidden, np.float32)
+        xd, wd = dev(x), dev(w)
+        ok(ops.rms_norm_f32(B(xd), B(wd), B(out), 3, hidden, 1e-5, stream()))
+        got = host(out, np.float32).reshape(3, hidden)
+        assert np.array_equal(got.view(np.uint32), oracle.rms_norm_f32(x, w, 1e-5).view(np.uint32))
+        x16 = x.astype(np.float16).view(np.uint16)
+        w16 = w.astype(np.float16).view(np.uint16)
+        out16 = empty(3 * hidden, np.uint16)
+        xd16, wd16 = dev(x16), dev(w16)
+        ok(ops.rms_norm_f16(B(xd16), B(wd16), B(out16), 3, hidden, 1e-5, stream()))
+        got16 = host(out16, np.uint16).reshape(3, hidden)
+        assert np.array_equal(got16, oracle.rms_norm_f16(x16, w16, 1e-5))
 
 
 def test_rms_norm_f16_bit_exact():
