@@ -81,6 +81,39 @@ __device__ __forceinline__ void head_slots(const FallbackArgs& f, uint32_t m0,
   }
 }
 
+// head_slots in two halves, for a caller that issues the loads early and
+// stores the slots once they have landed: a thread's slot (threads below
+// kPanelRows), loaded from clamped positions without a branch.  With no
+// slots (m == 0) the loads read entry 0 of `dummy`, a valid array of at
+// least one word the caller names.
+struct HeadSlotLoad {
+  uint32_t row;
+  float norm;
+  float slack;
+};
+__device__ __forceinline__ HeadSlotLoad head_slot_load(const FallbackArgs& f, uint32_t m0,
+                                                       const float* dummy) {
+  const uint32_t t = threadIdx.x < kPanelRows ? threadIdx.x : 0u;
+  const uint32_t i = m0 + t;
+  const uint32_t at = f.m == 0u ? 0u : (i < f.m ? i : f.m - 1u);
+  const uint32_t* rows = f.m > 0u ? f.slot_row : reinterpret_cast<const uint32_t*>(dummy);
+  const float* norms = f.m > 0u ? f.slot_norm : dummy;
+  const float* slacks = f.m > 0u ? f.slot_slack : dummy;
+  return HeadSlotLoad{rows[at], norms[at], slacks[at]};
+}
+__device__ __forceinline__ void head_slot_store(const FallbackArgs& f, uint32_t m0,
+                                                const HeadSlotLoad& v, uint32_t* src_row,
+                                                float* src_norm, float* src_slack) {
+  if (threadIdx.x < kPanelRows) {
+    const uint32_t i = m0 + threadIdx.x;
+    const uint32_t r = i < f.m ? v.row : kInvalidToken;
+    src_row[threadIdx.x] = r;
+    src_norm[threadIdx.x] = r != kInvalidToken ? v.norm : 0.0f;
+    src_slack[threadIdx.x] = r != kInvalidToken ? v.slack : 0.0f;
+    if (blockIdx.x == 0 && r != kInvalidToken && f.fb_map != nullptr) f.fb_map[r] = i;
+  }
+}
+
 // 8-lane max (lanes 8 s .. 8 s + 7): quad_perm xor 1 and xor 2, then the
 // mirror inside the half row.  v_max_f32 with the DPP operand directly (the
 // compiler's form adds a canonicalizing max per step); s_nop 1 is the

@@ -249,9 +249,12 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
   };
   // The head's A operand: a panel tile's hi rows staged in LDS (slot j in
   // LDS slot j); its MFMAs against every block of the tile
+  // (only the tile's real rows; the A rows of the others read whatever the
+  // LDS holds, and their scores are never used)
   auto stage_panel = [&](uint32_t pt) {
     const uint16_t* base = f.panel + static_cast<uint64_t>(pt) * kTileHalves;
-    stage_rows<H>(panel, kPanelRows, [&](uint32_t j) { return base + j * kPanelSlotHalves; });
+    const uint32_t n = f.m - pt * kPanelRows < kPanelRows ? f.m - pt * kPanelRows : kPanelRows;
+    stage_rows<H>(panel, n, [&](uint32_t j) { return base + j * kPanelSlotHalves; });
   };
   auto head_lds = [&](HeadAcc<kBlocks>& h) {
 #pragma unroll
@@ -302,6 +305,8 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
     const uint4 ix = p.range_index[static_cast<uint64_t>(tile) * rows + ri];
     const float norm_r = p.row_norm[ri];
     const float slack_r = p.row_slack[ri];
+    // panel tile 0's slots (stored once the plan has landed)
+    const HeadSlotLoad slot0 = head_slot_load(f, 0u, p.row_norm);
     __builtin_amdgcn_sched_barrier(0);
     {
       // Warm this XCD's L2 with the rows of z and the head's panel, which
@@ -375,6 +380,7 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
         ps.prefix[tid] = bn;
         ps.rprefix[tid] = bh;
       }
+      head_slot_store(f, 0u, slot0, src_row, src_norm, src_slack);
       if (tid == kThreads - 1 && rows == kPassRowsMax) {
         ps.prefix[rows] = bn + n;
         ps.rprefix[rows] = bh + has;
@@ -673,8 +679,10 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
     // (6) the unrestricted rows: the head against each panel tile's hi rows
     // (panel tile 0 was staged by the last batch) and its records
     for (uint32_t pt = 0; pt < panels; ++pt) {
-      if (pt > 0u) stage_panel(pt);  // the previous tile's readers are done
-      head_slots(f, pt * kPanelRows, src_row, src_norm, src_slack);
+      if (pt > 0u) {
+        stage_panel(pt);  // the previous tile's readers are done
+        head_slots(f, pt * kPanelRows, src_row, src_norm, src_slack);
+      }
       wait_vector_memory();
       __syncthreads();
       head_lds(h);
