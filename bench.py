@@ -64,7 +64,11 @@ def algorithmic_bytes(w) -> dict:
     pass     2 H T + 4 N + 4 H B + 4 (B_r + 1) + 12 B with T = V when there
              are unrestricted rows (the table is read once for both kinds of
              rows), else U; flops 2 (B_u H V + N H) (candidates and the
-             unrestricted rows' head, FP16 hi of z)."""
+             unrestricted rows' head, FP16 hi of z)
+    dense    2 V H + 2 H S with S = B_u + D slots (D: the lists the dense
+             head takes, at least max(64, V / 256) ids, when they hold 2 V
+             ids in all or B_u > 0); flops 2 S H V; the gather then moves the
+             other restricted rows' bytes (gather_rest)."""
     H, V = w.hidden, w.vocab
     counts = w.row_counts()
     restricted = w.row_state < w.states
@@ -76,7 +80,20 @@ def algorithmic_bytes(w) -> dict:
     logical = 2 * H * N + 4 * N + 4 * H * B_r + 4 * (B_r + 1) + 12 * B_r
     B = w.rows
     T = V if B_u > 0 else U
+    dense_min = max(64, V // 256)
+    cand = restricted & (counts >= dense_min)
+    on = bool(cand.any()) and (B_u > 0 or int(counts[cand].sum()) >= 2 * V)
+    dense_rows = cand if on else np.zeros_like(cand)
+    D = int(dense_rows.sum())
+    S = B_u + D
+    rest = restricted & ~dense_rows
+    N_rest = int(counts[rest].sum())
+    U_rest = w.distinct_restricted_ids(rest)
+    B_rest = int(rest.sum())
+    gather_rest = 2 * H * U_rest + 4 * N_rest + 4 * H * B_rest + 4 * (B_rest + 1) + 12 * B_rest
     return dict(gather=gather, gather_logical=logical, N=N, U=U, B_r=B_r, B_u=B_u,
+                D=D, dense_bytes=2 * V * H + 2 * H * S, dense_flops=2 * S * H * V,
+                gather_rest=gather_rest, B_rest=B_rest,
                 fallback_bytes=2 * V * H + 4 * H * B_u + 8 * B_u,
                 fallback_flops=2 * B_u * H * V,
                 pass_bytes=2 * H * T + 4 * N + 4 * H * B + 4 * (B_r + 1) + 12 * B,
@@ -396,8 +413,25 @@ def main() -> int:
     # the CSR gather
     one_pass = tail.table_pass
     fused = tail.fused
-    main_ms = kernel_loop(tail, "prepare" if fused else "restricted", args.steps, args.copies)
-    if fused:
+    dense = tail.dense
+    main_ms = kernel_loop(tail, "prepare" if fused else ("unrestricted" if dense else "restricted"),
+                          args.steps, args.copies)
+    if dense:
+        # the dense head (unrestricted rows and long ascending lists, one pass
+        # over the table) dominates; the gather takes the other rows
+        main_bytes = alg["dense_bytes"]
+        main_name = "dense_kernel (dense head: unrestricted rows + long ascending lists)"
+        achieved = main_bytes / (main_ms * 1e-3) / 1e9
+        traffic, traffic_source = profiled_traffic("dense_kernel", w.name)
+        rest_ms = kernel_loop(tail, "restricted", args.steps, args.copies)
+        fb = {"kernel": "inside dense_kernel (MFMA on the FP16 hi of z)",
+              "rows": alg["B_u"], "dense_list_rows": alg["D"],
+              "mfma_TFLOPs": round(alg["dense_flops"] / (main_ms * 1e-3) / 1e12, 2),
+              "mfma_util": round(alg["dense_flops"] / (main_ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+              "gather_rest": {"kernel": "gather_mfma_kernel (the other restricted rows)",
+                              "rows": alg["B_rest"], "avg_launch_us": round(rest_ms * 1e3, 2),
+                              "hbm_frac": round(alg["gather_rest"] / (rest_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}}
+    elif fused:
         # the same bytes as the gather: each distinct candidate row, the ids,
         # the hidden rows, the offsets and the outputs
         main_bytes = alg["gather"]
@@ -469,6 +503,22 @@ def main() -> int:
         if g_head is not None:
             result["gather_path"]["head_us"] = head["avg_launch_us"]
             result["gather_path"]["head_frac"] = head["hbm_frac"]
+        del g
+    if dense and not args.no_gather_path:
+        # the same step with every restricted row on the gather and the MFMA
+        # head for the unrestricted rows (MF_TAIL_NO_DENSE), same tokens
+        # required
+        g = DeviceTail(w, copies=args.copies, dense=False)
+        g_ms, _, _ = time_loop(g, ["tail"], args.steps, args.warmup, args.copies)
+        gtok, _, _ = g.results()
+        g_gather = kernel_loop(g, "restricted", args.steps, args.copies)
+        g_head = kernel_loop(g, "unrestricted", args.steps, args.copies) if alg["B_u"] > 0 else None
+        result["gather_path"] = {
+            "ms_per_step": round(g_ms, 5), "token_parity": bool(np.array_equal(gtok, tok)),
+            "gather_us": round(g_gather * 1e3, 2),
+            "gather_frac": round(alg["gather"] / (g_gather * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        if g_head is not None:
+            result["gather_path"]["head_us"] = round(g_head * 1e3, 2)
         del g
     if fused and not args.no_gather_path:
         # the same step on the separate kernels (MF_TAIL_NO_FUSED)

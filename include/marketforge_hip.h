@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define MF_ABI_VERSION 5u
+#define MF_ABI_VERSION 6u
 
 /* Status: include/marketforge/core/status.hpp:7-49.  The numeric codes equal
  * the reference ErrorCode enumerators so results stay schema-compatible. */
@@ -211,6 +211,16 @@ mf_status mf_linear_f16(mf_buffer input, mf_buffer weight, mf_buffer output,
  * without the flags; a list that turns out not to be ascending is rescored
  * in full, exactly.  MF_TAIL_TABLE_PASS alone changes nothing.
  *
+ * Dense head: otherwise, with MF_TAIL_SORTED_LISTS, hidden % 32 == 0,
+ * hidden >= 1024 and rows + unrestricted_count within the launch's panels
+ * (256 slots per 8 compute units: 8192 on MI355X), the unrestricted stage
+ * runs one pass over the table that scores the unrestricted rows and the
+ * long ascending lists (at least vocab / 256 and 64 ids) with MFMA against
+ * every token, keeping only the allowed ones; the gather skips those rows.
+ * The device takes the long lists when they hold at least 2 vocab ids in
+ * all, or whenever the call has unrestricted rows.  MF_TAIL_NO_DENSE keeps
+ * every restricted row on the gather.  The results are the same.
+ *
  * Short lists: a call with no unrestricted rows, max_count <= 128,
  * hidden % 8 == 0 and max_count within two rounds of one workgroup's LDS
  * stage of candidate rows (one round at hidden <= 576) runs as
@@ -248,13 +258,14 @@ typedef struct mf_decode_tail_args {
   uint64_t unrestricted_count;
   mf_buffer row_sequence;      /* u32 [rows] or address 0: see "Sequence table" */
   uint64_t flags;              /* MF_TAIL_HOLD_FINISHED | MF_TAIL_SORTED_LISTS | MF_TAIL_TABLE_PASS
-                                  | MF_TAIL_NO_FUSED */
+                                  | MF_TAIL_NO_FUSED | MF_TAIL_NO_DENSE */
 } mf_decode_tail_args;
 
 #define MF_TAIL_HOLD_FINISHED 1u
 #define MF_TAIL_SORTED_LISTS 2u
 #define MF_TAIL_TABLE_PASS 4u
 #define MF_TAIL_NO_FUSED 8u
+#define MF_TAIL_NO_DENSE 16u
 
 mf_status mf_decode_tail_workspace_bytes(const mf_decode_tail_args* args,
                                          uint64_t* bytes);
@@ -264,10 +275,13 @@ mf_status mf_decode_tail_workspace_bytes(const mf_decode_tail_args* args,
  * MF_TAIL_PATH_GATHER (restricted stage = CSR gather, unrestricted stage =
  * MFMA head) or MF_TAIL_PATH_TABLE_PASS (restricted stage = one pass over
  * the table for both kinds of rows, unrestricted stage empty) or
- * MF_TAIL_PATH_FUSED (the whole tail in the prepare stage's one kernel). */
+ * MF_TAIL_PATH_FUSED (the whole tail in the prepare stage's one kernel) or
+ * MF_TAIL_PATH_DENSE (restricted stage = CSR gather of the rows the dense
+ * head leaves, unrestricted stage = the dense head). */
 #define MF_TAIL_PATH_GATHER 0u
 #define MF_TAIL_PATH_TABLE_PASS 1u
 #define MF_TAIL_PATH_FUSED 2u
+#define MF_TAIL_PATH_DENSE 3u
 mf_status mf_decode_tail_path(const mf_decode_tail_args* args, uint32_t* path);
 /* Zero-fills a workspace with a fill kernel (safe under graph capture). */
 mf_status mf_workspace_init(mf_buffer workspace, uintptr_t stream);

@@ -33,10 +33,12 @@ TAIL_HOLD_FINISHED = 1
 TAIL_SORTED_LISTS = 2
 TAIL_TABLE_PASS = 4
 TAIL_NO_FUSED = 8
+TAIL_NO_DENSE = 16
 TAIL_PATH_GATHER = 0
 TAIL_PATH_TABLE_PASS = 1
 TAIL_PATH_FUSED = 2
-ABI_VERSION = 5
+TAIL_PATH_DENSE = 3
+ABI_VERSION = 6
 
 _U64 = ctypes.c_uint64
 _UP = ctypes.c_size_t  # uintptr_t

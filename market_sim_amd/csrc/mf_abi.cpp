@@ -460,10 +460,11 @@ constexpr uint32_t kFullTile = 256;  // selection over projected scores
 struct TailLayout {
   uint64_t y, row_inv, row_norm, row_slack, row_meta, y_hi, y_lo, fb_map, records, fb_records,
       fb_panel, fb_slot_row, fb_slot_norm, fb_slot_slack, scores, tok_norm, range_index,
-      row_tiles, total;
+      row_tiles, dense_spans, dense_flag, total;
   uint32_t tile, max_tiles, fb_tiles, fb_rows;
   bool pass;   // the table pass serves both kinds of rows
   bool fused;  // the one-kernel tail (short lists)
+  bool dense;  // the dense head serves unrestricted rows and long ascending lists
 };
 
 bool buffer_is(const mf_buffer& b, uint64_t bytes) { return b.address != 0 && b.bytes == bytes; }
@@ -500,6 +501,30 @@ bool fused_tail(const mf_decode_tail_args* a) {
   return stage > 0 && 2u * static_cast<uint64_t>(stage) >= a->max_count;
 }
 
+// The dense head (mf_dense.hip): lists declared ascending, a hidden size of
+// whole 32-feature steps wide enough that gathering a long list costs more
+// than scoring its row against every token, and every row fitting the
+// launch's panels (the compute units of each XCD, 256 slots each).  Which
+// rows it takes is decided on the device (dense_min_ids, dense_total_ids).
+constexpr uint64_t kDenseMinHidden = 1024;
+bool dense_head(const mf_decode_tail_args* a) {
+  if (!(a->flags & MF_TAIL_SORTED_LISTS) || (a->flags & MF_TAIL_NO_DENSE) ||
+      a->hidden % 32u != 0 || a->hidden < kDenseMinHidden) {
+    return false;
+  }
+  const uint64_t panels = device_cus() / 8u;
+  return a->rows + a->unrestricted_count <= panels * mf::kDensePanelSlots;
+}
+// A list the dense head may take: at least 1/256 of the vocabulary (and 64
+// ids); the head runs when those lists hold at least twice the vocabulary's
+// ids in all (their gather would read the table twice over), or whenever
+// unrestricted rows make it read the table anyway.
+uint32_t dense_min_ids(uint64_t vocab) {
+  const uint64_t m = vocab / 256u;
+  return static_cast<uint32_t>(m > 64u ? m : 64u);
+}
+uint64_t dense_total_ids(uint64_t vocab) { return 2u * vocab; }
+
 // Validation common to both decode-tail entry points; fills the layout.
 mf_status validate_tail(const mf_decode_tail_args* a, bool full, TailLayout& L) {
   if (a == nullptr) return status(MF_INVALID_ARGUMENT);
@@ -529,7 +554,8 @@ mf_status validate_tail(const mf_decode_tail_args* a, bool full, TailLayout& L) 
   // capacity that row_sequence indexes
   const bool table = a->row_sequence.address != 0;
   if ((a->flags & ~static_cast<uint64_t>(MF_TAIL_HOLD_FINISHED | MF_TAIL_SORTED_LISTS |
-                                         MF_TAIL_TABLE_PASS | MF_TAIL_NO_FUSED)) != 0) {
+                                         MF_TAIL_TABLE_PASS | MF_TAIL_NO_FUSED |
+                                         MF_TAIL_NO_DENSE)) != 0) {
     return status(MF_INVALID_ARGUMENT);
   }
   if (table && (a->row_state.bytes / 4u > kU32Max || a->row_state.bytes == 0 ||
@@ -587,6 +613,7 @@ mf_status validate_tail(const mf_decode_tail_args* a, bool full, TailLayout& L) 
   // table pass: one record per (row, 192-token range) holding its ids
   L.pass = !full && table_pass(a);
   L.fused = !full && !L.pass && fused_tail(a);
+  L.dense = !full && !L.pass && !L.fused && dense_head(a);
   if (L.pass) {
     const uint64_t longest = a->max_count == 0 ? 1 : a->max_count;
     L.max_tiles = static_cast<uint32_t>(longest < L.fb_tiles ? longest : L.fb_tiles);
@@ -595,6 +622,9 @@ mf_status validate_tail(const mf_decode_tail_args* a, bool full, TailLayout& L) 
   if (rows * L.max_tiles > kU32Max) return status(MF_RESOURCE_LIMIT);
   const uint64_t fb_rows = full ? 0 : a->unrestricted_count;
   L.fb_rows = static_cast<uint32_t>(fb_rows);
+  // the dense head's slots: the unrestricted rows, then any row
+  const uint64_t fb_slots = L.dense ? fb_rows + rows : fb_rows;
+  const uint64_t panel_rows = L.dense ? 0u : fb_rows;
   uint64_t off = 0;
   auto take = [&off](uint64_t bytes) {
     const uint64_t at = off;
@@ -611,16 +641,18 @@ mf_status validate_tail(const mf_decode_tail_args* a, bool full, TailLayout& L) 
   L.y_lo = take(split ? xe * 2u : 0u);
   L.fb_map = take(rows * 4u);
   L.records = take(rows * L.max_tiles * sizeof(mf::TileRecord));
-  L.fb_records = take(fb_rows * L.fb_tiles * sizeof(mf::TileRecord));
-  L.fb_panel = take(mf::panel_tiles(static_cast<uint32_t>(fb_rows)) *
+  L.fb_records = take(fb_slots * L.fb_tiles * sizeof(mf::TileRecord));
+  L.fb_panel = take(mf::panel_tiles(static_cast<uint32_t>(panel_rows)) *
                     mf::panel_tile_bytes(a->hidden));
-  L.fb_slot_row = take(fb_rows * 4u);
-  L.fb_slot_norm = take(fb_rows * 4u);
-  L.fb_slot_slack = take(fb_rows * 4u);
+  L.fb_slot_row = take(panel_rows * 4u);
+  L.fb_slot_norm = take(panel_rows * 4u);
+  L.fb_slot_slack = take(panel_rows * 4u);
   L.scores = take(full ? rows * a->vocab * 4u : 0u);
   L.tok_norm = take(full ? a->vocab * 4u : 0u);
   L.range_index = take(L.pass ? L.fb_tiles * rows * 16u : 0u);
   L.row_tiles = take(L.pass ? rows * 4u : 0u);
+  L.dense_spans = take(L.dense ? static_cast<uint64_t>(L.fb_tiles) * rows * 32u : 0u);
+  L.dense_flag = take(L.dense ? rows * 4u : 0u);
   L.total = off;
   return ok();
 }
@@ -674,7 +706,7 @@ mf::TailNormArgs norm_args(const mf_decode_tail_args* a, const TailLayout& L, ch
   n.row_sequence = ptr<const uint32_t>(a->row_sequence.address);
   n.capacity = static_cast<uint32_t>(n.row_sequence != nullptr ? a->row_state.bytes / 4u : a->rows);
   n.hold = (a->flags & MF_TAIL_HOLD_FINISHED) ? 1u : 0u;
-  if (L.fb_rows > 0) {  // the MFMA head's panel
+  if (L.fb_rows > 0 && !L.dense) {  // the MFMA head's panel
     n.fb_rows = ptr<const uint32_t>(a->unrestricted_rows.address);
     n.fb_m = static_cast<uint32_t>(a->unrestricted_count);
     n.fb_panel = reinterpret_cast<uint16_t*>(ws + L.fb_panel);
@@ -689,6 +721,15 @@ mf::TailNormArgs norm_args(const mf_decode_tail_args* a, const TailLayout& L, ch
     n.ranges = L.fb_tiles;
     n.records = reinterpret_cast<mf::TileRecord*>(ws + L.records);
     n.max_recs = L.max_tiles;
+  }
+  if (L.dense) {  // the dense head's span index and row choice
+    n.tokens = ptr<const uint32_t>(a->state_tokens.address);
+    n.ranges = L.fb_tiles;
+    n.dense_spans = reinterpret_cast<uint4*>(ws + L.dense_spans);
+    n.dense_flag = reinterpret_cast<uint32_t*>(ws + L.dense_flag);
+    n.dense_min = dense_min_ids(a->vocab);
+    n.dense_any = a->unrestricted_count > 0 ? 1u : 0u;
+    n.dense_total = dense_total_ids(a->vocab);
   }
   return n;
 }
@@ -727,7 +768,7 @@ mf::FinalizeArgs finalize_args(const mf_decode_tail_args* a, const TailLayout& L
   f.max_tiles = L.max_tiles;
   f.tile = L.tile;
   f.row_tiles = L.pass ? reinterpret_cast<const uint32_t*>(ws + L.row_tiles) : nullptr;
-  if (!full && a->unrestricted_count > 0) {
+  if (!full && (a->unrestricted_count > 0 || L.dense)) {
     f.fb_records = reinterpret_cast<const mf::TileRecord*>(ws + L.fb_records);
     f.fb_map = reinterpret_cast<const uint32_t*>(ws + L.fb_map);
     f.fb_tiles = L.fb_tiles;
@@ -762,6 +803,27 @@ mf::FallbackArgs fallback_args(const mf_decode_tail_args* a, const TailLayout& L
   mfma_bound_coefs(a->hidden, f.coef, f.coef2);
   f.groups = device_cus();
   return f;
+}
+
+mf::DenseArgs dense_args(const mf_decode_tail_args* a, const TailLayout& L, char* ws) {
+  mf::DenseArgs d{};
+  d.emb = ptr<const uint16_t>(a->embedding.address);
+  d.z_hi = reinterpret_cast<const uint16_t*>(ws + L.y_hi);
+  d.row_norm = reinterpret_cast<const float*>(ws + L.row_norm);
+  d.row_slack = reinterpret_cast<const float*>(ws + L.row_slack);
+  d.row_meta = reinterpret_cast<const mf::RowMeta*>(ws + L.row_meta);
+  d.spans = reinterpret_cast<const uint4*>(ws + L.dense_spans);
+  d.fb_rows = ptr<const uint32_t>(a->unrestricted_rows.address);
+  d.fb_m = static_cast<uint32_t>(a->unrestricted_count);
+  d.rows = static_cast<uint32_t>(a->rows);
+  d.H = static_cast<uint32_t>(a->hidden);
+  d.V = static_cast<uint32_t>(a->vocab);
+  d.ranges = L.fb_tiles;
+  d.records = reinterpret_cast<mf::TileRecord*>(ws + L.fb_records);
+  d.fb_map = reinterpret_cast<uint32_t*>(ws + L.fb_map);
+  pass_bound_coefs(a->hidden, d.coef, d.coef2);
+  d.groups = device_cus() / 8u * 8u;
+  return d;
 }
 
 mf::PassArgs pass_args(const mf_decode_tail_args* a, const TailLayout& L, char* ws) {
@@ -833,6 +895,10 @@ mf_status decode_tail_stage(const mf_decode_tail_args* args, uintptr_t stream, S
       break;
     }
     case Stage::kUnrestricted: {
+      if (L.dense) {
+        e = mf::launch_dense(dense_args(a, L, ws), s);
+        break;
+      }
       if (a->unrestricted_count == 0 || L.pass || L.fused) break;
       e = mf::launch_fallback(fallback_args(a, L, ws), s);
       break;
@@ -861,7 +927,10 @@ mf_status mf_decode_tail_path(const mf_decode_tail_args* args, uint32_t* path) {
   TailLayout L{};
   const mf_status v = validate_tail(args, false, L);
   if (v.code != MF_OK) return v;
-  *path = L.pass ? MF_TAIL_PATH_TABLE_PASS : L.fused ? MF_TAIL_PATH_FUSED : MF_TAIL_PATH_GATHER;
+  *path = L.pass    ? MF_TAIL_PATH_TABLE_PASS
+          : L.fused ? MF_TAIL_PATH_FUSED
+          : L.dense ? MF_TAIL_PATH_DENSE
+                    : MF_TAIL_PATH_GATHER;
   return ok();
 }
 

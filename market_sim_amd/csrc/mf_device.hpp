@@ -386,7 +386,9 @@ __device__ __forceinline__ void wave_sync() {
 }
 
 // Per-row metadata written by the decode-tail norm kernel.
-enum : uint32_t { kRowRestricted = 1u, kRowUnrestricted = 2u, kRowInvalid = 4u };
+// kRowDense (with kRowRestricted): the row's ascending list is scored by the
+// dense head (mf_dense.hip), not by the gather; set by the norm launch.
+enum : uint32_t { kRowRestricted = 1u, kRowUnrestricted = 2u, kRowInvalid = 4u, kRowDense = 8u };
 struct alignas(16) RowMeta {
   uint32_t list_begin;
   uint32_t count;

@@ -177,7 +177,14 @@ __device__ inline void finalize_row(const FinalizeArgs& a, uint32_t r, const Row
   const uint32_t lane = threadIdx.x % kWave;
   const TileRecord* recs;
   uint32_t ntiles;
-  if (meta.kind & kRowRestricted) {
+  if ((meta.kind & kRowDense) && a.fb_records != nullptr) {
+    // scored by the dense head: its records, list positions of the row's
+    // ascending list
+    const uint32_t m = a.fb_map[r];
+    if (m == kInvalidToken) return;
+    recs = a.fb_records + static_cast<uint64_t>(m) * a.fb_tiles;
+    ntiles = a.fb_tiles;
+  } else if (meta.kind & kRowRestricted) {
     recs = a.records + static_cast<uint64_t>(r) * a.max_tiles;
     ntiles = a.row_tiles != nullptr ? (a.row_tiles[r] & ~kRangesUnused)
                                     : (meta.count + a.tile - 1) / a.tile;

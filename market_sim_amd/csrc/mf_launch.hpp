@@ -138,6 +138,20 @@ struct TailNormArgs {
   uint32_t ranges;
   TileRecord* records;     // [rows, max_recs]
   uint32_t max_recs;
+  // Dense index (dense_spans null: none).  Walk workgroup r of the norm
+  // launch indexes row r when its list is restricted, at least dense_min
+  // long, strictly ascending and below V: per 192-token range g,
+  // dense_spans[(g * rows + r) * 2 + {0, 1}] = {m0, m1, m2, lo}, {m3, m4,
+  // m5, cnt} (the range's ids as a 192-bit mask, the list position of its
+  // first id, their count); dense_flag[r] = 1 (else 0).  A one-workgroup
+  // kernel after the launch decides: when the indexed lists hold at least
+  // dense_total ids, or any with dense_any, every indexed row gets
+  // kRowDense in row_meta.
+  uint4* dense_spans;      // [ranges, rows, 2]
+  uint32_t* dense_flag;    // [rows]
+  uint32_t dense_min;
+  uint32_t dense_any;      // 1: the table is read anyway (unrestricted rows)
+  uint64_t dense_total;
 };
 
 // row_tiles flag: the row's ranges are not used (its one record comes from
@@ -317,6 +331,36 @@ struct PassArgs {
 };
 
 hipError_t launch_pass(const PassArgs& args, hipStream_t stream);
+
+// ---- dense head (mf_dense.hip) -------------------------------------------------
+//
+// One launch over the table in 192-token tiles for the unrestricted rows
+// (fb_rows) and the kRowDense rows: slot j < fb_m is fb_rows[j] (when that is
+// an unrestricted row), then the kRowDense rows in row order; slot j's record
+// of tile t is records[j * ranges + t] (the MFMA head's format; list
+// positions for kRowDense rows), and fb_map[row] = j.
+constexpr uint32_t kDensePanelSlots = 256;
+struct DenseArgs {
+  const uint16_t* emb;        // [V, H]
+  const uint16_t* z_hi;       // [rows, H] FP16 hi of z = x * w
+  const float* row_norm;      // [rows]
+  const float* row_slack;     // [rows]
+  const RowMeta* row_meta;    // kinds after the norm launch
+  const uint4* spans;         // the norm launch's dense index
+  const uint32_t* fb_rows;    // [fb_m]
+  uint32_t fb_m;
+  uint32_t rows;
+  uint32_t H;
+  uint32_t V;
+  uint32_t ranges;            // 192-token tiles of the vocabulary
+  TileRecord* records;        // [fb_m + rows, ranges]
+  uint32_t* fb_map;           // [rows]
+  float coef;                 // b = ||e|| (coef ||z|| + coef2) + slack (FP16 hi of z)
+  float coef2;
+  uint32_t groups;            // workgroups: compute units, a multiple of 8 (XCDs)
+};
+// Slots one launch serves: (groups / 8) panels of kDensePanelSlots.
+hipError_t launch_dense(const DenseArgs& args, hipStream_t stream);
 // mf_short.hip: candidate rows one workgroup stages per round (0: H does
 // not fit), and the one-kernel tail
 uint32_t short_stage_rows(uint32_t H, uint32_t max_count);

@@ -21,7 +21,8 @@ struct TilePlan {
 };
 
 __device__ __forceinline__ bool row_gathered(const RowMeta& m, bool lookup) {
-  return (m.kind & kRowRestricted) || (lookup && (m.kind & kRowUnrestricted));
+  return ((m.kind & kRowRestricted) && !(m.kind & kRowDense)) ||
+         (lookup && (m.kind & kRowUnrestricted));
 }
 
 // Fills the plan (all threads call; ends with a barrier) and returns W.

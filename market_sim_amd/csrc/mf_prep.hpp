@@ -410,4 +410,97 @@ __device__ inline void range_end(const TailNormArgs& a, uint32_t r, const RangeR
   }
 }
 
+// ---- dense index (the spans the dense head reads, mf_dense.hip) ------------
+//
+// Walk workgroup r (kWalkWaves waves) indexes row r's list when it is a
+// candidate (restricted, at least dense_min ids): every id sets its bit in
+// the LDS mask of its 192-token range; an id >= V or a list that is not
+// strictly ascending leaves the row to the gather.  Then the ranges' counts
+// are scanned (the list position of each range's first id) and the spans
+// written out, range-major; dense_flag[r] says whether the row was indexed.
+// Which indexed rows the dense head takes is decided after the launch
+// (dense_choose_kernel, mf_tail.hip).  LDS: dense_lds_words(ranges).
+__host__ __device__ constexpr uint32_t dense_lds_words(uint32_t ranges) {
+  return 6u * ranges + 2u * kWalkWaves + 4u;
+}
+
+__device__ inline void dense_walk(const TailNormArgs& a, uint32_t r, uint32_t* lds) {
+  const uint32_t tid = threadIdx.x;
+  const uint32_t lane = tid % kWave;
+  const uint32_t wave = tid / kWave;
+  constexpr uint32_t kT = kWalkWaves * kWave;
+  const uint32_t G = a.ranges;
+  uint32_t* mask = lds;                      // [G][6]
+  uint32_t* wsum = lds + 6u * G;             // [kWalkWaves]
+  uint32_t* flags = wsum + 2u * kWalkWaves;  // [1]
+  const RangeRow w = range_row(a, r);
+  const bool cand = w.indexed && w.c >= a.dense_min;
+  bool ok = false;
+  if (cand) {
+    for (uint32_t i = tid; i < 6u * G; i += kT) mask[i] = 0u;
+    if (tid == 0) *flags = 0u;
+    __syncthreads();
+    const uint32_t b = w.b;
+    const uint32_t c = w.c;
+    bool bad = false;
+    constexpr uint32_t kU = 4;  // loads in flight per thread
+    for (uint32_t base = tid; base < c; base += kT * kU) {
+      uint32_t t[kU], tp[kU];
+#pragma unroll
+      for (uint32_t u = 0; u < kU; ++u) {
+        const uint32_t p = base + u * kT;
+        const uint32_t pc = p < c ? p : c - 1u;
+        t[u] = a.tokens[b + pc];
+        tp[u] = a.tokens[b + (pc > 0u ? pc - 1u : 0u)];
+      }
+#pragma unroll
+      for (uint32_t u = 0; u < kU; ++u) {
+        const uint32_t p = base + u * kT;
+        if (p < c) {
+          bad |= t[u] >= a.V || (p > 0u && t[u] <= tp[u]);
+          if (t[u] < a.V) {
+            const uint32_t g = t[u] / kHeadTileTokens;
+            atomicOr(&mask[g * 6u + (t[u] % kHeadTileTokens) / 32u], 1u << (t[u] % 32u));
+          }
+        }
+      }
+    }
+    if (__ballot(bad) != 0ull && lane == 0) atomicOr(flags, 1u);
+    __syncthreads();
+    ok = *flags == 0u;
+    if (ok) {
+      // exclusive scan of the ranges' counts: thread segments, then waves
+      const uint32_t per = (G + kT - 1u) / kT;
+      const uint32_t g0 = tid * per < G ? tid * per : G;
+      const uint32_t g1 = g0 + per < G ? g0 + per : G;
+      uint32_t local = 0u;
+      for (uint32_t g = g0; g < g1; ++g) {
+#pragma unroll
+        for (uint32_t k = 0; k < 6u; ++k) local += static_cast<uint32_t>(__popc(mask[g * 6u + k]));
+      }
+      uint32_t incl = local;
+#pragma unroll
+      for (int d = 1; d < kWave; d <<= 1) {
+        const uint32_t o = static_cast<uint32_t>(__shfl_up(static_cast<int>(incl), d));
+        if (static_cast<int>(lane) >= d) incl += o;
+      }
+      if (lane == kWave - 1) wsum[wave] = incl;
+      __syncthreads();
+      uint32_t run = incl - local;
+      for (uint32_t v = 0; v < wave; ++v) run += wsum[v];
+      for (uint32_t g = g0; g < g1; ++g) {
+        const uint32_t* m = mask + g * 6u;
+        uint32_t n = 0u;
+#pragma unroll
+        for (uint32_t k = 0; k < 6u; ++k) n += static_cast<uint32_t>(__popc(m[k]));
+        uint4* out = a.dense_spans + (static_cast<uint64_t>(g) * a.rows + r) * 2u;
+        out[0] = uint4{m[0], m[1], m[2], run};
+        out[1] = uint4{m[3], m[4], m[5], n};
+        run += n;
+      }
+    }
+  }
+  if (tid == 0) a.dense_flag[r] = ok ? 1u : 0u;
+}
+
 }  // namespace mf

@@ -41,10 +41,16 @@ __global__ __launch_bounds__(kWalkWaves * kWave) void tail_norm_kernel(TailNormA
   const uint32_t items = a.rows + (a.fb_panel != nullptr ? a.fb_m : 0u);
   const uint32_t wave = threadIdx.x / kWave;
   if (blockIdx.x < items) {
-    if (wave == 0) prep_item(a, blockIdx.x, lds, &inverse_shared, true);
+    if (wave == 0) {
+      prep_item(a, blockIdx.x, lds, &inverse_shared, true);
+    }
     return;
   }
   const uint32_t r = blockIdx.x - items;
+  if (a.dense_spans != nullptr) {
+    dense_walk(a, r, reinterpret_cast<uint32_t*>(lds));
+    return;
+  }
   const RangeLds L = RangeLds::at(reinterpret_cast<uint32_t*>(lds), a.ranges);
   const RangeRow w = range_row(a, r);
   if (!w.indexed) {
@@ -54,6 +60,34 @@ __global__ __launch_bounds__(kWalkWaves * kWave) void tail_norm_kernel(TailNormA
   range_walk(a, w, L, wave);
   __syncthreads();
   range_end(a, r, w, L);
+}
+
+// The dense head's rows, after the norm launch: with the indexed lists
+// (dense_flag) holding at least dense_total ids, or with dense_any (the call
+// has unrestricted rows, so the table is read anyway), every indexed row
+// gets kRowDense.  One workgroup.
+__global__ __launch_bounds__(kThreads) void dense_choose_kernel(TailNormArgs a) {
+  __shared__ uint64_t wave_total[kThreads / kWave];
+  const uint32_t tid = threadIdx.x;
+  uint64_t sum = 0u;
+  for (uint32_t r = tid; r < a.rows; r += kThreads) {
+    if (a.dense_flag[r] != 0u) sum += a.row_meta[r].count;
+  }
+#pragma unroll
+  for (int m = kWave / 2; m > 0; m >>= 1) {
+    const uint32_t lo = static_cast<uint32_t>(__shfl_xor(static_cast<int>(sum & 0xFFFFFFFFu), m));
+    const uint32_t hi = static_cast<uint32_t>(__shfl_xor(static_cast<int>(sum >> 32), m));
+    sum += (static_cast<uint64_t>(hi) << 32) | lo;
+  }
+  if (tid % kWave == 0) wave_total[tid / kWave] = sum;
+  __syncthreads();
+  uint64_t total = 0u;
+  for (uint32_t w = 0; w < kThreads / kWave; ++w) total += wave_total[w];
+  const bool on = total > 0u && (a.dense_any != 0u || total >= a.dense_total);
+  if (!on) return;
+  for (uint32_t r = tid; r < a.rows; r += kThreads) {
+    if (a.dense_flag[r] != 0u) a.row_meta[r].kind |= kRowDense;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -333,12 +367,17 @@ __global__ __launch_bounds__(kWave) void finalize_kernel(FinalizeArgs a) {
 hipError_t launch_tail_norm(const TailNormArgs& args, hipStream_t stream) {
   const size_t norm_lds = 3u * static_cast<size_t>(args.H) * sizeof(float);
   const size_t walk_lds =
-      args.range_index != nullptr ? range_lds_words(args.ranges) * sizeof(uint32_t) : 0u;
+      args.range_index != nullptr ? range_lds_words(args.ranges) * sizeof(uint32_t)
+      : args.dense_spans != nullptr ? dense_lds_words(args.ranges) * sizeof(uint32_t)
+                                    : 0u;
   const uint32_t slots = args.fb_panel != nullptr ? args.fb_m : 0u;
-  const uint32_t walks = args.range_index != nullptr ? args.rows : 0u;
+  const uint32_t walks = args.range_index != nullptr || args.dense_spans != nullptr ? args.rows : 0u;
   const uint32_t threads = walks > 0 ? kWalkWaves * kWave : kWave;
   hipLaunchKernelGGL(tail_norm_kernel, dim3(args.rows + slots + walks), dim3(threads),
                      norm_lds > walk_lds ? norm_lds : walk_lds, stream, args);
+  if (args.dense_spans != nullptr) {
+    hipLaunchKernelGGL(dense_choose_kernel, dim3(1), dim3(kThreads), 0, stream, args);
+  }
   return hipGetLastError();
 }
 

@@ -202,8 +202,8 @@ def decode_tail_workspace_bytes(args: abi.DecodeTailArgs, full: bool = False) ->
 
 
 def decode_tail_path(args: abi.DecodeTailArgs) -> int:
-    """abi.TAIL_PATH_GATHER, abi.TAIL_PATH_TABLE_PASS or abi.TAIL_PATH_FUSED: the kernels
-    mf_decode_tail_f16 runs for these arguments."""
+    """abi.TAIL_PATH_GATHER, abi.TAIL_PATH_TABLE_PASS, abi.TAIL_PATH_FUSED or
+    abi.TAIL_PATH_DENSE: the kernels mf_decode_tail_f16 runs for these arguments."""
     n = ctypes.c_uint32()
     abi.check("decode_tail_path", abi.lib().mf_decode_tail_path(ctypes.byref(args), ctypes.byref(n)))
     return n.value

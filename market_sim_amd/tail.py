@@ -32,19 +32,21 @@ class DeviceTail:
                  copies: int = 1, full: bool = False, advance: Optional[str] = None,
                  unrestricted: Optional[np.ndarray] = None,
                  sorted_lists: Optional[bool] = None, table_pass: bool = False,
-                 fused: bool = True):
+                 fused: bool = True, dense: bool = True):
         import torch
         self.w = w
         # MF_TAIL_SORTED_LISTS (the one-pass table kernel where it pays):
         # declared when the lists are strictly ascending (None: checked
         # here) or by the caller; table_pass asks for that kernel even
         # without unrestricted rows.  fused=False keeps packs of short lists
-        # off the one-kernel tail (MF_TAIL_NO_FUSED).
+        # off the one-kernel tail (MF_TAIL_NO_FUSED); dense=False keeps long
+        # ascending lists on the gather (MF_TAIL_NO_DENSE).
         if sorted_lists is None:
             sorted_lists = workloads.lists_ascending(w.state_offsets, w.state_tokens)
         self.flags = (abi.TAIL_SORTED_LISTS if sorted_lists else 0) | \
             (abi.TAIL_TABLE_PASS if table_pass else 0) | \
-            (0 if fused else abi.TAIL_NO_FUSED)
+            (0 if fused else abi.TAIL_NO_FUSED) | \
+            (0 if dense else abi.TAIL_NO_DENSE)
         # the rows handed to the MFMA head (default: the rows whose state is
         # MF_STATE_UNRESTRICTED)
         self._unrestricted = unrestricted
@@ -125,6 +127,11 @@ class DeviceTail:
     def fused(self) -> bool:
         """The library runs the one-kernel tail (short lists) for this tail."""
         return not self.full and ops.decode_tail_path(self.args(0)) == abi.TAIL_PATH_FUSED
+
+    @property
+    def dense(self) -> bool:
+        """The unrestricted stage is the dense head."""
+        return not self.full and ops.decode_tail_path(self.args(0)) == abi.TAIL_PATH_DENSE
 
     def launch(self, table: int = 0, args: Optional[abi.DecodeTailArgs] = None) -> None:
         a = args if args is not None else self.args(table)

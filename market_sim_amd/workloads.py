@@ -72,11 +72,15 @@ class Workload:
         out[ok] = off[rs[ok] + 1] - off[rs[ok]]
         return out
 
-    def distinct_restricted_ids(self) -> int:
-        """U: distinct embedding rows touched by the restricted rows."""
+    def distinct_restricted_ids(self, rows: Optional[np.ndarray] = None) -> int:
+        """U: distinct embedding rows touched by the restricted rows (or by the
+        rows a boolean mask ``rows`` selects among them)."""
         seen = np.zeros(self.vocab, bool)
         off = self.state_offsets
-        for s in np.unique(self.row_state[self.row_state < self.states]):
+        sel = self.row_state < self.states
+        if rows is not None:
+            sel = sel & rows
+        for s in np.unique(self.row_state[sel]):
             seen[self.state_tokens[off[s]:off[s + 1]]] = True
         return int(seen.sum())
 

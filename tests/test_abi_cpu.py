@@ -26,7 +26,7 @@ def test_library_exports_every_declared_symbol():
     lib = abi.lib()
     for name in declared_functions():
         assert hasattr(lib, name), name
-    assert lib.mf_abi_version() == 5
+    assert lib.mf_abi_version() == 6
 
 
 def b(addr, n):
@@ -121,6 +121,33 @@ def _tail_args(**over):
     return a
 
 
+def test_decode_tail_path_choice():
+    """Which kernels run: the dense head (unrestricted stage) for ascending
+    lists at hidden >= 1024 with hidden % 32 == 0, unless MF_TAIL_NO_DENSE;
+    the CSR gather and the MFMA head otherwise."""
+    l = abi.lib()
+    path = ctypes.c_uint32()
+
+    def path_of(flags, hidden, rows=1024, vocab=4096):
+        a = _tail_args(flags=flags, rows=rows, hidden=hidden, vocab=vocab, max_count=min(4000, vocab),
+                       x=b(0x10000000, rows * hidden * 4), norm_weight=b(0x20000000, hidden * 4),
+                       embedding=b(0x30000000, vocab * hidden * 2),
+                       row_state=b(0x40000000, rows * 4), out_token=b(0x50000000, rows * 4),
+                       out_score=b(0x60000000, rows * 4), workspace=b(0x70000000, 1 << 30))
+        assert l.mf_decode_tail_path(ctypes.byref(a), ctypes.byref(path)).code == abi.MF_OK
+        return path.value
+
+    assert path_of(abi.TAIL_SORTED_LISTS, 2048) == abi.TAIL_PATH_DENSE
+    assert path_of(abi.TAIL_SORTED_LISTS, 1056) == abi.TAIL_PATH_DENSE
+    assert path_of(abi.TAIL_SORTED_LISTS | abi.TAIL_NO_DENSE, 2048) == abi.TAIL_PATH_GATHER
+    assert path_of(0, 2048) == abi.TAIL_PATH_GATHER
+    # hidden below 1024 or not whole 32-feature steps
+    assert path_of(abi.TAIL_SORTED_LISTS | abi.TAIL_NO_FUSED, 576) == abi.TAIL_PATH_GATHER
+    assert path_of(abi.TAIL_SORTED_LISTS, 2040) == abi.TAIL_PATH_GATHER
+    # more rows than the launch's panels hold (256 slots per 8 compute units)
+    assert path_of(abi.TAIL_SORTED_LISTS, 1024, rows=9000, vocab=512) == abi.TAIL_PATH_GATHER
+
+
 def test_decode_tail_validation():
     l = abi.lib()
     n = ctypes.c_uint64()
@@ -176,7 +203,8 @@ def test_decode_tail_sequence_table_and_flags_validation():
     assert ws_code(flags=abi.TAIL_HOLD_FINISHED | abi.TAIL_SORTED_LISTS) == abi.MF_OK
     assert ws_code(flags=abi.TAIL_SORTED_LISTS | abi.TAIL_TABLE_PASS) == abi.MF_OK
     assert ws_code(flags=abi.TAIL_NO_FUSED) == abi.MF_OK
-    assert ws_code(flags=16) == abi.MF_INVALID_ARGUMENT
+    assert ws_code(flags=abi.TAIL_SORTED_LISTS | abi.TAIL_NO_DENSE) == abi.MF_OK
+    assert ws_code(flags=32) == abi.MF_INVALID_ARGUMENT
 
 
 def test_sorted_lists_flag_sizes_the_range_index():
