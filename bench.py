@@ -65,10 +65,12 @@ def algorithmic_bytes(w) -> dict:
              are unrestricted rows (the table is read once for both kinds of
              rows), else U; flops 2 (B_u H V + N H) (candidates and the
              unrestricted rows' head, FP16 hi of z)
-    dense    2 V H + 2 H S with S = B_u + D slots (D: the lists the dense
-             head takes, at least max(64, V / 256) ids, when they hold 2 V
-             ids in all or B_u > 0); flops 2 S H V; the gather then moves the
-             other restricted rows' bytes (gather_rest)."""
+    dense    2 V H + 2 H S with S = B_u + D slots (D: the longest lists
+             of at least max(64, V / 256) ids, as many as fill the room the
+             B_u rows leave in their panels of 256 slots, then whole panels
+             while a panel's lists hold 5 V / 2 ids); flops 2 S H V; the
+             gather then moves the other restricted rows' bytes
+             (gather_rest)."""
     H, V = w.hidden, w.vocab
     counts = w.row_counts()
     restricted = w.row_state < w.states
@@ -81,10 +83,13 @@ def algorithmic_bytes(w) -> dict:
     B = w.rows
     T = V if B_u > 0 else U
     dense_min = max(64, V // 256)
-    cand = restricted & (counts >= dense_min)
-    on = bool(cand.any()) and (B_u > 0 or int(counts[cand].sum()) >= 2 * V)
-    dense_rows = cand if on else np.zeros_like(cand)
-    D = int(dense_rows.sum())
+    cand = np.nonzero(restricted & (counts >= dense_min))[0]
+    order = cand[np.lexsort((cand, -counts[cand]))]  # longest first, then by row
+    D = min(-(-B_u // 256) * 256 - B_u, order.size)
+    while D < order.size and int(counts[order[D:D + 256]].sum()) >= 5 * V // 2:
+        D = min(D + 256, order.size)
+    dense_rows = np.zeros(restricted.shape, bool)
+    dense_rows[order[:D]] = True
     S = B_u + D
     rest = restricted & ~dense_rows
     N_rest = int(counts[rest].sum())

@@ -217,9 +217,12 @@ mf_status mf_linear_f16(mf_buffer input, mf_buffer weight, mf_buffer output,
  * runs one pass over the table that scores the unrestricted rows and the
  * long ascending lists (at least vocab / 256 and 64 ids) with MFMA against
  * every token, keeping only the allowed ones; the gather skips those rows.
- * The device takes the long lists when they hold at least 2 vocab ids in
- * all, or whenever the call has unrestricted rows.  MF_TAIL_NO_DENSE keeps
- * every restricted row on the gather.  The results are the same.
+ * The device takes the longest lists, as many as fill the room the
+ * unrestricted rows leave in their panels of 256 slots, then whole panels
+ * while the lists of the next panel hold at least 5/2 vocab ids (a panel's
+ * pass costs about as much as gathering that many rows).
+ * MF_TAIL_NO_DENSE keeps every restricted row on the gather.  The results
+ * are the same.
  *
  * Short lists: a call with no unrestricted rows, max_count <= 128,
  * hidden % 8 == 0 and max_count within two rounds of one workgroup's LDS

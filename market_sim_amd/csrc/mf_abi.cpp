@@ -504,7 +504,8 @@ bool fused_tail(const mf_decode_tail_args* a) {
 // The dense head (mf_dense.hip): lists declared ascending, a hidden size of
 // whole 32-feature steps wide enough that gathering a long list costs more
 // than scoring its row against every token, and every row fitting the
-// launch's panels (the compute units of each XCD, 256 slots each).  Which
+// launch's panels (the compute units of each XCD, 256 slots each) and the
+// row ranking's 32-bit keys.  Which
 // rows it takes is decided on the device (dense_min_ids, dense_total_ids).
 constexpr uint64_t kDenseMinHidden = 1024;
 bool dense_head(const mf_decode_tail_args* a) {
@@ -512,18 +513,23 @@ bool dense_head(const mf_decode_tail_args* a) {
       a->hidden % 32u != 0 || a->hidden < kDenseMinHidden) {
     return false;
   }
+  // the row ranking packs (count, row) into 32 bits: rows < 2^13, lists < 2^19
   const uint64_t panels = device_cus() / 8u;
-  return a->rows + a->unrestricted_count <= panels * mf::kDensePanelSlots;
+  return a->rows + a->unrestricted_count <= panels * mf::kDensePanelSlots && a->rows <= 8191u &&
+         a->vocab < (1u << 19);
 }
 // A list the dense head may take: at least 1/256 of the vocabulary (and 64
-// ids); the head runs when those lists hold at least twice the vocabulary's
-// ids in all (their gather would read the table twice over), or whenever
-// unrestricted rows make it read the table anyway.
+// ids).  A panel of the dense head is added when its lists hold at least
+// 5/2 of the vocabulary's ids: one panel's pass over the table and the
+// gather of that many candidate rows take about the same time (both are
+// bound by what each compute unit's memory pipeline moves, and both scale
+// with the hidden size; measured at V = 128256, H = 2048: a panel pass
+// 190 us, the gather 7.2 TB/s of candidate rows).
 uint32_t dense_min_ids(uint64_t vocab) {
   const uint64_t m = vocab / 256u;
   return static_cast<uint32_t>(m > 64u ? m : 64u);
 }
-uint64_t dense_total_ids(uint64_t vocab) { return 2u * vocab; }
+uint64_t dense_panel_ids(uint64_t vocab) { return vocab * 5u / 2u; }
 
 // Validation common to both decode-tail entry points; fills the layout.
 mf_status validate_tail(const mf_decode_tail_args* a, bool full, TailLayout& L) {
@@ -728,8 +734,10 @@ mf::TailNormArgs norm_args(const mf_decode_tail_args* a, const TailLayout& L, ch
     n.dense_spans = reinterpret_cast<uint4*>(ws + L.dense_spans);
     n.dense_flag = reinterpret_cast<uint32_t*>(ws + L.dense_flag);
     n.dense_min = dense_min_ids(a->vocab);
-    n.dense_any = a->unrestricted_count > 0 ? 1u : 0u;
-    n.dense_total = dense_total_ids(a->vocab);
+    n.dense_fb = static_cast<uint32_t>(a->unrestricted_count);
+    n.dense_sort = 1u;
+    while (n.dense_sort < a->rows) n.dense_sort <<= 1;
+    n.dense_panel_ids = dense_panel_ids(a->vocab);
   }
   return n;
 }

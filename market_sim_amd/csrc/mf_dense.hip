@@ -27,7 +27,8 @@
 // token ids for unrestricted ones).
 //
 // Workgroups: one per compute unit.  Each computes the slot list itself (a
-// prefix over the rows' kinds), so P = ceil(slots / 256) panels; the
+// prefix over the rows' kinds), so P = ceil(slots / 256) panels of equal
+// size (to one slot); row blocks past a panel's slots get no MFMA.  The
 // compute units of an XCD (blockIdx % 8) form groups of P workgroups that
 // run the same run of tiles, one panel each, so the table tiles of a group
 // are read from HBM once and from the XCD's L2 by the other panels.
@@ -85,9 +86,11 @@ __host__ __device__ constexpr uint32_t dense_lds_bytes() {
 __device__ __forceinline__ uint32_t swz(uint32_t r) { return ((r >> 1) ^ (r >> 3)) & 3u; }
 
 // The slot list of the launch: unrestricted rows first (fb_rows order), then
-// the kRowDense rows in row order.  Fills this panel's slot table; returns
-// the number of slots.
-__device__ uint32_t dense_slots(const DenseArgs& a, DenseShared& sh, uint32_t panel, bool map) {
+// the kRowDense rows in row order; panel p of P takes slots [p0, p0 + n)
+// with p0 = p S / P (S slots), so the panels differ by one slot at most.
+// Fills this panel's slot table.
+__device__ void dense_slots(const DenseArgs& a, DenseShared& sh, uint32_t p0, uint32_t n,
+                            bool map) {
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid % kWave;
   const uint32_t wave = tid / kWave;
@@ -106,19 +109,13 @@ __device__ uint32_t dense_slots(const DenseArgs& a, DenseShared& sh, uint32_t pa
   if (lane == kWave - 1) sh.wave_sum[wave] = incl;
   __syncthreads();
   uint32_t before = incl - local;
-  uint32_t total = 0u;
 #pragma unroll
-  for (uint32_t w = 0; w < kWaves; ++w) {
-    before += w < wave ? sh.wave_sum[w] : 0u;
-    total += sh.wave_sum[w];
-  }
-  const uint32_t n_slots = a.fb_m + total;
-  const uint32_t p0 = panel * kDensePanelSlots;
+  for (uint32_t w = 0; w < kWaves; ++w) before += w < wave ? sh.wave_sum[w] : 0u;
   // unrestricted slots of this panel (a listed row that is not unrestricted,
   // or not a row, gets no slot work)
   {
     const uint32_t gs = p0 + tid;
-    if (gs < a.fb_m) {
+    if (tid < n && gs < a.fb_m) {
       const uint32_t r = a.fb_rows[gs];
       if (r < a.rows && (a.row_meta[r].kind & kRowUnrestricted)) {
         sh.slot_row[tid] = r;
@@ -130,7 +127,7 @@ __device__ uint32_t dense_slots(const DenseArgs& a, DenseShared& sh, uint32_t pa
   uint32_t k = a.fb_m + before;
   for (uint32_t r = r0; r < r1; ++r) {
     if (a.row_meta[r].kind & kRowDense) {
-      if (k >= p0 && k < p0 + kDensePanelSlots) {
+      if (k >= p0 && k < p0 + n) {
         sh.slot_row[k - p0] = r;
         sh.slot_kind[k - p0] = kSlotList;
       }
@@ -147,7 +144,6 @@ __device__ uint32_t dense_slots(const DenseArgs& a, DenseShared& sh, uint32_t pa
     if (map && kind != kSlotNone) a.fb_map[r] = p0 + tid;
   }
   __syncthreads();
-  return n_slots;
 }
 
 __global__ __launch_bounds__(kThreads) void dense_kernel(DenseArgs a) {
@@ -187,12 +183,17 @@ __global__ __launch_bounds__(kThreads) void dense_kernel(DenseArgs a) {
   const uint32_t gpx = per_xcd / P;
   if (l >= gpx * P) return;
   const uint32_t panel = l % P;
+  const uint32_t p0 = panel * n_slots / P;
+  const uint32_t pn = (panel + 1u) * n_slots / P - p0;
+  // row blocks with slots; wave parity wm takes blocks 2 i + wm, i < nact
+  const uint32_t nrb = (pn + 15u) / 16u;
+  const uint32_t nact = nrb > wm ? (nrb - wm + 1u) / 2u : 0u;
   const uint32_t grp = x * gpx + l / P;
   const uint32_t groups = xcds * gpx;
   const uint32_t tiles = a.ranges;
   const uint32_t t_begin = static_cast<uint32_t>(static_cast<uint64_t>(tiles) * grp / groups);
   const uint32_t t_end = static_cast<uint32_t>(static_cast<uint64_t>(tiles) * (grp + 1u) / groups);
-  dense_slots(a, sh, panel, grp == 0u);
+  dense_slots(a, sh, p0, pn, grp == 0u);
   const uint32_t H = a.H;
   const uint32_t steps = H / 32u;
   // per-lane copy sources: A rows (4 copies of 16 rows), span records (2
@@ -218,264 +219,280 @@ __global__ __launch_bounds__(kThreads) void dense_kernel(DenseArgs a) {
       burst_to_lds(src, dst + (wave * 2u + j) * kWave);
     }
   };
-  if (t_begin < t_end) issue_span(t_begin);
-  for (uint32_t tile = t_begin; tile < t_end; ++tile) {
-    if (tile + 1u < t_end) issue_span(tile + 1u);
-    const uint32_t tok0 = tile * kHeadTileTokens;
-    const uint32_t nt = a.V - tok0 < kHeadTileTokens ? a.V - tok0 : kHeadTileTokens;
-    const uint16_t* tbase = a.emb + static_cast<uint64_t>(tok0) * H;
-    uint32_t boff[kBDma];
-#pragma unroll
-    for (int j = 0; j < kBDma; ++j) {
-      const uint32_t t = (wave * kBDma + j) * 16u + lane / 4u;
-      const uint32_t tc = t < nt ? t : nt - 1u;
-      boff[j] = tc * H + (((lane % 4u) ^ swz(t)) * 8u);
-    }
-    auto issue = [&](uint32_t s) {
-      unsigned char* st = dyn + (s % kStages) * kStageBytes;
-      const uint32_t f = s * 32u;
-#pragma unroll
-      for (int j = 0; j < kADma; ++j) burst_to_lds(a.z_hi + aoff[j] + f, st + (wave * kADma + j) * 1024u);
-#pragma unroll
+  // the tiles, with NACT of the wave's row blocks holding slots (a variant
+  // per count, so the loop has no branch around an MFMA)
+  auto run = [&]<int NACT>() {
+    if (t_begin < t_end) issue_span(t_begin);
+    for (uint32_t tile = t_begin; tile < t_end; ++tile) {
+      if (tile + 1u < t_end) issue_span(tile + 1u);
+      const uint32_t tok0 = tile * kHeadTileTokens;
+      const uint32_t nt = a.V - tok0 < kHeadTileTokens ? a.V - tok0 : kHeadTileTokens;
+      const uint16_t* tbase = a.emb + static_cast<uint64_t>(tok0) * H;
+      uint32_t boff[kBDma];
+  #pragma unroll
       for (int j = 0; j < kBDma; ++j) {
-        burst_to_lds(tbase + boff[j] + f, st + kABytes + (wave * kBDma + j) * 1024u);
+        const uint32_t t = (wave * kBDma + j) * 16u + lane / 4u;
+        const uint32_t tc = t < nt ? t : nt - 1u;
+        boff[j] = tc * H + (((lane % 4u) ^ swz(t)) * 8u);
       }
-    };
-    floatx4 acc[kRBw][kTBw];
-    floatx4 gram[kGramBw];
-#pragma unroll
-    for (int i = 0; i < kRBw; ++i) {
-#pragma unroll
-      for (int j = 0; j < kTBw; ++j) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-    }
-#pragma unroll
-    for (int j = 0; j < kGramBw; ++j) gram[j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int s = 0; s < kStages - 1; ++s) issue(static_cast<uint32_t>(s) < steps ? s : steps - 1u);
-    for (uint32_t s = 0; s < steps; ++s) {
-      // step s's copies have landed (later steps' may be in flight); then
-      // every wave's copies are visible, and the stage step s - 1 used is
-      // free for step s + kStages - 1
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"((kStages - 2) * kDmaPerWave) : "memory");
-      __syncthreads();
-      issue(s + kStages - 1 < steps ? s + kStages - 1 : steps - 1u);
-      const unsigned char* st = dyn + (s % kStages) * kStageBytes;
-      half8_t fa[kRBw], fb[kTBw];
-#pragma unroll
+      auto issue = [&](uint32_t s) {
+        unsigned char* st = dyn + (s % kStages) * kStageBytes;
+        const uint32_t f = s * 32u;
+  #pragma unroll
+        for (int j = 0; j < kADma; ++j) burst_to_lds(a.z_hi + aoff[j] + f, st + (wave * kADma + j) * 1024u);
+  #pragma unroll
+        for (int j = 0; j < kBDma; ++j) {
+          burst_to_lds(tbase + boff[j] + f, st + kABytes + (wave * kBDma + j) * 1024u);
+        }
+      };
+      floatx4 acc[kRBw][kTBw];
+      floatx4 gram[kGramBw];
+  #pragma unroll
       for (int i = 0; i < kRBw; ++i) {
-        const uint32_t r = (2u * i + wm) * 16u + col;
-        fa[i] = *reinterpret_cast<const half8_t*>(st + r * 64u + ((kb ^ swz(r)) * 16u));
+  #pragma unroll
+        for (int j = 0; j < kTBw; ++j) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
       }
-#pragma unroll
-      for (int j = 0; j < kTBw; ++j) {
-        const uint32_t t = (wn * kTBw + j) * 16u + col;
-        fb[j] = *reinterpret_cast<const half8_t*>(st + kABytes + t * 64u + ((kb ^ swz(t)) * 16u));
-      }
-#pragma unroll
-      for (int j = 0; j < kGramBw; ++j) {
-        const half8_t g = wm == 0u ? fb[j] : fb[kGramBw + j];  // (wm is wave-uniform)
-        gram[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(g, g, gram[j], 0, 0, 0);
-      }
-#pragma unroll
-      for (int i = 0; i < kRBw; ++i) {
-#pragma unroll
+  #pragma unroll
+      for (int j = 0; j < kGramBw; ++j) gram[j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  #pragma unroll
+      for (int s = 0; s < kStages - 1; ++s) issue(static_cast<uint32_t>(s) < steps ? s : steps - 1u);
+      for (uint32_t s = 0; s < steps; ++s) {
+        // step s's copies have landed (later steps' may be in flight); then
+        // every wave's copies are visible, and the stage step s - 1 used is
+        // free for step s + kStages - 1
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"((kStages - 2) * kDmaPerWave) : "memory");
+        __syncthreads();
+        issue(s + kStages - 1 < steps ? s + kStages - 1 : steps - 1u);
+        const unsigned char* st = dyn + (s % kStages) * kStageBytes;
+        half8_t fa[kRBw], fb[kTBw];
+  #pragma unroll
+        for (int i = 0; i < NACT; ++i) {
+          const uint32_t r = (2u * i + wm) * 16u + col;
+          fa[i] = *reinterpret_cast<const half8_t*>(st + r * 64u + ((kb ^ swz(r)) * 16u));
+        }
+  #pragma unroll
         for (int j = 0; j < kTBw; ++j) {
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+          const uint32_t t = (wn * kTBw + j) * 16u + col;
+          fb[j] = *reinterpret_cast<const half8_t*>(st + kABytes + t * 64u + ((kb ^ swz(t)) * 16u));
         }
-      }
-    }
-    // the copies past the last step, and the span copies, have landed
-    wait_vector_memory();
-    __syncthreads();
-
-    // token norms: the Gram diagonal of column c sits in lane c + 16 (c / 4),
-    // element c % 4; a NaN norm (non-finite table row) propagates
-    float tn_local = 0.0f;
-    bool tn_nan = false;
-#pragma unroll
-    for (int j = 0; j < kGramBw; ++j) {
-      const uint32_t e = col % 4u;
-      const float d = e == 0u ? gram[j][0] : (e == 1u ? gram[j][1] : (e == 2u ? gram[j][2] : gram[j][3]));
-      const uint32_t t = (wn * kTBw + wm * kGramBw + j) * 16u + col;
-      if (col / 4u == kb && t < nt) {
-        const float v = __fsqrt_rn(d) * (1.0f + 0x1p-7f);
-        tn_nan |= v != v;
-        tn_local = __builtin_fmaxf(tn_local, v);
-      }
-    }
-    {
-      const bool any_nan = __ballot(tn_nan) != 0ull;
-      const float m = wave_max(tn_local);
-      if (lane == 0) sh.tn[wave] = any_nan ? __builtin_nanf("") : m;
-    }
-    const uint32_t b = tile & 1u;
-    // the allowed words of every slot in its span record: unrestricted slots
-    // allow the tile's tokens below nt, empty slots nothing
-    {
-      const uint32_t kind = sh.slot_kind[tid];
-      if (kind != kSlotList) {
-        uint32_t w[6];
-#pragma unroll
-        for (int k = 0; k < 6; ++k) {
-          const uint32_t lo = k * 32u;
-          w[k] = kind == kSlotNone ? 0u
-                 : (nt >= lo + 32u ? 0xFFFFFFFFu : (nt > lo ? (1u << (nt - lo)) - 1u : 0u));
+  #pragma unroll
+        for (int j = 0; j < kGramBw; ++j) {
+          const half8_t g = wm == 0u ? fb[j] : fb[kGramBw + j];  // (wm is wave-uniform)
+          gram[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(g, g, gram[j], 0, 0, 0);
         }
-        sh.span[b][tid][0] = uint4{w[0], w[1], w[2], tok0};
-        sh.span[b][tid][1] = uint4{w[3], w[4], w[5], kind == kSlotNone ? 0u : nt};
-      }
-    }
-    __syncthreads();
-    // lane bases: slot (i, q) of this lane is sbase + 32 i + q (opaque to
-    // the compiler, so that the epilogue's addresses are formed here and not
-    // hoisted out of the tile loop, where they would outlive the registers)
-    uint32_t sbase = wm * 16u + 4u * kb;
-    asm volatile("" : "+v"(sbase));
-    const uint4* spn = &sh.span[b][sbase][wn];
-    const uint32_t sel0 = 1u << col;
-    const uint32_t sel1 = 1u << (16u + col);
-    // Per-lane values of each slot go to LDS rows of 33 words (the stage
-    // area, free now): word 16 half + column of slot s's row, padded so the
-    // four slots of one write sit on different banks.
-    float* gl1 = reinterpret_cast<float*>(dyn);                          // best
-    float* gl2 = reinterpret_cast<float*>(dyn + kEpiRowsBytes);          // second best
-    uint8_t* glj = dyn + 2u * kEpiRowsBytes;  // token block of the best
-    TileRecord* stage_rec = reinterpret_cast<TileRecord*>(dyn + 2u * kEpiRowsBytes + kEpiBlockBytes);
-    const uint32_t lw = sbase * kEpiRow + wn * 16u + col;  // this lane's word of slot sbase
-    // per slot and lane: the best and second best allowed scores of the
-    // lane's six tokens and the block of the best (the best is NaN when one
-    // of its allowed scores is not finite)
-#pragma unroll
-    for (int i = 0; i < kRBw; ++i) {
-      uint4 w4[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) w4[q] = spn[(32 * i + q) * 2];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const uint32_t w[3] = {w4[q].x, w4[q].y, w4[q].z};
-        float m1 = -__builtin_huge_valf();
-        float m2 = -__builtin_huge_valf();
-        uint32_t j1 = 0u;
-        bool bad = false;
-#pragma unroll
-        for (int j = 0; j < kTBw; ++j) {
-          const bool allowed = (w[j / 2] & (j % 2 == 0 ? sel0 : sel1)) != 0u;
-          const float v = acc[i][j][q];
-          bad |= allowed && !__builtin_isfinite(v);
-          const bool top = allowed && v > m1;
-          const bool second = allowed && !top && v > m2;
-          m2 = top ? m1 : (second ? v : m2);
-          j1 = top ? static_cast<uint32_t>(j) : j1;
-          m1 = top ? v : m1;
-        }
-        gl1[lw + (32 * i + q) * kEpiRow] = bad ? __builtin_nanf("") : m1;
-        gl2[lw + (32 * i + q) * kEpiRow] = m2;
-        glj[lw + (32 * i + q) * kEpiRow] = static_cast<uint8_t>(j1);
-      }
-    }
-    __syncthreads();
-    // the slot's record (thread s), written into its LDS stage.  G = the
-    // best allowed score, b the bound, L = fl(G - b); the members are the
-    // lane bests with fl(g + b) >= L (a lane's other scores are at most its
-    // second best: when that qualifies too, the record is crowded)
-    {
-      float tn_max = sh.tn[0];
-#pragma unroll
-      for (int w = 1; w < kWaves; ++w) {
-        const float v = sh.tn[w];
-        tn_max = (tn_max != tn_max || v != v) ? __builtin_nanf("") : __builtin_fmaxf(tn_max, v);
-      }
-      const uint32_t s = tid;
-      const uint32_t kind = sh.slot_kind[s];
-      const uint4 h0 = sh.span[b][s][0];
-      const uint4 h1 = sh.span[b][s][1];
-      const uint32_t lo = h0.w;
-      const uint32_t cnt = h1.w;
-      TileRecord& rec = stage_rec[s];
-      if (cnt == 0u) {
-        reinterpret_cast<uint4*>(&rec)[0] =
-            uint4{__float_as_uint(-__builtin_huge_valf()), 0u, kInvalidToken, lo};
-        reinterpret_cast<uint4*>(&rec)[1] =
-            uint4{lo, 0u, 0u, __float_as_uint(-__builtin_huge_valf())};
-      } else {
-        const float* r1 = gl1 + s * kEpiRow;
-        const float* r2 = gl2 + s * kEpiRow;
-        float G = -__builtin_huge_valf();
-        bool fin = true;
-#pragma unroll
-        for (int u = 0; u < 32; ++u) {
-          const float v = r1[u];
-          fin &= v == v;
-          G = __builtin_fmaxf(G, v);
-        }
-        const float bs = __builtin_fmaf(tn_max, __builtin_fmaf(a.coef, sh.slot_norm[s], a.coef2),
-                                        sh.slot_slack[s]);
-        const float L = G - bs;
-        const bool finite = fin && bs < 0x1p100f;
-        uint32_t members = 0u;  // bit u: lane u's best is a member
-        bool crowded = false;
-#pragma unroll
-        for (int u = 0; u < 32; ++u) {
-          members |= (r1[u] + bs >= L) ? (1u << u) : 0u;
-          crowded |= r2[u] + bs >= L;
-        }
-        const uint32_t total = static_cast<uint32_t>(__popc(members));
-        const bool ordinary = finite && !crowded && total <= static_cast<uint32_t>(kTileMembers);
-        const uint32_t ws[6] = {h0.x, h0.y, h0.z, h1.x, h1.y, h1.z};
-        // the tile's lowest allowed token (cnt > 0 bits)
-        uint32_t first = kHeadTileTokens;
-#pragma unroll
-        for (int u = 5; u >= 0; --u) {
-          if (ws[u] != 0u) first = u * 32u + static_cast<uint32_t>(__builtin_ctz(ws[u]));
-        }
-        const uint32_t flags =
-            ordinary ? 0u : (finite ? kTileRescoreAll | kTileCrowded : kTileRescoreAll);
-        reinterpret_cast<uint4*>(&rec)[0] = uint4{__float_as_uint(L), flags, tok0 + first, lo};
-        reinterpret_cast<uint4*>(&rec)[1] =
-            uint4{lo, cnt, ordinary ? total : 0u, __float_as_uint(G + bs)};
-        if (ordinary) {
-          uint32_t k = 0u;
-          uint32_t left = members;
-          while (left != 0u) {
-            const uint32_t u = static_cast<uint32_t>(__builtin_ctz(left));
-            left &= left - 1u;
-            // half u / 16, column u % 16, block of the half glj
-            const uint32_t off = ((u / 16u) * kTBw + glj[s * kEpiRow + u]) * 16u + (u % 16u);
-            const float v = r1[u];
-            // list position: lo + the allowed tokens below off
-            uint32_t pos = tok0 + off;
-            if (kind == kSlotList) {
-              uint32_t rank = 0u;
-#pragma unroll
-              for (uint32_t t = 0; t < 6u; ++t) {
-                const uint32_t below = off >= (t + 1u) * 32u ? 0xFFFFFFFFu
-                                       : (off > t * 32u ? (1u << (off - t * 32u)) - 1u : 0u);
-                rank += static_cast<uint32_t>(__popc(ws[t] & below));
-              }
-              pos = lo + rank;
-            }
-            rec.m[k] = TileMember{tok0 + off, pos, v - bs, v + bs};
-            ++k;
+  #pragma unroll
+        for (int i = 0; i < NACT; ++i) {
+  #pragma unroll
+          for (int j = 0; j < kTBw; ++j) {
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[i], fb[j], acc[i][j], 0, 0, 0);
           }
         }
       }
-    }
-    __syncthreads();
-    // the staged records out, 16 bytes per thread and step (each record is
-    // contiguous in global memory); no wait for these stores before the
-    // next tile, only for the LDS reads
-    {
-      constexpr uint32_t kPieces = sizeof(TileRecord) / 16u;
-      const uint4* from = reinterpret_cast<const uint4*>(stage_rec);
-      for (uint32_t u = tid; u < kDensePanelSlots * kPieces; u += kThreads) {
-        const uint32_t s = u / kPieces;
-        if (sh.slot_kind[s] == kSlotNone) continue;
-        uint4* to = reinterpret_cast<uint4*>(
-            a.records + (static_cast<uint64_t>(panel) * kDensePanelSlots + s) * tiles + tile);
-        to[u % kPieces] = from[u];
+      // the copies past the last step, and the span copies, have landed
+      wait_vector_memory();
+      __syncthreads();
+
+      // token norms: the Gram diagonal of column c sits in lane c + 16 (c / 4),
+      // element c % 4; a NaN norm (non-finite table row) propagates
+      float tn_local = 0.0f;
+      bool tn_nan = false;
+  #pragma unroll
+      for (int j = 0; j < kGramBw; ++j) {
+        const uint32_t e = col % 4u;
+        const float d = e == 0u ? gram[j][0] : (e == 1u ? gram[j][1] : (e == 2u ? gram[j][2] : gram[j][3]));
+        const uint32_t t = (wn * kTBw + wm * kGramBw + j) * 16u + col;
+        if (col / 4u == kb && t < nt) {
+          const float v = __fsqrt_rn(d) * (1.0f + 0x1p-7f);
+          tn_nan |= v != v;
+          tn_local = __builtin_fmaxf(tn_local, v);
+        }
       }
+      {
+        const bool any_nan = __ballot(tn_nan) != 0ull;
+        const float m = wave_max(tn_local);
+        if (lane == 0) sh.tn[wave] = any_nan ? __builtin_nanf("") : m;
+      }
+      const uint32_t b = tile & 1u;
+      // the allowed words of every slot in its span record: unrestricted slots
+      // allow the tile's tokens below nt, empty slots nothing
+      {
+        const uint32_t kind = sh.slot_kind[tid];
+        if (kind != kSlotList) {
+          uint32_t w[6];
+  #pragma unroll
+          for (int k = 0; k < 6; ++k) {
+            const uint32_t lo = k * 32u;
+            w[k] = kind == kSlotNone ? 0u
+                   : (nt >= lo + 32u ? 0xFFFFFFFFu : (nt > lo ? (1u << (nt - lo)) - 1u : 0u));
+          }
+          sh.span[b][tid][0] = uint4{w[0], w[1], w[2], tok0};
+          sh.span[b][tid][1] = uint4{w[3], w[4], w[5], kind == kSlotNone ? 0u : nt};
+        }
+      }
+      __syncthreads();
+      // lane bases: slot (i, q) of this lane is sbase + 32 i + q (opaque to
+      // the compiler, so that the epilogue's addresses are formed here and not
+      // hoisted out of the tile loop, where they would outlive the registers)
+      uint32_t sbase = wm * 16u + 4u * kb;
+      asm volatile("" : "+v"(sbase));
+      const uint4* spn = &sh.span[b][sbase][wn];
+      const uint32_t sel0 = 1u << col;
+      const uint32_t sel1 = 1u << (16u + col);
+      // Per-lane values of each slot go to LDS rows of 33 words (the stage
+      // area, free now): word 16 half + column of slot s's row, padded so the
+      // four slots of one write sit on different banks.
+      float* gl1 = reinterpret_cast<float*>(dyn);                          // best
+      float* gl2 = reinterpret_cast<float*>(dyn + kEpiRowsBytes);          // second best
+      uint8_t* glj = dyn + 2u * kEpiRowsBytes;  // token block of the best
+      TileRecord* stage_rec = reinterpret_cast<TileRecord*>(dyn + 2u * kEpiRowsBytes + kEpiBlockBytes);
+      const uint32_t lw = sbase * kEpiRow + wn * 16u + col;  // this lane's word of slot sbase
+      // per slot and lane: the best and second best allowed scores of the
+      // lane's six tokens and the block of the best (the best is NaN when one
+      // of its allowed scores is not finite); the row blocks past the panel's
+      // slots hold none of its slots
+  #pragma unroll
+      for (int i = 0; i < NACT; ++i) {
+        uint4 w4[4];
+  #pragma unroll
+        for (int q = 0; q < 4; ++q) w4[q] = spn[(32 * i + q) * 2];
+  #pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t w[3] = {w4[q].x, w4[q].y, w4[q].z};
+          float m1 = -__builtin_huge_valf();
+          float m2 = -__builtin_huge_valf();
+          uint32_t j1 = 0u;
+          bool bad = false;
+  #pragma unroll
+          for (int j = 0; j < kTBw; ++j) {
+            const bool allowed = (w[j / 2] & (j % 2 == 0 ? sel0 : sel1)) != 0u;
+            const float v = acc[i][j][q];
+            bad |= allowed && !__builtin_isfinite(v);
+            const bool top = allowed && v > m1;
+            const bool second = allowed && !top && v > m2;
+            m2 = top ? m1 : (second ? v : m2);
+            j1 = top ? static_cast<uint32_t>(j) : j1;
+            m1 = top ? v : m1;
+          }
+          gl1[lw + (32 * i + q) * kEpiRow] = bad ? __builtin_nanf("") : m1;
+          gl2[lw + (32 * i + q) * kEpiRow] = m2;
+          glj[lw + (32 * i + q) * kEpiRow] = static_cast<uint8_t>(j1);
+        }
+      }
+      __syncthreads();
+      // the slot's record (thread s), written into its LDS stage.  G = the
+      // best allowed score, b the bound, L = fl(G - b); the members are the
+      // lane bests with fl(g + b) >= L (a lane's other scores are at most its
+      // second best: when that qualifies too, the record is crowded)
+      {
+        float tn_max = sh.tn[0];
+  #pragma unroll
+        for (int w = 1; w < kWaves; ++w) {
+          const float v = sh.tn[w];
+          tn_max = (tn_max != tn_max || v != v) ? __builtin_nanf("") : __builtin_fmaxf(tn_max, v);
+        }
+        const uint32_t s = tid;
+        const uint32_t kind = sh.slot_kind[s];
+        const uint4 h0 = sh.span[b][s][0];
+        const uint4 h1 = sh.span[b][s][1];
+        const uint32_t lo = h0.w;
+        const uint32_t cnt = h1.w;
+        TileRecord& rec = stage_rec[s];
+        if (cnt == 0u) {
+          reinterpret_cast<uint4*>(&rec)[0] =
+              uint4{__float_as_uint(-__builtin_huge_valf()), 0u, kInvalidToken, lo};
+          reinterpret_cast<uint4*>(&rec)[1] =
+              uint4{lo, 0u, 0u, __float_as_uint(-__builtin_huge_valf())};
+        } else {
+          const float* r1 = gl1 + s * kEpiRow;
+          const float* r2 = gl2 + s * kEpiRow;
+          float G = -__builtin_huge_valf();
+          bool fin = true;
+  #pragma unroll
+          for (int u = 0; u < 32; ++u) {
+            const float v = r1[u];
+            fin &= v == v;
+            G = __builtin_fmaxf(G, v);
+          }
+          const float bs = __builtin_fmaf(tn_max, __builtin_fmaf(a.coef, sh.slot_norm[s], a.coef2),
+                                          sh.slot_slack[s]);
+          const float L = G - bs;
+          const bool finite = fin && bs < 0x1p100f;
+          uint32_t members = 0u;  // bit u: lane u's best is a member
+          bool crowded = false;
+  #pragma unroll
+          for (int u = 0; u < 32; ++u) {
+            members |= (r1[u] + bs >= L) ? (1u << u) : 0u;
+            crowded |= r2[u] + bs >= L;
+          }
+          const uint32_t total = static_cast<uint32_t>(__popc(members));
+          const bool ordinary = finite && !crowded && total <= static_cast<uint32_t>(kTileMembers);
+          const uint32_t ws[6] = {h0.x, h0.y, h0.z, h1.x, h1.y, h1.z};
+          // the tile's lowest allowed token (cnt > 0 bits)
+          uint32_t first = kHeadTileTokens;
+  #pragma unroll
+          for (int u = 5; u >= 0; --u) {
+            if (ws[u] != 0u) first = u * 32u + static_cast<uint32_t>(__builtin_ctz(ws[u]));
+          }
+          const uint32_t flags =
+              ordinary ? 0u : (finite ? kTileRescoreAll | kTileCrowded : kTileRescoreAll);
+          reinterpret_cast<uint4*>(&rec)[0] = uint4{__float_as_uint(L), flags, tok0 + first, lo};
+          reinterpret_cast<uint4*>(&rec)[1] =
+              uint4{lo, cnt, ordinary ? total : 0u, __float_as_uint(G + bs)};
+          if (ordinary) {
+            uint32_t k = 0u;
+            uint32_t left = members;
+            while (left != 0u) {
+              const uint32_t u = static_cast<uint32_t>(__builtin_ctz(left));
+              left &= left - 1u;
+              // half u / 16, column u % 16, block of the half glj
+              const uint32_t off = ((u / 16u) * kTBw + glj[s * kEpiRow + u]) * 16u + (u % 16u);
+              const float v = r1[u];
+              // list position: lo + the allowed tokens below off
+              uint32_t pos = tok0 + off;
+              if (kind == kSlotList) {
+                uint32_t rank = 0u;
+  #pragma unroll
+                for (uint32_t t = 0; t < 6u; ++t) {
+                  const uint32_t below = off >= (t + 1u) * 32u ? 0xFFFFFFFFu
+                                         : (off > t * 32u ? (1u << (off - t * 32u)) - 1u : 0u);
+                  rank += static_cast<uint32_t>(__popc(ws[t] & below));
+                }
+                pos = lo + rank;
+              }
+              rec.m[k] = TileMember{tok0 + off, pos, v - bs, v + bs};
+              ++k;
+            }
+          }
+        }
+      }
+      __syncthreads();
+      // the staged records out, 16 bytes per thread and step (each record is
+      // contiguous in global memory); no wait for these stores before the
+      // next tile, only for the LDS reads
+      {
+        constexpr uint32_t kPieces = sizeof(TileRecord) / 16u;
+        const uint4* from = reinterpret_cast<const uint4*>(stage_rec);
+        for (uint32_t u = tid; u < kDensePanelSlots * kPieces; u += kThreads) {
+          const uint32_t s = u / kPieces;
+          if (sh.slot_kind[s] == kSlotNone) continue;
+          uint4* to = reinterpret_cast<uint4*>(
+              a.records + (static_cast<uint64_t>(p0) + s) * tiles + tile);
+          to[u % kPieces] = from[u];
+        }
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     }
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  };
+  switch (nact) {
+    case 8: run.template operator()<8>(); break;
+    case 7: run.template operator()<7>(); break;
+    case 6: run.template operator()<6>(); break;
+    case 5: run.template operator()<5>(); break;
+    case 4: run.template operator()<4>(); break;
+    case 3: run.template operator()<3>(); break;
+    case 2: run.template operator()<2>(); break;
+    case 1: run.template operator()<1>(); break;
+    default: run.template operator()<0>(); break;
   }
 }
 

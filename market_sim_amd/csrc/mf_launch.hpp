@@ -144,14 +144,16 @@ struct TailNormArgs {
   // dense_spans[(g * rows + r) * 2 + {0, 1}] = {m0, m1, m2, lo}, {m3, m4,
   // m5, cnt} (the range's ids as a 192-bit mask, the list position of its
   // first id, their count); dense_flag[r] = 1 (else 0).  A one-workgroup
-  // kernel after the launch decides: when the indexed lists hold at least
-  // dense_total ids, or any with dense_any, every indexed row gets
-  // kRowDense in row_meta.
+  // kernel after the launch (dense_choose_kernel) gives the longest indexed
+  // lists kRowDense in row_meta: as many as fill the room dense_fb
+  // unrestricted rows leave in their panels, then whole panels while the
+  // lists of the next panel hold at least dense_panel_ids ids.
   uint4* dense_spans;      // [ranges, rows, 2]
   uint32_t* dense_flag;    // [rows]
   uint32_t dense_min;
-  uint32_t dense_any;      // 1: the table is read anyway (unrestricted rows)
-  uint64_t dense_total;
+  uint32_t dense_fb;       // unrestricted rows of the call
+  uint32_t dense_sort;     // power of two >= rows (the ranking's size)
+  uint64_t dense_panel_ids;
 };
 
 // row_tiles flag: the row's ranges are not used (its one record comes from

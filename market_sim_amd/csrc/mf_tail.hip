@@ -62,31 +62,96 @@ __global__ __launch_bounds__(kWalkWaves * kWave) void tail_norm_kernel(TailNormA
   range_end(a, r, w, L);
 }
 
-// The dense head's rows, after the norm launch: with the indexed lists
-// (dense_flag) holding at least dense_total ids, or with dense_any (the call
-// has unrestricted rows, so the table is read anyway), every indexed row
-// gets kRowDense.  One workgroup.
+// The dense head's rows, after the norm launch.  The indexed lists
+// (dense_flag) are ranked by length (longest first, then by row); the head
+// takes the D longest, D filling whole panels of kDensePanelSlots slots
+// after the dense_fb unrestricted rows: the room the unrestricted rows leave
+// in their panels (which read the table anyway) is filled for free, and a
+// further panel is added only while the lists it would take hold at least
+// dense_panel_ids ids (a panel's pass over the table costs about as much
+// as gathering that many candidate rows).  One workgroup; dynamic LDS:
+// dense_sort 4-byte keys, dense_sort the power of two >= rows.
 __global__ __launch_bounds__(kThreads) void dense_choose_kernel(TailNormArgs a) {
-  __shared__ uint64_t wave_total[kThreads / kWave];
+  // 32-bit keys (count << 13) | (8191 - row): descending order is longest
+  // first, then by row (rows < 8192, counts < 2^19 here)
+  extern __shared__ uint32_t keys[];
+  __shared__ uint32_t wave_part[kThreads / kWave];
+  __shared__ uint64_t wave_ids[kThreads / kWave];
   const uint32_t tid = threadIdx.x;
-  uint64_t sum = 0u;
-  for (uint32_t r = tid; r < a.rows; r += kThreads) {
-    if (a.dense_flag[r] != 0u) sum += a.row_meta[r].count;
-  }
+  const uint32_t lane = tid % kWave;
+  const uint32_t wave = tid / kWave;
+  // the candidates, compacted in row order: thread segments and a block scan
+  const uint32_t per = (a.rows + kThreads - 1u) / kThreads;
+  const uint32_t r0 = tid * per < a.rows ? tid * per : a.rows;
+  const uint32_t r1 = r0 + per < a.rows ? r0 + per : a.rows;
+  uint32_t local = 0u;
+  for (uint32_t r = r0; r < r1; ++r) local += a.dense_flag[r] != 0u ? 1u : 0u;
+  uint32_t incl = local;
 #pragma unroll
-  for (int m = kWave / 2; m > 0; m >>= 1) {
-    const uint32_t lo = static_cast<uint32_t>(__shfl_xor(static_cast<int>(sum & 0xFFFFFFFFu), m));
-    const uint32_t hi = static_cast<uint32_t>(__shfl_xor(static_cast<int>(sum >> 32), m));
-    sum += (static_cast<uint64_t>(hi) << 32) | lo;
+  for (int d = 1; d < kWave; d <<= 1) {
+    const uint32_t o = static_cast<uint32_t>(__shfl_up(static_cast<int>(incl), d));
+    if (static_cast<int>(lane) >= d) incl += o;
   }
-  if (tid % kWave == 0) wave_total[tid / kWave] = sum;
+  if (lane == kWave - 1) wave_part[wave] = incl;
   __syncthreads();
-  uint64_t total = 0u;
-  for (uint32_t w = 0; w < kThreads / kWave; ++w) total += wave_total[w];
-  const bool on = total > 0u && (a.dense_any != 0u || total >= a.dense_total);
-  if (!on) return;
-  for (uint32_t r = tid; r < a.rows; r += kThreads) {
-    if (a.dense_flag[r] != 0u) a.row_meta[r].kind |= kRowDense;
+  uint32_t at = incl - local;
+  uint32_t nc = 0u;
+  for (uint32_t w = 0; w < kThreads / kWave; ++w) {
+    at += w < wave ? wave_part[w] : 0u;
+    nc += wave_part[w];
+  }
+  if (nc == 0u) return;
+  for (uint32_t r = r0; r < r1; ++r) {
+    if (a.dense_flag[r] != 0u) keys[at++] = (a.row_meta[r].count << 13) | (8191u - r);
+  }
+  uint32_t n2 = 1u;
+  while (n2 < nc) n2 <<= 1;
+  for (uint32_t i = nc + tid; i < n2; i += kThreads) keys[i] = 0u;
+  __syncthreads();
+  // bitonic sort, descending: n2 / 2 compare-exchanges per stage
+  for (uint32_t k = 2; k <= n2; k <<= 1) {
+    for (uint32_t j = k >> 1; j > 0; j >>= 1) {
+      for (uint32_t p = tid; p < n2 / 2u; p += kThreads) {
+        const uint32_t i = (p / j) * 2u * j + (p % j);
+        const uint32_t l = i + j;
+        const uint32_t x = keys[i];
+        const uint32_t y = keys[l];
+        const bool descending = (i & k) == 0u;
+        if (descending ? x < y : x > y) {
+          keys[i] = y;
+          keys[l] = x;
+        }
+      }
+      __syncthreads();
+    }
+  }
+  // D: the free room of the unrestricted rows' panels, then whole panels
+  // while their lists hold enough ids
+  const uint32_t fb = a.dense_fb;
+  const uint32_t fb_panels = (fb + kDensePanelSlots - 1u) / kDensePanelSlots;
+  uint32_t D = fb_panels * kDensePanelSlots - fb;
+  D = D < nc ? D : nc;
+  while (D < nc) {
+    const uint32_t end = D + kDensePanelSlots < nc ? D + kDensePanelSlots : nc;
+    uint64_t ids = 0u;
+    for (uint32_t i = D + tid; i < end; i += kThreads) ids += keys[i] >> 13;
+#pragma unroll
+    for (int m = kWave / 2; m > 0; m >>= 1) {
+      const uint32_t lo = static_cast<uint32_t>(__shfl_xor(static_cast<int>(ids & 0xFFFFFFFFu), m));
+      const uint32_t hi = static_cast<uint32_t>(__shfl_xor(static_cast<int>(ids >> 32), m));
+      ids += (static_cast<uint64_t>(hi) << 32) | lo;
+    }
+    if (lane == 0) wave_ids[wave] = ids;
+    __syncthreads();
+    uint64_t total = 0u;
+    for (uint32_t w = 0; w < kThreads / kWave; ++w) total += wave_ids[w];
+    __syncthreads();
+    if (total < a.dense_panel_ids) break;
+    D = end;
+  }
+  for (uint32_t i = tid; i < D; i += kThreads) {
+    const uint32_t r = 8191u - (keys[i] & 8191u);
+    a.row_meta[r].kind |= kRowDense;
   }
 }
 
@@ -376,7 +441,8 @@ hipError_t launch_tail_norm(const TailNormArgs& args, hipStream_t stream) {
   hipLaunchKernelGGL(tail_norm_kernel, dim3(args.rows + slots + walks), dim3(threads),
                      norm_lds > walk_lds ? norm_lds : walk_lds, stream, args);
   if (args.dense_spans != nullptr) {
-    hipLaunchKernelGGL(dense_choose_kernel, dim3(1), dim3(kThreads), 0, stream, args);
+    hipLaunchKernelGGL(dense_choose_kernel, dim3(1), dim3(kThreads),
+                       static_cast<size_t>(args.dense_sort) * sizeof(uint32_t), stream, args);
   }
   return hipGetLastError();
 }
