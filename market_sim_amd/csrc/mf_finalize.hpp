@@ -167,29 +167,35 @@ __device__ __forceinline__ float records_lower(const FinalizeArgs& a, uint32_t r
   return q - __builtin_fabsf(q) * 0x1p-20f - 0x1p-126f;
 }
 
-// Finalizes row r (meta = its metadata) with one wave.  ys_ready: L.ys
-// already holds the row's normalized hidden vector (otherwise it is loaded
-// from a.y).  Writes token, score and next state of the row; rows that are
-// neither gathered nor served by the MFMA head are left alone (their outputs
-// were preset by the norm kernel).
+// Finalizes row r (meta = its metadata) with one wave.  stage_y() puts the
+// row's normalized hidden vector into L.ys; it is called once the record
+// headers are in flight, before the first rescore, so the caller can keep
+// the vector's loads in flight meanwhile.  Writes token, score and next
+// state of the row; rows that are neither gathered nor served by the MFMA
+// head are left alone (their outputs were preset by the norm kernel).
+template <typename StageY>
 __device__ inline void finalize_row(const FinalizeArgs& a, uint32_t r, const RowMeta& meta,
-                                    const FinalizeLds& L, bool ys_ready) {
+                                    const FinalizeLds& L, StageY&& stage_y) {
   const uint32_t lane = threadIdx.x % kWave;
   const TileRecord* recs;
   uint32_t ntiles;
+  // the per-row words the record pointer needs, loaded beside the metadata
+  // (not after it)
+  const uint32_t fb_slot = a.fb_map != nullptr ? a.fb_map[r] : kInvalidToken;
+  const uint32_t row_tiles = a.row_tiles != nullptr ? a.row_tiles[r] : 0u;
   if ((meta.kind & kRowDense) && a.fb_records != nullptr) {
     // scored by the dense head: its records, list positions of the row's
     // ascending list
-    const uint32_t m = a.fb_map[r];
+    const uint32_t m = fb_slot;
     if (m == kInvalidToken) return;
     recs = a.fb_records + static_cast<uint64_t>(m) * a.fb_tiles;
     ntiles = a.fb_tiles;
   } else if (meta.kind & kRowRestricted) {
     recs = a.records + static_cast<uint64_t>(r) * a.max_tiles;
-    ntiles = a.row_tiles != nullptr ? (a.row_tiles[r] & ~kRangesUnused)
+    ntiles = a.row_tiles != nullptr ? (row_tiles & ~kRangesUnused)
                                     : (meta.count + a.tile - 1) / a.tile;
   } else if ((meta.kind & kRowUnrestricted) && a.fb_records != nullptr) {
-    const uint32_t m = a.fb_map[r];
+    const uint32_t m = fb_slot;
     if (m == kInvalidToken) return;
     recs = a.fb_records + static_cast<uint64_t>(m) * a.fb_tiles;
     ntiles = a.fb_tiles;
@@ -199,17 +205,7 @@ __device__ inline void finalize_row(const FinalizeArgs& a, uint32_t r, const Row
   } else {
     return;
   }
-  if (!ys_ready) {
-    if ((a.H & 3u) == 0) {
-      copy16_to_lds<4>(reinterpret_cast<uint4*>(L.ys),
-                       reinterpret_cast<const uint4*>(a.y + static_cast<uint64_t>(r) * a.H),
-                       a.H / 4, lane, kWave);
-    } else {
-      for (uint32_t f = lane; f < a.H; f += kWave) L.ys[f] = a.y[static_cast<uint64_t>(r) * a.H + f];
-    }
-  }
   const bool virtual_list = meta.kind & kRowUnrestricted;
-  wave_sync();
   // pass 1: validity, the best lower bound of ordinary tiles, lowest id.
   // Per tile the header (best_lower, flags, min_token, min_pos), the counts
   // (begin, count, n_members) and the first member, kRecBlock tiles per lane
@@ -266,6 +262,8 @@ __device__ inline void finalize_row(const FinalizeArgs& a, uint32_t r, const Row
   const bool has_all = wave_sum_u32(any_all) != 0u;
   lg = wave_max(lg);
   wave_min_token(mt, mp);
+  stage_y();
+  wave_sync();
 
   // tiles that need every candidate rescored (non-finite values, crowded
   // windows): exact scores, which then also bound the window.  A crowded

@@ -405,6 +405,7 @@ __global__ __launch_bounds__(kThreads) void gather_planned_kernel(GatherArgs a) 
 constexpr uint32_t kStage = 8;  // embedding rows staged in LDS per rescore pass
 constexpr uint32_t kCandMax = 2 * kWave * kTileMembers;
 
+template <uint32_t kYRegs>
 __global__ __launch_bounds__(kWave) void finalize_kernel(FinalizeArgs a) {
   extern __shared__ __align__(16) float lds[];
   __shared__ uint32_t cand_token[kCandMax];
@@ -414,17 +415,35 @@ __global__ __launch_bounds__(kWave) void finalize_kernel(FinalizeArgs a) {
                       kCandMax, &words};
   const uint32_t r = blockIdx.x;
   const uint32_t lane = threadIdx.x;
-  // the loads that need nothing else go first: the row's hidden vector, then
-  // its metadata
-  if ((a.H & 3u) == 0) {
-    copy16_to_lds<4>(reinterpret_cast<uint4*>(L.ys),
-                     reinterpret_cast<const uint4*>(a.y + static_cast<uint64_t>(r) * a.H), a.H / 4,
-                     lane, kWave);
-  } else {
-    for (uint32_t f = lane; f < a.H; f += kWave) L.ys[f] = a.y[static_cast<uint64_t>(r) * a.H + f];
-  }
   const RowMeta meta = a.row_meta[r];
-  finalize_row(a, r, meta, L, true);
+  const float* yrow = a.y + static_cast<uint64_t>(r) * a.H;
+  if constexpr (kYRegs > 0) {
+    // rows of at most 256 kYRegs features: the hidden vector's loads stay
+    // in flight in registers while the record headers load; stored to LDS
+    // before the first rescore
+    float4 yv[kYRegs];
+    const uint32_t n4 = a.H / 4u;
+#pragma unroll
+    for (uint32_t u = 0; u < kYRegs; ++u) {
+      const uint32_t q = lane + u * kWave;
+      yv[u] = q < n4 ? reinterpret_cast<const float4*>(yrow)[q] : float4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    finalize_row(a, r, meta, L, [&]() {
+#pragma unroll
+      for (uint32_t u = 0; u < kYRegs; ++u) {
+        const uint32_t q = lane + u * kWave;
+        if (q < n4) reinterpret_cast<float4*>(L.ys)[q] = yv[u];
+      }
+    });
+  } else {
+    if ((a.H & 3u) == 0) {
+      copy16_to_lds<4>(reinterpret_cast<uint4*>(L.ys), reinterpret_cast<const uint4*>(yrow), a.H / 4,
+                       lane, kWave);
+    } else {
+      for (uint32_t f = lane; f < a.H; f += kWave) L.ys[f] = yrow[f];
+    }
+    finalize_row(a, r, meta, L, []() {});
+  }
 }
 
 } // namespace
@@ -491,7 +510,13 @@ hipError_t launch_gather(ScoreSource source, const GatherArgs& a, hipStream_t st
 hipError_t launch_finalize(const FinalizeArgs& a, hipStream_t stream) {
   const size_t lds = static_cast<size_t>(a.H) * sizeof(float) +
                      static_cast<size_t>(kStage) * a.H * sizeof(uint16_t);
-  hipLaunchKernelGGL(finalize_kernel, dim3(a.rows), dim3(kWave), lds, stream, a);
+  if (a.H % 4u == 0 && a.H <= 4u * kWave * 4u) {
+    hipLaunchKernelGGL(finalize_kernel<4>, dim3(a.rows), dim3(kWave), lds, stream, a);
+  } else if (a.H % 4u == 0 && a.H <= 4u * kWave * 8u) {
+    hipLaunchKernelGGL(finalize_kernel<8>, dim3(a.rows), dim3(kWave), lds, stream, a);
+  } else {
+    hipLaunchKernelGGL(finalize_kernel<0>, dim3(a.rows), dim3(kWave), lds, stream, a);
+  }
   return hipGetLastError();
 }
 
