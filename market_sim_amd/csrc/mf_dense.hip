@@ -358,22 +358,25 @@ __global__ __launch_bounds__(kThreads) void dense_kernel(DenseArgs a) {
   #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const uint32_t w[3] = {w4[q].x, w4[q].y, w4[q].z};
+          // arithmetic form (one condition per select, no lane-mask logic):
+          // va = the score or -inf, vb - vb is NaN exactly when an allowed score is
+          // not finite
           float m1 = -__builtin_huge_valf();
           float m2 = -__builtin_huge_valf();
+          float badacc = 0.0f;
           uint32_t j1 = 0u;
-          bool bad = false;
-  #pragma unroll
+#pragma unroll
           for (int j = 0; j < kTBw; ++j) {
             const bool allowed = (w[j / 2] & (j % 2 == 0 ? sel0 : sel1)) != 0u;
             const float v = acc[i][j][q];
-            bad |= allowed && !__builtin_isfinite(v);
-            const bool top = allowed && v > m1;
-            const bool second = allowed && !top && v > m2;
-            m2 = top ? m1 : (second ? v : m2);
-            j1 = top ? static_cast<uint32_t>(j) : j1;
-            m1 = top ? v : m1;
+            const float va = allowed ? v : -__builtin_huge_valf();
+            const float vb = allowed ? v : 0.0f;
+            badacc += vb - vb;
+            m2 = __builtin_fmaxf(m2, __builtin_fminf(m1, va));
+            j1 = va > m1 ? static_cast<uint32_t>(j) : j1;
+            m1 = __builtin_fmaxf(m1, va);
           }
-          gl1[lw + (32 * i + q) * kEpiRow] = bad ? __builtin_nanf("") : m1;
+          gl1[lw + (32 * i + q) * kEpiRow] = badacc != badacc ? __builtin_nanf("") : m1;
           gl2[lw + (32 * i + q) * kEpiRow] = m2;
           glj[lw + (32 * i + q) * kEpiRow] = static_cast<uint8_t>(j1);
         }
