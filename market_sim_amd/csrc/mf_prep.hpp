@@ -443,7 +443,7 @@ __device__ inline void dense_walk(const TailNormArgs& a, uint32_t r, uint32_t* l
     const uint32_t b = w.b;
     const uint32_t c = w.c;
     bool bad = false;
-    constexpr uint32_t kU = 4;  // loads in flight per thread
+    constexpr uint32_t kU = 16;  // loads in flight per thread
     for (uint32_t base = tid; base < c; base += kT * kU) {
       uint32_t t[kU], tp[kU];
 #pragma unroll
