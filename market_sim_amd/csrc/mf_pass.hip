@@ -74,6 +74,19 @@ static_assert(kPassRowsMax <= 256u && kPairBatch <= kNoPair, "bucket entry field
 __device__ __forceinline__ uint32_t pair_pack(uint32_t slot, uint32_t k, uint32_t c, uint32_t r) {
   return slot | (k << 8) | (c << 18) | (r << 22);
 }
+// A staged slot's class: slot % 8.  With the slot stride of the panel's
+// rows (2 mod 4 bank groups of 16 bytes), the A reads of one K offset by the
+// lanes of columns 0-3 and 12-15 of a group meet no bank conflict when their
+// slots have distinct classes, and the same for columns 4-11 (the lanes one
+// ds_read_b128 cycle serves); the buckets deal each block's candidates so
+// that those two halves of a group hold distinct classes wherever the counts
+// allow.
+constexpr uint32_t kSlotClasses = 8;
+// column of entry i (0..7) of half h of a group: h = 0 takes columns 0-3,
+// 12-15, h = 1 columns 4-11
+__device__ __forceinline__ uint32_t half_col(uint32_t h, uint32_t i) {
+  return h == 0u ? (i < 4u ? i : i + 8u) : 4u + i;
+}
 // Per-row flags of a batch: bit 31 = the record is rescored in full; the low
 // bits count the members.
 constexpr uint32_t kRowAll = 0x80000000u;
@@ -111,10 +124,11 @@ struct alignas(16) PassShared {
   uint32_t row_flags[kPassRowsMax];     // kRowAll | members
   uint32_t ptok[kPairBatch];            // candidate k of the batch: id, g + b, row
   float pupper[kPairBatch];             // (+inf: not scored)
+  float pscore[kPairBatch];             // candidate k's fast score
   uint16_t prow[kPairBatch];
-  uint32_t bent[kBucketSlots];
-  uint32_t bcount[kHeadTileBlocks];
-  uint32_t bfill[kHeadTileBlocks];
+  alignas(16) uint32_t bent[kBucketSlots];  // read 16 bytes at a time
+  uint32_t bcount[kHeadTileBlocks * kSlotClasses];  // candidates per (block, slot class)
+  uint32_t bfill[kHeadTileBlocks * kSlotClasses];   // rank of the class's next candidate
   uint32_t bstart[kHeadTileBlocks + 1];  // padded bucket starts (multiples of 16)
   uint32_t wave_n[kWaves];
   uint32_t wave_h[kWaves];
@@ -162,7 +176,7 @@ __device__ __forceinline__ uint32_t last_within(const uint32_t* v, uint32_t rows
 // Copies `n` FP16 rows of H halves into LDS slots (slot_bytes(H) each),
 // wave w taking the 1 KiB copies w, w + 4, ...: piece q of the area is 16
 // bytes of slot q / per at offset q % per; src(i) is slot i's row.  The pad
-// piece and the lanes past the last piece read piece 0 of a staged row.
+// pieces and the lanes past the last piece read piece 0 of a staged row.
 template <uint32_t H, typename Src>
 __device__ __forceinline__ void stage_rows(unsigned char* area, uint32_t n, Src src) {
   constexpr uint32_t per = slot_bytes(H) / 16u;
@@ -173,7 +187,7 @@ __device__ __forceinline__ void stage_rows(unsigned char* area, uint32_t n, Src 
     const uint32_t q = c * kWave + lane;
     const uint32_t i = q < pieces ? q / per : 0u;
     const uint32_t pp = q < pieces ? q % per : 0u;
-    burst_to_lds(src(i) + (pp < per - 1u ? pp : 0u) * 8u, area + c * kWave * 16u);
+    burst_to_lds(src(i) + (pp < H / 8u ? pp : 0u) * 8u, area + c * kWave * 16u);
   }
 }
 
@@ -204,7 +218,7 @@ __device__ __forceinline__ void stage_rows_batched(unsigned char* area, uint32_t
     for (uint32_t u = 0; u < kRound; ++u) {
       const uint32_t c = c0 + u * kWaves;
       if (c < copies) {
-        burst_to_lds(z + static_cast<uint64_t>(rr[u]) * H + (pp[u] < per - 1u ? pp[u] : 0u) * 8u,
+        burst_to_lds(z + static_cast<uint64_t>(rr[u]) * H + (pp[u] < H / 8u ? pp[u] : 0u) * 8u,
                      area + c * kWave * 16u);
       }
     }
@@ -291,9 +305,6 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
     }
   };
 
-  constexpr int kWarm = 4;  // 16-byte loads per lane and array (16 KiB of each per workgroup)
-  uint32_t warm[2][kWarm] = {};
-
   for (uint32_t tile = t_begin; tile < t_end; ++tile) {
     const uint32_t t0 = tile * kHeadTileTokens;
     // (1) the small loads first, ahead of the table's: the plan's per-row
@@ -307,29 +318,6 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
     const float slack_r = p.row_slack[ri];
     // panel tile 0's slots (stored once the plan has landed)
     const HeadSlotLoad slot0 = head_slot_load(f, 0u, p.row_norm);
-    __builtin_amdgcn_sched_barrier(0);
-    {
-      // Warm this XCD's L2 with the rows of z and the head's panel, which
-      // the norm kernel wrote just before (from every XCD): workgroup i
-      // runs on XCD i % 8, and the 32 workgroups of an XCD each touch a
-      // 32nd of both, so that the staging copies below hit L2 instead of
-      // queueing 32 misses per line at the last-level cache.  Issued after
-      // the plan's loads (which do not wait for them), every tile (no
-      // branch around loads); the values are not used.
-      const uint32_t share = (blockIdx.x / 8u) % 32u;
-      auto touch = [&](const uint16_t* base, uint64_t bytes, uint32_t (&w)[kWarm]) {
-        const uint64_t part = (bytes / 32u + 1023u) & ~uint64_t{1023u};
-        const unsigned char* b = reinterpret_cast<const unsigned char*>(base);
-#pragma unroll
-        for (int u = 0; u < kWarm; ++u) {
-          const uint64_t o = share * part + (static_cast<uint64_t>(u) * kThreads + tid) * 16u;
-          w[u] = *reinterpret_cast<const uint32_t*>(b + (o + 16u <= bytes ? o : 0u));
-        }
-      };
-      touch(p.z_hi, static_cast<uint64_t>(rows) * H * 2u, warm[0]);
-      touch(panels > 0u ? f.panel : p.z_hi,
-            panels > 0u ? static_cast<uint64_t>(panels) * panel_tile_bytes(H) : 16u, warm[1]);
-    }
     __builtin_amdgcn_sched_barrier(0);
     // the tile's first block of table rows, behind the small loads: it
     // streams while the plan is scanned and the rows of z are staged
@@ -411,10 +399,7 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
       const uint32_t nb = ps.prefix[r1] - k0;
       const uint32_t s0 = ps.rprefix[r0];
       const uint32_t nz = ps.rprefix[r1] - s0;
-      if (tid < kHeadTileBlocks) {
-        ps.bcount[tid] = 0u;
-        ps.bfill[tid] = 0u;
-      }
+      if (tid < kHeadTileBlocks * kSlotClasses) ps.bcount[tid] = 0u;
       if (tid >= r0 && tid < r1) {
         const uint32_t n = ps.count[tid];
         if (n > 0u) {
@@ -464,38 +449,63 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
       __builtin_amdgcn_sched_barrier(0);
       // buckets: each candidate in its 16-token block's bucket
       uint32_t blk[2];
+      uint32_t slot[2];
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         const uint32_t k = k0 + tid + u * kThreads;
         const uint32_t c = tok[u] - t0;
         blk[u] = (k < k0 + nb && c < kHeadTileTokens) ? c / 16u : kHeadTileBlocks;
+        slot[u] = ps.rprefix[row[u]] - s0;
         if (k < k0 + nb) {
           ps.ptok[k - k0] = tok[u];
           ps.pupper[k - k0] = __builtin_huge_valf();
           if (blk[u] < kHeadTileBlocks) {
-            atomicAdd(&ps.bcount[blk[u]], 1u);
+            atomicAdd(&ps.bcount[blk[u] * kSlotClasses + slot[u] % kSlotClasses], 1u);
           } else {
             atomicOr(&ps.row_flags[row[u]], kRowAll);  // an id outside the tile: rescore in full
           }
         }
       }
       __syncthreads();
-      if (tid == 0) {
-        uint32_t run = 0u;
-        for (uint32_t b = 0; b < kHeadTileBlocks; ++b) {
-          ps.bstart[b] = run;
-          run += (ps.bcount[b] + 15u) & ~15u;
+      if (wave == 0) {
+        // lane b < 12: block b's classes in order (each class's first rank
+        // into bfill), its padded size, and an exclusive scan over blocks
+        uint32_t n = 0u;
+        if (lane < kHeadTileBlocks) {
+          uint32_t c[kSlotClasses];
+#pragma unroll
+          for (uint32_t q = 0; q < kSlotClasses; ++q) c[q] = ps.bcount[lane * kSlotClasses + q];
+#pragma unroll
+          for (uint32_t q = 0; q < kSlotClasses; ++q) {
+            ps.bfill[lane * kSlotClasses + q] = n;
+            n += c[q];
+          }
         }
-        ps.bstart[kHeadTileBlocks] = run;
+        const uint32_t padded = (n + 15u) & ~15u;
+        uint32_t incl = padded;
+#pragma unroll
+        for (int d = 1; d < 16; d <<= 1) {
+          const uint32_t o = static_cast<uint32_t>(__shfl_up(static_cast<int>(incl), d));
+          if (static_cast<int>(lane) >= d) incl += o;
+        }
+        if (lane < kHeadTileBlocks) ps.bstart[lane] = incl - padded;
+        if (lane == kHeadTileBlocks - 1) ps.bstart[kHeadTileBlocks] = incl;
       }
       for (uint32_t e = tid; e < kBucketSlots; e += kThreads) ps.bent[e] = pair_pack(0u, kNoPair, 0u, 0u);
       __syncthreads();
+      // rank k of a candidate in its block (classes in order); the block's
+      // P = size / 8 halves of groups take ranks k = j, j + P, ...: half
+      // j = k % P is half j % 2 of group j / 2, entry k / P in it
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         if (blk[u] < kHeadTileBlocks) {
-          const uint32_t at = ps.bstart[blk[u]] + atomicAdd(&ps.bfill[blk[u]], 1u);
+          const uint32_t k = atomicAdd(&ps.bfill[blk[u] * kSlotClasses + slot[u] % kSlotClasses], 1u);
+          const uint32_t b0 = ps.bstart[blk[u]];
+          const uint32_t P = (ps.bstart[blk[u] + 1] - b0) / 8u;
+          const uint32_t j = k % P;
+          const uint32_t at = b0 + (j / 2u) * 16u + half_col(j % 2u, k / P);
           const uint32_t r = row[u];
-          ps.bent[at] = pair_pack(ps.rprefix[r] - s0, tid + u * kThreads, (tok[u] - t0) % 16u, r);
+          ps.bent[at] = pair_pack(slot[u], tid + u * kThreads, (tok[u] - t0) % 16u, r);
         }
       }
       __syncthreads();  // buckets and staged rows visible
@@ -506,48 +516,29 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
       // A block's groups run as a software pipeline over two halves of the
       // K range: while the MFMAs of one half run, the other half's A rows
       // (the next group's first half, or this group's second) are read from
-      // LDS, and the previous group's epilogue (its candidates' scores out
-      // of the accumulators, bounds, LDS atomics) runs between this group's
-      // halves, after its MFMAs had a whole half to finish.  Reads of a group
-      // past the block's last re-read the last group (no branch around LDS
-      // reads, whose waits the compiler counts in order).
+      // LDS, and the previous group's scores leave the accumulators between
+      // this group's halves, after its MFMAs had a whole half to finish.
+      // The loop holds no wait but the ones for its A rows: a lane holds
+      // D[i][lane % 16] for the four candidates i = 4 (lane / 16) + e (one
+      // 16-byte read of their bucket entries), and writes the element whose
+      // candidate's column is lane % 16 to pscore; bounds and row maxima
+      // follow once every block is scored.  Reads of a group past the
+      // block's last re-read the last group (no branch around LDS reads,
+      // whose waits the compiler counts in order).
       constexpr int kHalf = (kSteps + 1) / 2;
-      struct Pending {
-        floatx4 acc;
-        uint32_t ge;
-        float tnv, f1, f2;
-      };
-      // candidate i = lane (lanes 0..15): D[i][c] sits in lane
-      // 16 (i / 4) + c, element i % 4
-      auto epilogue = [&](const Pending& pd) {
-        const floatx4 acc = pd.acc;
-        const uint32_t k = (pd.ge >> 8) & 0x3FFu;
-        const uint32_t c = (pd.ge >> 18) & 15u;
-        const uint32_t r = pd.ge >> 22;
-        const bool mine = lane < 16u && k != kNoPair;
-        const int src = lane < 16u ? static_cast<int>(16u * (lane / 4u) + c) : static_cast<int>(lane);
-        const float v0 = __shfl(acc[0], src);
-        const float v1 = __shfl(acc[1], src);
-        const float v2 = __shfl(acc[2], src);
-        const float v3 = __shfl(acc[3], src);
-        if (mine) {
-          const uint32_t e = lane % 4u;
-          const float gs = e == 0u ? v0 : (e == 1u ? v1 : (e == 2u ? v2 : v3));
-          const float bnd = __builtin_fmaf(pd.tnv, pd.f1, pd.f2);
-          const bool ok = __builtin_isfinite(gs) && __builtin_isfinite(bnd) && bnd < 0x1p100f;
-          if (ok) {
-            atomicMax(&ps.row_lower[r], order_bits(gs - bnd));
-            atomicMax(&ps.row_upper[r], order_bits(gs + bnd));
-            ps.pupper[k] = gs + bnd;
-          } else {
-            atomicOr(&ps.row_flags[r], kRowAll);
-          }
+      auto dump = [&](const floatx4& acc, const uint4& gq) {
+        const uint32_t g[4] = {gq.x, gq.y, gq.z, gq.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t k = (g[e] >> 8) & 0x3FFu;
+          if (k != kNoPair && ((g[e] >> 18) & 15u) == col) ps.pscore[k] = acc[e];
         }
       };
-      auto score_block = [&](const half8_t(&b)[kSteps], uint32_t blk_id, uint32_t qa, uint32_t qz) {
+      auto score_block = [&](const half8_t(&b)[kSteps], uint32_t qa, uint32_t qz) {
         half8_t a0[kHalf];
         half8_t a1[kHalf];
         auto a_src = [&](uint32_t ge) { return stage + (ge & 0xFFu) * kSlot + kb * 16u; };
+        auto entries = [&](uint32_t q) { return *reinterpret_cast<const uint4*>(&ps.bent[q * 16u + 4u * kb]); };
         auto read_half = [&](half8_t(&dst)[kHalf], const unsigned char* from, int h0) {
 #pragma unroll
           for (int s = 0; s < kHalf; ++s) {
@@ -561,35 +552,36 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
           }
         };
         uint32_t ge = ps.bent[qa * 16u + col];
+        uint4 gq = entries(qa);
         const unsigned char* from = a_src(ge);
         read_half(a0, from, 0);
-        // nothing pending yet: an entry without a candidate
-        Pending pd{{0.0f, 0.0f, 0.0f, 0.0f}, pair_pack(0u, kNoPair, 0u, 0u), 0.0f, 0.0f, 0.0f};
+        // nothing pending yet: entries without a candidate
+        floatx4 pacc = {0.0f, 0.0f, 0.0f, 0.0f};
+        const uint32_t none = pair_pack(0u, kNoPair, 0u, 0u);
+        uint4 pq = {none, none, none, none};
         for (uint32_t q = qa; q < qz; ++q) {
           const uint32_t qn = q + 1u < qz ? q + 1u : q;
           const uint32_t ge_n = ps.bent[qn * 16u + col];
-          const uint32_t c = (ge >> 18) & 15u;
-          const uint32_t r = ge >> 22;
-          const float tnv = ps.tn[blk_id * 16u + c];
-          const float f1 = ps.rf1[r];
-          const float f2 = ps.rf2[r];
+          const uint4 gq_n = entries(qn);
           read_half(a1, from, kHalf);
           __builtin_amdgcn_sched_barrier(0);
           floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
           mfma_half(a0, 0, acc);
           __builtin_amdgcn_sched_barrier(0);
-          epilogue(pd);
+          dump(pacc, pq);
           __builtin_amdgcn_sched_barrier(0);
           const unsigned char* from_n = a_src(ge_n);
           read_half(a0, from_n, 0);
           __builtin_amdgcn_sched_barrier(0);
           mfma_half(a1, kHalf, acc);
           __builtin_amdgcn_sched_barrier(0);
-          pd = Pending{acc, ge, tnv, f1, f2};
+          pacc = acc;
+          pq = gq;
           ge = ge_n;
+          gq = gq_n;
           from = from_n;
         }
-        epilogue(pd);
+        dump(pacc, pq);
       };
 #pragma unroll
       for (int tb = 0; tb < kBlocks; ++tb) {
@@ -611,7 +603,7 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
         }
         const uint32_t qa = __builtin_amdgcn_readfirstlane(ps.bstart[blk_id] / 16u);
         const uint32_t qz = __builtin_amdgcn_readfirstlane(ps.bstart[blk_id + 1] / 16u);
-        if (qa < qz) score_block(bt[tb], blk_id, qa, qz);
+        if (qa < qz) score_block(bt[tb], qa, qz);
         if constexpr (first) {
           if (tb == 0) {
             __builtin_amdgcn_sched_barrier(0);
@@ -625,6 +617,32 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
       // written
       const bool last = r1 >= rows || nb == 0u;
       if (last && panels > 0u) stage_panel(0u);
+
+      // each candidate's bound (the token's norm bound, the row's terms),
+      // its row's maxima of g - b and g + b (order-preserving integer bits);
+      // a non-finite score or bound marks the record "rescore all".  An id
+      // outside the tile was never scored (its row is rescored in full).
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const uint32_t kk = tid + u * kThreads;
+        if (kk < nb) {
+          const uint32_t c = ps.ptok[kk] - t0;
+          if (c < kHeadTileTokens) {
+            const uint32_t r = ps.prow[kk];
+            const float gs = ps.pscore[kk];
+            const float bnd = __builtin_fmaf(ps.tn[c], ps.rf1[r], ps.rf2[r]);
+            const bool ok = __builtin_isfinite(gs) && __builtin_isfinite(bnd) && bnd < 0x1p100f;
+            if (ok) {
+              atomicMax(&ps.row_lower[r], order_bits(gs - bnd));
+              atomicMax(&ps.row_upper[r], order_bits(gs + bnd));
+              ps.pupper[kk] = gs + bnd;
+            } else {
+              atomicOr(&ps.row_flags[r], kRowAll);
+            }
+          }
+        }
+      }
+      __syncthreads();
 
       // (5) one window record per (row, tile).  The best lower bound came
       // from the scoring; each candidate then checks itself against its
@@ -690,10 +708,6 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
                                           pt * kPanelRows, tile, tiles);
     }
   }
-  uint32_t warm_all = 0u;
-#pragma unroll
-  for (int u = 0; u < kWarm; ++u) warm_all ^= warm[0][u] ^ warm[1][u];
-  asm volatile("" ::"v"(warm_all));  // keeps the warming loads
 }
 
 template <int kSteps>
