@@ -13,6 +13,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <stddef.h>
 #include <stdint.h>
 
 namespace mf {
@@ -339,6 +340,10 @@ struct alignas(16) TileRecord {
   float upper_max;    // max of g + b over the tile (kTileCrowded)
   TileMember m[kTileMembers];
 };
+// the header is written and read as two 16-byte words
+static_assert(offsetof(TileRecord, best_lower) == 0 && offsetof(TileRecord, min_pos) == 12 &&
+                  offsetof(TileRecord, begin) == 16 && offsetof(TileRecord, upper_max) == 28,
+              "tile record header layout");
 
 // Copies n 16-byte pieces from global memory to LDS with `lanes` threads
 // (this one is `tid`), kBatch loads per thread in flight before their stores:

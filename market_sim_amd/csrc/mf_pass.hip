@@ -676,14 +676,13 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
         const bool ordinary = !all && members <= static_cast<uint32_t>(kTileMembers);
         TileRecord* rec = p.records + static_cast<uint64_t>(r) * p.max_recs + ps.rec[r];
         const uint32_t lo = ps.lo[r];
-        rec->best_lower = from_order_bits(ps.row_lower[r]);
-        rec->flags = ordinary ? 0u : (all ? kTileRescoreAll : kTileRescoreAll | kTileCrowded);
-        rec->upper_max = from_order_bits(ps.row_upper[r]);
-        rec->min_token = ps.ptok[ps.prefix[r] - k0];
-        rec->min_pos = lo;
-        rec->begin = lo;
-        rec->count = n;
-        rec->n_members = ordinary ? members : 0u;
+        // the header in two 16-byte stores: {best_lower, flags, min_token,
+        // min_pos} and {begin, count, n_members, upper_max}
+        uint4* hd = reinterpret_cast<uint4*>(rec);
+        hd[0] = uint4{__float_as_uint(from_order_bits(ps.row_lower[r])),
+                      ordinary ? 0u : (all ? kTileRescoreAll : kTileRescoreAll | kTileCrowded),
+                      ps.ptok[ps.prefix[r] - k0], lo};
+        hd[1] = uint4{lo, n, ordinary ? members : 0u, __float_as_uint(from_order_bits(ps.row_upper[r]))};
       }
       __syncthreads();  // the batch's LDS is free again
       r0 = r1;
