@@ -564,17 +564,12 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
           const uint32_t ge_n = ps.bent[qn * 16u + col];
           const uint4 gq_n = entries(qn);
           read_half(a1, from, kHalf);
-          __builtin_amdgcn_sched_barrier(0);
           floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
           mfma_half(a0, 0, acc);
-          __builtin_amdgcn_sched_barrier(0);
           dump(pacc, pq);
-          __builtin_amdgcn_sched_barrier(0);
           const unsigned char* from_n = a_src(ge_n);
           read_half(a0, from_n, 0);
-          __builtin_amdgcn_sched_barrier(0);
           mfma_half(a1, kHalf, acc);
-          __builtin_amdgcn_sched_barrier(0);
           pacc = acc;
           pq = gq;
           ge = ge_n;
