@@ -494,7 +494,7 @@ __device__ void summarize_block(const HeadArgs& a, Y ys, HeadShared& sh, uint32_
 // L never exceeds the row's best exact score, so no stage drops the winner.
 // All threads must call; every thread gets the record.
 template <typename Y>
-__device__ Record merge_records(const HeadArgs& a, Y ys, HeadShared& sh, uint32_t n) {
+__device__ __forceinline__ Record merge_records(const HeadArgs& a, Y ys, HeadShared& sh, uint32_t n) {
   const int tid = threadIdx.x;
   uint32_t inv = 0u;
   float lo = -__builtin_huge_valf();
@@ -532,7 +532,7 @@ __device__ Record merge_records(const HeadArgs& a, Y ys, HeadShared& sh, uint32_
 
 // Merges the row's records (sh.recs[0, n)) and writes its outputs.
 template <typename Y>
-__device__ void finalize_row(const HeadArgs& a, uint32_t r, Y ys, HeadShared& sh, uint32_t n) {
+__device__ __forceinline__ void finalize_row(const HeadArgs& a, uint32_t r, Y ys, HeadShared& sh, uint32_t n) {
   const Record m = merge_records(a, ys, sh, n);
   if (threadIdx.x == 0) {
     uint32_t token = kInvalidToken;
