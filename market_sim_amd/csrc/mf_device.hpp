@@ -16,6 +16,32 @@
 #include <stddef.h>
 #include <stdint.h>
 
+// Phase timeline of a kernel (builds with -DMF_PASS_TIMELINE only): lane 0
+// of each wave stores the real-time counter (100 MHz) at phase k into
+// mf_timeline[(workgroup * 4 + wave) * 32 + k] (an array of the translation
+// unit's own); MF_STAMP_VALUE records a value there instead.  Without the
+// macro both are nothing.
+#ifdef MF_PASS_TIMELINE
+#define MF_STAMP(k)                                                                   \
+  do {                                                                                \
+    if (threadIdx.x % 64u == 0u)                                                      \
+      mf_timeline[(blockIdx.x * 4u + threadIdx.x / 64u) * 32u + (k)] =                \
+          __builtin_amdgcn_s_memrealtime();                                           \
+  } while (0)
+#define MF_STAMP_VALUE(k, v)                                                          \
+  do {                                                                                \
+    if (threadIdx.x % 64u == 0u)                                                      \
+      mf_timeline[(blockIdx.x * 4u + threadIdx.x / 64u) * 32u + (k)] = (v);           \
+  } while (0)
+#else
+#define MF_STAMP_VALUE(k, v) \
+  do {                       \
+  } while (0)
+#define MF_STAMP(k) \
+  do {              \
+  } while (0)
+#endif
+
 namespace mf {
 
 constexpr uint32_t kInvalidToken = 0xFFFFFFFFu;

@@ -55,6 +55,14 @@
 #include "mf_head.hpp"
 #include "mf_launch.hpp"
 
+#ifdef MF_PASS_TIMELINE
+static __device__ unsigned long long mf_timeline[1024 * 4 * 32];
+extern "C" int mf_debug_pass_timeline(void* dst, unsigned long bytes) {
+  return static_cast<int>(hipMemcpyFromSymbol(dst, HIP_SYMBOL(mf_timeline), bytes, 0,
+                                              hipMemcpyDeviceToHost));
+}
+#endif
+
 namespace mf {
 namespace {
 
@@ -305,6 +313,7 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
     }
   };
 
+  MF_STAMP(0);
   for (uint32_t tile = t_begin; tile < t_end; ++tile) {
     const uint32_t t0 = tile * kHeadTileTokens;
     // (1) the small loads first, ahead of the table's: the plan's per-row
@@ -323,6 +332,7 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
     // streams while the plan is scanned and the rows of z are staged
     load_block(tile, 0);
     __builtin_amdgcn_sched_barrier(0);
+    MF_STAMP(1);
 
     // (2) per row its span [lo, hi) in the tile; exclusive scans over the
     // rows: candidates and rows with candidates
@@ -375,6 +385,7 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
       }
       __syncthreads();
     }
+    MF_STAMP(2);
 
     // (3) batches of whole rows.  The first is scored block by block as the
     // table rows land; the others (rows past the LDS stage) afterwards.
@@ -416,6 +427,7 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
         ps.row_flags[tid] = 0u;
       }
       __syncthreads();  // slot rows, candidate rows, cleared counters
+      if constexpr (first) MF_STAMP(3);
       // the batch's rows of z straight into LDS (block 0 of the table rows
       // streams ahead of them), then its candidate ids (lanes past the
       // batch load candidate k0 again, a valid list position, instead of
@@ -439,14 +451,17 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
 #pragma unroll
       for (int u = 0; u < 2; ++u) tok[u] = p.tokens[at[u]];
       __builtin_amdgcn_sched_barrier(0);
+      if constexpr (first) MF_STAMP(4);
       // every load has landed (block 0, the staged rows, the ids: a wait the
       // compiler sees, so that it counts the later table loads in order);
       // first batch: block 1 (it streams while block 0 is scored; block 2 is
       // issued once block 0 is scored)
       __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
       __builtin_amdgcn_sched_barrier(0);
+      if constexpr (first) MF_STAMP(5);
       if constexpr (first) load_block(tile, 1);
       __builtin_amdgcn_sched_barrier(0);
+      if constexpr (first) MF_STAMP(16);
       // buckets: each candidate in its 16-token block's bucket
       uint32_t blk[2];
       uint32_t slot[2];
@@ -467,6 +482,7 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
         }
       }
       __syncthreads();
+      if constexpr (first) MF_STAMP(17);
       if (wave == 0) {
         // lane b < 12: block b's classes in order (each class's first rank
         // into bfill), its padded size, and an exclusive scan over blocks
@@ -493,6 +509,7 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
       }
       for (uint32_t e = tid; e < kBucketSlots; e += kThreads) ps.bent[e] = pair_pack(0u, kNoPair, 0u, 0u);
       __syncthreads();
+      if constexpr (first) MF_STAMP(18);
       // rank k of a candidate in its block (classes in order); the block's
       // P = size / 8 halves of groups take ranks k = j, j + P, ...: half
       // j = k % P is half j % 2 of group j / 2, entry k / P in it
@@ -509,6 +526,7 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
         }
       }
       __syncthreads();  // buckets and staged rows visible
+      if constexpr (first) MF_STAMP(6);
 
       // (4) this wave's blocks in landing order: token norms (first batch),
       // the candidates 16 at a time, the next block's rows (first batch)
@@ -599,19 +617,23 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
         const uint32_t qa = __builtin_amdgcn_readfirstlane(ps.bstart[blk_id] / 16u);
         const uint32_t qz = __builtin_amdgcn_readfirstlane(ps.bstart[blk_id + 1] / 16u);
         if (qa < qz) score_block(bt[tb], qa, qz);
+        if constexpr (first) MF_STAMP(7 + tb);
         if constexpr (first) {
           if (tb == 0) {
             __builtin_amdgcn_sched_barrier(0);
             load_block(tile, 2);
             __builtin_amdgcn_sched_barrier(0);
+            MF_STAMP(22);
           }
         }
       }
       __syncthreads();  // every candidate scored; the staging area is free
+      if constexpr (first) MF_STAMP(10);
       // the last batch: panel tile 0's hi rows land while the records are
       // written
       const bool last = r1 >= rows || nb == 0u;
       if (last && panels > 0u) stage_panel(0u);
+      if constexpr (first) MF_STAMP(20);
 
       // each candidate's bound (the token's norm bound, the row's terms),
       // its row's maxima of g - b and g + b (order-preserving integer bits);
@@ -638,6 +660,7 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
         }
       }
       __syncthreads();
+      if constexpr (first) MF_STAMP(11);
 
       // (5) one window record per (row, tile).  The best lower bound came
       // from the scoring; each candidate then checks itself against its
@@ -680,6 +703,7 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
         hd[1] = uint4{lo, n, ordinary ? members : 0u, __float_as_uint(from_order_bits(ps.row_upper[r]))};
       }
       __syncthreads();  // the batch's LDS is free again
+      if constexpr (first) MF_STAMP(12);
       r0 = r1;
       return r0 < rows && nb > 0u;
     };
@@ -697,11 +721,14 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
       }
       wait_vector_memory();
       __syncthreads();
+      MF_STAMP(13);
       head_lds(h);
+      MF_STAMP(14);
       head_records<kWaves, kBlocks, true>(f, h, epi, src_row, src_norm, src_slack,
                                           pt * kPanelRows, tile, tiles);
     }
   }
+  MF_STAMP(15);
 }
 
 template <int kSteps>
