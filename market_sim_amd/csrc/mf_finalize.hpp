@@ -85,12 +85,86 @@ __device__ float chain_lds(const float* ys, const uint16_t* row, uint32_t H) {
   return s;
 }
 
-// Rescores candidates cand_token[0..n) of one row in the reference order,
-// stage_rows rows at a time staged in LDS; returns the wave's best.
+// The value of lane l - 1 in lane l (DPP wavefront shift right by one;
+// lane 0 keeps its own).
+__device__ __forceinline__ float lane_shift_right(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x138,
+                                                    0xF, 0xF, false));
+}
+
+// Reference-order scores with the operands in registers.  Features are cut
+// into segments of kChainSeg; with nseg = H / kChainSeg segments, lane
+// nseg c + k holds segment k of y and of candidate c's table row (FP32), so
+// 64 / nseg candidates are scored at once.  The chain runs segment by
+// segment: the lanes holding segment k take their kChainSeg steps from
+// registers, then every value moves one lane up, which hands each partial
+// sum to the lane holding the next segment of the same candidate.  The
+// steps and their order are those of the reference chain; only the place of
+// the running sum changes.  Candidate c's score ends in lane nseg c + nseg - 1.
+constexpr uint32_t kChainSeg = 64;
+template <bool kMulAdd>
+__device__ __forceinline__ Best rescore_segmented(const FinalizeArgs& a, const FinalizeLds& L,
+                                                  uint32_t n) {
+  const uint32_t lane = threadIdx.x % kWave;
+  const uint32_t H = a.H;
+  const uint32_t nseg = H / kChainSeg;
+  const uint32_t per_pass = kWave / nseg;
+  const uint32_t c = lane / nseg;
+  const uint32_t k = lane % nseg;
+  Best best = best_identity();
+  for (uint32_t base = 0; base < n; base += per_pass) {
+    const uint32_t m = n - base < per_pass ? n - base : per_pass;
+    const bool active = c < m;
+    const uint32_t j = base + (active ? c : 0u);
+    const uint32_t token = L.cand_token[j];
+    // segment k of the table row (global) and of y (LDS)
+    const uint4* e4 = reinterpret_cast<const uint4*>(a.emb + static_cast<uint64_t>(token) * H + k * kChainSeg);
+    uint4 ep[kChainSeg / 8];
+#pragma unroll
+    for (uint32_t q = 0; q < kChainSeg / 8; ++q) ep[q] = e4[q];
+    const float4* y4 = reinterpret_cast<const float4*>(L.ys + k * kChainSeg);
+    float yv[kChainSeg];
+#pragma unroll
+    for (uint32_t q = 0; q < kChainSeg / 4; ++q) {
+      const float4 v = y4[q];
+      yv[4 * q] = v.x;
+      yv[4 * q + 1] = v.y;
+      yv[4 * q + 2] = v.z;
+      yv[4 * q + 3] = v.w;
+    }
+    float ev[kChainSeg];
+#pragma unroll
+    for (uint32_t q = 0; q < kChainSeg / 8; ++q) {
+      const uint16_t* hv = reinterpret_cast<const uint16_t*>(&ep[q]);
+#pragma unroll
+      for (uint32_t i = 0; i < 8; ++i) ev[8 * q + i] = half_to_float(hv[i]);
+    }
+    float s = 0.0f;
+    for (uint32_t seg = 0; seg < nseg; ++seg) {
+      if (k == seg) {
+#pragma unroll
+        for (uint32_t i = 0; i < kChainSeg; ++i) s = order_step<kMulAdd>(s, yv[i], ev[i]);
+      }
+      if (seg + 1 < nseg) s = lane_shift_right(s);
+    }
+    if (active && k == nseg - 1u) best = best_of(best, best_leaf(s, token, L.cand_pos[j]));
+  }
+  return wave_best(best);
+}
+
+// Rescores candidates cand_token[0..n) of one row in the reference order:
+// in registers (rescore_segmented) when H is a multiple of kChainSeg of at
+// most kWave segments, else stage_rows rows at a time staged in LDS;
+// returns the wave's best.
 __device__ inline Best rescore_candidates(const FinalizeArgs& a, const FinalizeLds& L,
                                           uint32_t n) {
   const uint32_t lane = threadIdx.x % kWave;
   const uint32_t H = a.H;
+  if (H % kChainSeg == 0u && H <= kChainSeg * kWave &&
+      (reinterpret_cast<uintptr_t>(a.emb) & 15u) == 0) {
+    wave_sync();
+    return a.order == 1 ? rescore_segmented<true>(a, L, n) : rescore_segmented<false>(a, L, n);
+  }
   Best best = best_identity();
   for (uint32_t base = 0; base < n; base += L.stage_rows) {
     const uint32_t m = n - base < L.stage_rows ? n - base : L.stage_rows;
