@@ -409,6 +409,13 @@ __device__ __forceinline__ void wait_vector_memory() {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
+// The value of lane l - 1 in lane l (DPP wavefront shift right by one;
+// lane 0 keeps its own).
+__device__ __forceinline__ float lane_shift_right(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x138,
+                                                    0xF, 0xF, false));
+}
+
 // LDS writes of this wave are visible to every lane of the wave afterwards.
 __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");

@@ -85,13 +85,6 @@ __device__ float chain_lds(const float* ys, const uint16_t* row, uint32_t H) {
   return s;
 }
 
-// The value of lane l - 1 in lane l (DPP wavefront shift right by one;
-// lane 0 keeps its own).
-__device__ __forceinline__ float lane_shift_right(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x138,
-                                                    0xF, 0xF, false));
-}
-
 // Reference-order scores with the operands in registers.  Features are cut
 // into segments of kChainSeg; with nseg = H / kChainSeg segments, lane
 // nseg c + k holds segment k of y and of candidate c's table row (FP32), so

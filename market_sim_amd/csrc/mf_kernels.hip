@@ -96,7 +96,8 @@ __global__ __launch_bounds__(kWave) void rms_norm_kernel(
   __syncthreads();
   // sum of the squares in feature order, then mean, + epsilon, sqrt and
   // reciprocal, each rounded once (rms_norm.cu:104-182)
-  if (lane == 0) inverse_shared = norm_inverse(sequential_sum(sq, H), H, epsilon);
+  const float sum_squares = sequential_sum_wave(sq, H);
+  if (lane == 0) inverse_shared = norm_inverse(sum_squares, H, epsilon);
   __syncthreads();
   const float inverse = inverse_shared;
   float norm_sq = 0.0f;

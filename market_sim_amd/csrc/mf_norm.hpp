@@ -54,6 +54,43 @@ __device__ inline float sequential_sum(const float* sq, uint32_t H) {
   return s;
 }
 
+// sequential_sum by the whole wave (every lane calls; every lane gets the
+// sum).  When H is a multiple of 64 of at most 64 segments, lane k holds the
+// squares [64 k, 64 k + 64) in registers and the sum runs segment by
+// segment, handed one lane up between segments: the same additions in the
+// same order, from registers instead of LDS reads.  Otherwise lane 0 runs
+// sequential_sum.
+__device__ inline float sequential_sum_wave(const float* sq, uint32_t H) {
+  constexpr uint32_t kSeg = 64;
+  const uint32_t lane = threadIdx.x % kWave;
+  if (H % kSeg == 0u && H <= kSeg * kWave) {
+    const uint32_t nseg = H / kSeg;
+    const uint32_t k = lane < nseg ? lane : 0u;
+    const float4* q = reinterpret_cast<const float4*>(sq + k * kSeg);
+    float v[kSeg];
+#pragma unroll
+    for (uint32_t i = 0; i < kSeg / 4; ++i) {
+      const float4 t = q[i];
+      v[4 * i] = t.x;
+      v[4 * i + 1] = t.y;
+      v[4 * i + 2] = t.z;
+      v[4 * i + 3] = t.w;
+    }
+    float s = 0.0f;
+    for (uint32_t seg = 0; seg < nseg; ++seg) {
+      if (lane == seg) {
+#pragma unroll
+        for (uint32_t i = 0; i < kSeg; ++i) s = s + v[i];
+      }
+      if (seg + 1 < nseg) s = lane_shift_right(s);
+    }
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), nseg - 1u));
+  }
+  float s = 0.0f;
+  if (lane == 0) s = sequential_sum(sq, H);
+  return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(s)));
+}
+
 // inv of a row from its sum of squares (operators.cpp:531-533)
 __device__ __forceinline__ float norm_inverse(float sum_squares, uint32_t H, float epsilon) {
   const float mean = div_rn(sum_squares, static_cast<float>(H));
@@ -91,7 +128,8 @@ __device__ inline void norm_chain_wave(const float* __restrict__ x, const float*
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  if (lane == 0) *inv_slot = norm_inverse(sequential_sum(sq, H), H, epsilon);
+  const float sum_squares = sequential_sum_wave(sq, H);
+  if (lane == 0) *inv_slot = norm_inverse(sum_squares, H, epsilon);
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");

@@ -147,10 +147,11 @@ __device__ inline void prep_item(const TailNormArgs& a, uint32_t item, float* ld
     }
   }
   wave_sync();
+  // the reference-order chain: rows only (a slot needs z, not y), and only
+  // when it is not deferred to the gather launch
+  const float sum_squares = chain ? sequential_sum_wave(sq, H) : 0.0f;
   if (lane == 0) {
-    // the reference-order chain: rows only (a slot needs z, not y), and
-    // only when it is not deferred to the gather launch
-    if (chain) *inv_slot = norm_inverse(sequential_sum(sq, H), H, a.epsilon);
+    if (chain) *inv_slot = norm_inverse(sum_squares, H, a.epsilon);
     if (!slot) {
       a.row_meta[r] = l.meta;
       if (l.meta.kind != kRowRestricted) {

@@ -173,9 +173,8 @@ __global__ __launch_bounds__(kShortThreads) void short_tail_kernel(TailNormArgs 
   const uint32_t count = meta.count;
   const uint32_t m0 = count < stage_rows ? count : stage_rows;
   if (wave == 0) {
-    if (lane == 0) {
-      sh.inv = weighted ? norm_inverse(sequential_sum(sq, H), H, n.epsilon) : 1.0f;
-    }
+    const float sum_squares = weighted ? sequential_sum_wave(sq, H) : 0.0f;
+    if (lane == 0) sh.inv = weighted ? norm_inverse(sum_squares, H, n.epsilon) : 1.0f;
   } else {
     stage_part(n, f, sh, es, 0u, m0, wave - 1u, kShortWaves - 1u);
   }
