@@ -475,9 +475,21 @@ bool optional_is(const mf_buffer& b, uint64_t bytes) {
 // The restricted gather runs on MFMA when H is a multiple of the 32-feature
 // MFMA step (64-candidate wave tiles); otherwise on the VALU dot.
 bool mfma_gather(uint64_t H) { return H % 32u == 0; }
-uint32_t gather_tile(uint64_t H) {
-  if (mfma_gather(H)) return mf::kGatherWaveTile;
-  return H == 2048 ? 128u : 64u;
+// Candidates per gather tile (one wave each on the MFMA gather).  Tiles of
+// 64 unless the pack is small: when even the upper bound of its 64-candidate
+// tiles (every row as long as the longest list) stays under four per
+// compute unit of an MI355X (256 CUs), a wave would stream 64 rows through
+// eight dependent load units while most SIMDs idle, so the tiles shrink to
+// 32 or 16 candidates (more waves, one or two units each; the finalize
+// merges the extra records).
+constexpr uint64_t kGatherSmallPack = 4u * 256u;
+uint32_t gather_tile(uint64_t H, uint64_t rows, uint64_t max_count) {
+  if (!mfma_gather(H)) return H == 2048 ? 128u : 64u;
+  const uint64_t lists = max_count == 0 ? 1 : max_count;
+  const uint64_t t64 = rows * ((lists + mf::kGatherWaveTile - 1) / mf::kGatherWaveTile);
+  if (t64 >= kGatherSmallPack) return mf::kGatherWaveTile;
+  const uint64_t t32 = rows * ((lists + 31) / 32);
+  return t32 >= kGatherSmallPack ? 32u : 16u;
 }
 
 // The table pass (one launch for restricted and unrestricted rows): lists
@@ -612,7 +624,7 @@ mf_status validate_tail(const mf_decode_tail_args* a, bool full, TailLayout& L) 
     L.tile = kFullTile;
     L.max_tiles = static_cast<uint32_t>((longest + L.tile - 1) / L.tile);
   } else {
-    L.tile = gather_tile(a->hidden);
+    L.tile = gather_tile(a->hidden, a->rows, a->max_count);
     L.max_tiles = static_cast<uint32_t>(a->max_count == 0 ? 1 : (a->max_count + L.tile - 1) / L.tile);
   }
   L.fb_tiles = mf::fallback_tiles(static_cast<uint32_t>(a->vocab));

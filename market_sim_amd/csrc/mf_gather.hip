@@ -1,7 +1,8 @@
 // The restricted gather on the matrix cores (restricted stage of
 // mf_decode_tail_f16 when H % 32 == 0).
 //
-// A wave owns one tile: up to 64 consecutive candidates of one row's list,
+// A wave owns one tile: up to a.tile consecutive candidates of one row's
+// list (64; 32 or 16 for packs too small to give every SIMD a tile of 64),
 // the granularity of the window records the finalize kernel merges.  It
 // scores them 16 at a time with v_mfma_f32_16x16x32_f16:
 //
@@ -102,8 +103,8 @@ template <int KC>
 __device__ void mfma_tile(const GatherArgs& a, uint32_t r, uint32_t k, uint32_t list_begin,
                           uint32_t count, uint16_t* stage, uint32_t& staged) {
   const uint32_t lane = threadIdx.x % kWave;
-  const uint32_t begin = k * kGatherWaveTile;
-  const uint32_t n = count - begin < kGatherWaveTile ? count - begin : kGatherWaveTile;
+  const uint32_t begin = k * a.tile;
+  const uint32_t n = count - begin < a.tile ? count - begin : a.tile;
   const bool live = lane < n;
   const uint32_t id = a.tokens[list_begin + begin + (live ? lane : n - 1)];
   const uint32_t t = live ? id : 0u;
@@ -283,7 +284,7 @@ __global__ __launch_bounds__(kThreads) void gather_mfma_kernel(GatherArgs a) {
   }
   uint16_t* stage = stages + static_cast<size_t>(threadIdx.x / kWave) * 2u * a.H;
   uint32_t staged = kInvalidToken;
-  const uint64_t W = plan_tiles<kThreads>(a.row_meta, a.rows, kGatherWaveTile, false, plan);
+  const uint64_t W = plan_tiles<kThreads>(a.row_meta, a.rows, a.tile, false, plan);
   const uint64_t slots = static_cast<uint64_t>(gridDim.x - chain_groups) * kWaves;
   const uint64_t me =
       static_cast<uint64_t>(blockIdx.x - chain_groups) * kWaves + threadIdx.x / kWave;
@@ -305,7 +306,7 @@ __global__ __launch_bounds__(kWave) void gather_mfma_grid_kernel(GatherArgs a) {
   const uint32_t k = blockIdx.x / a.rows;
   extern __shared__ __align__(16) uint16_t stages[];  // [2 H]
   const RowMeta meta = a.row_meta[r];
-  if (!row_gathered(meta, false) || k * kGatherWaveTile >= meta.count) return;
+  if (!row_gathered(meta, false) || k * a.tile >= meta.count) return;
   uint32_t staged = kInvalidToken;
   mfma_tile<KC>(a, r, k, meta.list_begin, meta.count, stages, staged);
 }
@@ -370,7 +371,8 @@ hipError_t launch_variant(const GatherArgs& a, hipStream_t stream) {
 }  // namespace
 
 hipError_t launch_gather_mfma(const GatherArgs& a, hipStream_t stream) {
-  if (a.H == 0 || a.H % kStep != 0 || a.tile != kGatherWaveTile || a.y_hi == nullptr ||
+  if (a.H == 0 || a.H % kStep != 0 ||
+      (a.tile != 16u && a.tile != 32u && a.tile != kGatherWaveTile) || a.y_hi == nullptr ||
       a.y_lo == nullptr || a.row_norm == nullptr || a.row_slack == nullptr) {
     return hipErrorInvalidValue;
   }
