@@ -207,9 +207,17 @@ __device__ __forceinline__ uint32_t collect_members(const TileRecord* recs, uint
                                                     float lg, const FinalizeLds& L) {
   uint32_t overflow = 0u;
   const uint32_t nm = n_members < kTileMembers ? n_members : kTileMembers;
-  for (uint32_t j = 0; j < nm; ++j) {
-    const TileMember mm = j == 0 ? first : recs[t].m[j];
-    if (mm.upper >= lg) {
+  // the other members' loads issued together (one line with the header)
+  TileMember ms[kTileMembers];
+  ms[0] = first;
+#pragma unroll
+  for (uint32_t j = 1; j < static_cast<uint32_t>(kTileMembers); ++j) {
+    ms[j] = j < nm ? recs[t].m[j] : TileMember{0u, 0u, 0.0f, -__builtin_huge_valf()};
+  }
+#pragma unroll
+  for (uint32_t j = 0; j < static_cast<uint32_t>(kTileMembers); ++j) {
+    const TileMember mm = ms[j];
+    if (j < nm && mm.upper >= lg) {
       const uint32_t slot = atomicAdd(&L.w->n_cand, 1u);
       if (slot < L.cand_max) {
         L.cand_token[slot] = mm.token;
@@ -404,6 +412,8 @@ __device__ inline void finalize_row(const FinalizeArgs& a, uint32_t r, const Row
     for (uint32_t u = 0; u < kRecBlock; ++u) {
       const uint32_t t = base + u * kWave + lane;
       if (h[u].y != 0u || t >= ntiles) continue;
+      // no member of a tile whose best upper bound is below the window
+      if (__uint_as_float(c[u].w) < lg) continue;
       overflow |= collect_members(recs, t, c[u].z, m0[u], lg, L);
     }
   }
