@@ -355,3 +355,20 @@ def test_duplicate_and_foreign_unrestricted_rows():
     staged = _staged(t)
     for a, b in zip(fused, staged):
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@pytest.mark.parametrize("rows,lo,hi", [(16, 1, 512), (64, 300, 600), (128, 300, 600)])
+def test_gather_tile_sizes(rows, lo, hi):
+    """Packs on either side of the small-pack rule of the MFMA gather (tiles
+    of 64 candidates unless rows x ceil(longest / 64) < 1024, then 32 unless
+    rows x ceil(longest / 32) < 1024, then 16): 16 rows of <= 512 ids take
+    16-candidate tiles, 64 rows of 300-600 ids 32-candidate tiles, 128 rows
+    64-candidate tiles.  No unrestricted rows, lists above the one-kernel
+    tail's limit, so the modes without the table pass run the gather."""
+    w = wl.ragged_pack("tiles", 71 + rows, 8192, 576, rows, "uniform", hi, 0.0, size_lo=lo)
+    m = w.max_count
+    t64 = rows * -(-m // 64)
+    t32 = rows * -(-m // 32)
+    tile = 64 if t64 >= 1024 else (32 if t32 >= 1024 else 16)
+    assert tile == {16: 16, 64: 32, 128: 64}[rows], (m, t64, t32)
+    _same(_tail(w).run(), _oracle(w))
