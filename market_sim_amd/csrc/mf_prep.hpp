@@ -181,7 +181,47 @@ __device__ inline void prep_item(const TailNormArgs& a, uint32_t item, float* ld
   // hi + lo.  z differs from y / inv by at most 3 roundings per element.
   float z_sq = 0.0f;
   float x_sq = 0.0f;
-  for (uint32_t c = lane; c < H; c += kWave) {
+  // four features per lane at a time: 16-byte LDS reads, 16-byte y stores
+  // and 8-byte stores of the FP16 hi and lo halves (per element the same
+  // values; the bound sums x_sq and z_sq take any order)
+  const uint32_t c4 = (H % 4u == 0u) ? H : 0u;
+  for (uint32_t q = lane; q < c4 / 4u; q += kWave) {
+    const float4 xv = reinterpret_cast<const float4*>(xs)[q];
+    float4 yv = xv;
+    float4 zv = xv;
+    if (weighted) {
+      const float4 wv = reinterpret_cast<const float4*>(ws)[q];
+      const float4 sv = reinterpret_cast<const float4*>(sq)[q];
+      yv = float4{(xv.x * inverse) * wv.x, (xv.y * inverse) * wv.y, (xv.z * inverse) * wv.z,
+                  (xv.w * inverse) * wv.w};
+      zv = float4{xv.x * wv.x, xv.y * wv.y, xv.z * wv.z, xv.w * wv.w};
+      x_sq += (sv.x + sv.y) + (sv.z + sv.w);
+    }
+    if (write_y) reinterpret_cast<float4*>(a.y + r * H)[q] = yv;
+    if (split) {
+      const float zz[4] = {zv.x, zv.y, zv.z, zv.w};
+      uint16_t hv[4], lv[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        z_sq = __builtin_fmaf(zz[k], zz[k], z_sq);
+        const _Float16 hi = static_cast<_Float16>(zz[k]);
+        hv[k] = __builtin_bit_cast(uint16_t, hi);
+        lv[k] = float_to_half_rne(zz[k] - static_cast<float>(hi));
+      }
+      const uint2 hp{static_cast<uint32_t>(hv[0]) | (static_cast<uint32_t>(hv[1]) << 16),
+                     static_cast<uint32_t>(hv[2]) | (static_cast<uint32_t>(hv[3]) << 16)};
+      const uint2 lp{static_cast<uint32_t>(lv[0]) | (static_cast<uint32_t>(lv[1]) << 16),
+                     static_cast<uint32_t>(lv[2]) | (static_cast<uint32_t>(lv[3]) << 16)};
+      if (slot) {
+        reinterpret_cast<uint2*>(panel_hi)[q] = hp;
+        reinterpret_cast<uint2*>(panel_hi + H + kPanelPad)[q] = lp;
+      } else {
+        reinterpret_cast<uint2*>(a.y_hi + r * H)[q] = hp;
+        reinterpret_cast<uint2*>(a.y_lo + r * H)[q] = lp;
+      }
+    }
+  }
+  for (uint32_t c = c4 + lane; c < H; c += kWave) {
     const float xv = xs[c];
     float yv = xv;
     float zv = xv;
@@ -247,7 +287,7 @@ __device__ inline void prep_item(const TailNormArgs& a, uint32_t item, float* ld
 // A list that is not strictly ascending, or holds an id >= V, is not
 // indexed: the row gets one record covering its whole list, "rescore all"
 // (exact, in the finalize) or "invalid".  LDS: range_lds_words(ranges).
-constexpr uint32_t kWalkWaves = 4;
+constexpr uint32_t kWalkWaves = 8;
 
 __host__ __device__ constexpr uint32_t range_bit_words(uint32_t ranges) { return ranges / 32u + 1u; }
 __host__ __device__ constexpr uint32_t range_lds_words(uint32_t ranges) {
@@ -356,7 +396,7 @@ __device__ inline void range_walk(const TailNormArgs& a, const RangeRow& w, cons
   }
 }
 
-// All kWalkWaves waves (after the barrier): range g = tid, tid + 256, ...
+// All kWalkWaves waves (after the barrier): range g = tid, tid + 64 kWalkWaves, ...
 __device__ inline void range_end(const TailNormArgs& a, uint32_t r, const RangeRow& w,
                                  const RangeLds& L) {
   const uint32_t tid = threadIdx.x;
