@@ -12,8 +12,11 @@ build time) and is used to pin the restatement.
 Pinning status per function (tests that pin it):
   half<->float          exhaustive vs numpy float16 (test_oracle_golden.py)
   rms_norm_f32          bit-exact vs reference operators.cpp (_ref) + hand values
-  dot_fma               tiny-head known answer, exact rational scores
+  rms_norm_f16          numpy RNE half of the reference rms_norm_f32 (_ref),
+                        subnormal and overflowing outputs included
+  dot_fma               exact rational chain; tiny-head known answer
   dot_mul_add           bit-exact vs reference linear_f32 (_ref) + [-2, 3]
+  FP32-table dots       exact rational chains in both orders (cfg1 path)
   selection rules       reference test cases (ties, NaN, sentinels), real logits
   decode_tail           float64 brute force + margin, one-hot closed forms,
                         real market DFA advance vs reference TokenDfa (_ref)

@@ -16,6 +16,11 @@
  *                                          every one of the 65536 halves.
  *   orc_rms_norm_f32     reference operators.cpp compiled into oracle/_ref,
  *                        bit-exact; hand values of cpu_operator_tests.cpp:59-108.
+ *   orc_rms_norm_f16     numpy's IEEE float32 -> float16 cast of the reference
+ *                        rms_norm_f32 (oracle/_ref) on the decoded inputs, bit
+ *                        for bit, with half-subnormal and overflowing outputs;
+ *                        x * (inv * w) and a pairwise sum of squares shown to
+ *                        differ (tests/test_oracle_pin_f16_norm_f32_table.py).
  *   orc_dot_fma          the ascending single-rounding chain evaluated in
  *                        exact rational arithmetic on rows spanning many
  *                        binades, bit for bit (tests/test_oracle_fma_pin.py,
@@ -25,6 +30,11 @@
  *                        [14, 8, 1] and exact rational scores.
  *   orc_dot_mul_add      reference linear_f32 in oracle/_ref, bit-exact;
  *                        linear known answer [-2, 3].
+ *   dot_in_order_f32     (FP32 table, both orders) exact rational chains on
+ *                        rows spanning many binades, reached through
+ *                        orc_decode_tail with one candidate per row; other
+ *                        orders shown to differ on the same rows
+ *                        (tests/test_oracle_pin_f16_norm_f32_table.py).
  *   orc_select_*         greedy/restricted tie, NaN and sentinel cases of
  *                        cuda_tests.cu:508-565, 567-697, 1173-1277, 1341-1403;
  *                        real SmolLM2 logits fixture -> [198, 198, 504].
