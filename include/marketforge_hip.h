@@ -10,9 +10,8 @@
  * or torch type appears here.
  *
  * Conventions kept from the reference:
- *   - ops borrow caller buffers: they never allocate (the comparator
- *     mf_decode_tail_full_f16 creates one rocBLAS handle per device) and
- *     never synchronize;
+ *   - ops borrow caller buffers: they never allocate and never
+ *     synchronize;
  *   - work is asynchronous on the caller's stream;
  *   - validation happens before any launch, in the reference order: zero
  *     dimensions / bad epsilon / null stream -> MF_INVALID_ARGUMENT; limits ->
@@ -212,8 +211,10 @@ mf_status mf_linear_f16(mf_buffer input, mf_buffer weight, mf_buffer output,
  * in full, exactly.  MF_TAIL_TABLE_PASS alone changes nothing.
  *
  * Dense head: otherwise, with MF_TAIL_SORTED_LISTS, hidden % 32 == 0,
- * hidden >= 1024 and rows + unrestricted_count within the launch's panels
- * (256 slots per 8 compute units: 8192 on MI355X), the unrestricted stage
+ * hidden >= 1024, rows <= 8191, vocab < 2^19 (the device's ranking packs
+ * (count, row) into 32 bits) and rows + unrestricted_count within the
+ * launch's panels (256 slots per 8 compute units: 8192 on MI355X), the
+ * unrestricted stage
  * runs one pass over the table that scores the unrestricted rows and the
  * long ascending lists (at least vocab / 256 and 64 ids) with MFMA against
  * every token, keeping only the allowed ones; the gather skips those rows.
@@ -332,14 +333,13 @@ mf_status mf_decode_tail_unrestricted(const mf_decode_tail_args* args,
 mf_status mf_decode_tail_finalize(const mf_decode_tail_args* args, uintptr_t stream);
 
 /* The full-output-projection comparator for the same contract: a GEMM
- * projection of every row over the whole vocabulary into FP32 scores (two
- * rocBLAS FP16 GEMMs, the normalized row split into FP16 hi and lo parts,
- * FP32 accumulation), then the restricted selection over those scores (the
- * shape of the reference's "full" path,
+ * projection of every row over the whole vocabulary into FP32 scores (the
+ * library's own MFMA projection kernel, the normalized row split into FP16
+ * hi and lo parts, FP32 accumulation), then the restricted selection over
+ * those scores (the shape of the reference's "full" path,
  * src/tools/cuda_restricted_output_head_bench.cu:181-191).  Outputs are
  * bit-identical to mf_decode_tail_f16.  Needs
- * mf_decode_tail_full_workspace_bytes of workspace.  The first call on a
- * device creates that device's rocBLAS handle. */
+ * mf_decode_tail_full_workspace_bytes of workspace. */
 mf_status mf_decode_tail_full_workspace_bytes(const mf_decode_tail_args* args,
                                               uint64_t* bytes);
 mf_status mf_decode_tail_full_f16(const mf_decode_tail_args* args,
