@@ -308,10 +308,15 @@ mf_status mf_decode_tail_f16(const mf_decode_tail_args* args, uintptr_t stream);
  * held from library load until the process ends; args->workspace is not
  * used.  Same kernels, same results as mf_decode_tail_f16.  A call whose
  * workspace (mf_decode_tail_workspace_bytes) exceeds the array returns
- * MF_RESOURCE_LIMIT before any launch.  The first call on a device looks up
- * that device's array and zero-fills it on the call's stream.  Every call on
- * one GPU shares that GPU's array: calls that overlap in time on one GPU
- * (two streams, two threads) race and must be ordered by the caller. */
+ * MF_RESOURCE_LIMIT before any launch.  The first successful call on a
+ * device looks up that device's array and zero-fills it on the call's stream
+ * (a fill kernel, no memset node); until then every call tries again, and a
+ * first call on a stream under graph capture returns
+ * MF_DEVICE_RUNTIME_FAILURE with detail hipErrorStreamCaptureUnsupported
+ * before any launch, so make one eager call on each device before capturing.
+ * Every call on one GPU shares that GPU's array: calls that overlap in time
+ * on one GPU (two streams, two threads) race and must be ordered by the
+ * caller. */
 uint64_t mf_decode_tail_noalloc_max_bytes(void);
 mf_status mf_decode_tail_f16_noalloc(const mf_decode_tail_args* args, uintptr_t stream);
 

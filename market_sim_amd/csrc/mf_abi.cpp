@@ -1021,31 +1021,43 @@ constexpr uint64_t kScratchBytes = 16ull << 20;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 struct ScratchSlot {
-  std::once_flag once;
-  hipError_t error = hipSuccess;
+  std::mutex lock;
+  bool ready = false;
   void* address = nullptr;
 };
 ScratchSlot g_scratch[64];
 
 // The current device's array: its address, looked up with that device
-// current on the first call there, when the array is also zero-filled on the
-// caller's stream (the state every workspace starts from).
+// current on the first successful call there, when the array is also
+// zero-filled on the caller's stream (the state every workspace starts
+// from).  Only success is latched: a call that fails here (a bad stream, a
+// failed lookup) leaves the next call to try again.  A stream under graph
+// capture cannot carry that first fill (it would become a graph node that
+// eager calls made before a replay never see), so a first call under
+// capture is refused with hipErrorStreamCaptureUnsupported.
 hipError_t scratch_address(hipStream_t stream, void** out) {
+  *out = nullptr;
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
   ScratchSlot& slot = g_scratch[dev];
-  std::call_once(slot.once, [&slot, stream]() {
+  std::lock_guard<std::mutex> guard(slot.lock);
+  if (!slot.ready) {
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing(stream, &capture);
+    if (e != hipSuccess) return e;
+    if (capture != hipStreamCaptureStatusNone) return hipErrorStreamCaptureUnsupported;
     void* p = nullptr;
-    hipError_t r = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-    if (r == hipSuccess && p == nullptr) r = hipErrorInvalidSymbol;
-    if (r == hipSuccess) r = mf::launch_fill_zero(p, kScratchBytes, stream);
-    slot.error = r;
-    slot.address = r == hipSuccess ? p : nullptr;
-  });
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e == hipSuccess && p == nullptr) e = hipErrorInvalidSymbol;
+    if (e == hipSuccess) e = mf::launch_fill_zero(p, kScratchBytes, stream);
+    if (e != hipSuccess) return e;
+    slot.address = p;
+    slot.ready = true;
+  }
   *out = slot.address;
-  return slot.error;
+  return hipSuccess;
 }
 
 }  // namespace

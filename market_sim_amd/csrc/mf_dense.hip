@@ -506,6 +506,13 @@ hipError_t launch_dense(const DenseArgs& args, hipStream_t stream) {
       args.groups % 8u != 0 || args.z_hi == nullptr || args.spans == nullptr) {
     return hipErrorInvalidValue;
   }
+  // every slot needs a panel of this launch: a workgroup past its XCD's
+  // panels would return without writing its records and fb_map entries,
+  // and the finalize would read stale records
+  if (static_cast<uint64_t>(args.fb_m) + args.rows >
+      static_cast<uint64_t>(args.groups / 8u) * kDensePanelSlots) {
+    return hipErrorInvalidValue;
+  }
   const uint32_t lds = dense_lds_bytes();
   hipLaunchKernelGGL(dense_kernel, dim3(args.groups), dim3(kThreads), lds, stream, args);
   return hipGetLastError();

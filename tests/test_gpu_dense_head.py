@@ -67,8 +67,9 @@ def _dense_and_gather(w, exp=None, **kw):
     return got
 
 
-def _pack(seed, vocab, hidden, rows, longest, unrestricted):
-    return wl.ragged_pack("dense", seed, vocab, hidden, rows, "log", longest, unrestricted)
+def _pack(seed, vocab, hidden, rows, longest, unrestricted, size_kind="log", size_lo=1):
+    return wl.ragged_pack("dense", seed, vocab, hidden, rows, size_kind, longest, unrestricted,
+                          size_lo=size_lo)
 
 
 def test_scaled_cfg5_with_unrestricted_rows():
@@ -192,9 +193,8 @@ def test_duplicate_and_foreign_unrestricted_rows():
 
 
 def test_repeated_calls_and_stages():
-    """The arrival counter and the length sum reset themselves: repeated calls
-    on one workspace give the same bits, and so do the four stage entry
-    points called one by one."""
+    """Repeated calls on one workspace give the same bits, and so do the four
+    stage entry points called one by one."""
     from market_sim_amd import ops
     w = _pack(9, 10000, 1024, 72, 8192, 0.05)
     t = _tail(w)
@@ -212,6 +212,30 @@ def test_repeated_calls_and_stages():
     for x, y in zip(first, staged):
         assert np.array_equal(_bits(x), _bits(y))
     _same(first, _oracle(w))
+
+
+def test_unrestricted_rows_fill_two_panels():
+    """More than 256 unrestricted rows (300 of 600): the dense head runs
+    P >= 2 panels of equal size, so the slot split across panels, the
+    per-XCD groups of P workgroups and fb_map written by every panel's first
+    group are exercised; exact against the oracle and the gather."""
+    w = _pack(12, 6000, 1024, 600, 4096, 0.5)
+    assert w.unrestricted_rows.size > 256
+    _dense_and_gather(w)
+
+
+def test_long_lists_take_a_second_panel():
+    """No unrestricted rows and 300 long ascending lists (2000-4000 ids of a
+    6000-token vocabulary): the device fills the first panel with the 256
+    longest and, since the remaining 44 lists still hold more than 5/2 vocab
+    ids, takes them as a second panel (slots > 256); exact against the
+    oracle and the gather."""
+    w = _pack(13, 6000, 1024, 300, 4000, 0.0, size_kind="uniform", size_lo=2000)
+    lens = np.sort(np.diff(w.state_offsets.astype(np.int64))[w.row_state])[::-1]
+    dense_min = max(64, w.vocab // 256)
+    assert (lens >= dense_min).sum() == 300
+    assert lens[256:].sum() >= 5 * w.vocab // 2
+    _dense_and_gather(w)
 
 
 def test_decode_steps_with_device_states():
