@@ -73,3 +73,21 @@ def test_algorithmic_pass_bytes_count_the_table_once_with_unrestricted_rows():
     H, V, B = w.hidden, w.vocab, w.rows
     assert alg["pass_bytes"] == (2 * H * V + 4 * alg["N"] + 4 * H * B + 4 * (alg["B_r"] + 1)
                                  + 12 * B)
+
+
+def test_cpu_baseline_on_the_pre_decoded_table_gives_the_same_bits():
+    """cpu_baseline times the oracle on the FP16 table decoded to FP32 before
+    the timed region; its outputs (the parity leg's expected values) must be
+    the bits the FP16 table gives."""
+    import numpy as np
+
+    import oracle
+    bench = _bench()
+    w = workloads.config(3, seed=4, scale_vocab=3000, scale_rows=24)
+    cb = bench.cpu_baseline(w, 0.05)
+    tok, sc, nx = cb.pop("_outputs")
+    etok, esc, enx = oracle.decode_tail(w.x, w.norm_weight, w.epsilon, w.embedding,
+                                        w.row_state, w.state_offsets, w.state_tokens, threads=4)
+    assert np.array_equal(tok, etok) and np.array_equal(nx, enx)
+    assert np.array_equal(sc.view(np.uint32), esc.view(np.uint32))
+    assert cb["kind"] == "port" and cb["cores"] >= 1 and "pre-decoded" in cb["sample"]
