@@ -864,6 +864,11 @@ mf::PassArgs pass_args(const mf_decode_tail_args* a, const TailLayout& L, char* 
   p.rows = static_cast<uint32_t>(a->rows);
   p.ranges = L.fb_tiles;
   pass_bound_coefs(a->hidden, p.coef, p.coef2);
+  // the pass scores the unrestricted rows on the FP16 hi of z alone too, so
+  // their windows take the hi-only coefficients (|z - hi| <= 2^-11 |z|), not
+  // the hi + lo ones of the separate MFMA head
+  p.head.coef = p.coef;
+  p.head.coef2 = p.coef2;
   return p;
 }
 

@@ -372,3 +372,47 @@ def test_gather_tile_sizes(rows, lo, hi):
     tile = 64 if t64 >= 1024 else (32 if t32 >= 1024 else 16)
     assert tile == {16: 16, 64: 32, 128: 64}[rows], (m, t64, t32)
     _same(_tail(w).run(), _oracle(w))
+
+
+def _hi_rounding_near_tie():
+    """An unrestricted row whose exact winner loses on the FP16 hi of z by
+    more than the window of an FP16 hi+lo score, but less than the window of
+    a hi-only score: every feature of z sits 0.99 half-ulps from its FP16
+    rounding (z = 1 + 2^-10 +- 0.99 2^-11, so hi = 1 + 2^-10 and the rounding
+    error follows a sign pattern p), token A = p / 16 (aligned with the
+    rounding error) and token B = -p / 16 moved up one or two FP16 ulps per
+    feature.  Exactly, z . A - z . B = 0.0046 > 0; on hi, B leads A by
+    0.030, between the hi+lo window (0.025) and the hi-only one (0.087).  The
+    other rows of the table are tiny.  Row 1 is restricted to [A, B]."""
+    H, V, A, B = 576, 600, 10, 20
+    rng = np.random.default_rng(1)
+    p = np.where(rng.permutation(H) % 2 == 0, 1.0, -1.0)
+    z = (1.0 + 2.0 ** -10 + p * 0.99 * 2.0 ** -11).astype(np.float32)
+    assert np.all(z.astype(np.float16).astype(np.float64) == 1.0 + 2.0 ** -10)
+    emb = (rng.standard_normal((V, H)) * 1e-5).astype(np.float16)
+    emb[A] = (p / 16).astype(np.float16)
+    base = (-p / 16).astype(np.float16).view(np.uint16).astype(np.int64)
+    steps = np.ones(H, np.int64)
+    steps[np.nonzero(p > 0)[0][:125]] = 2
+    emb[B] = np.where(p > 0, base - steps, base + steps).astype(np.uint16).view(np.float16)
+    z64 = z.astype(np.float64)
+    hi = z.astype(np.float16).astype(np.float64)
+    ea, eb = emb[A].astype(np.float64), emb[B].astype(np.float64)
+    assert z64 @ ea - z64 @ eb > 0.004          # A wins exactly
+    assert 0.028 < hi @ eb - hi @ ea < 0.032    # B leads on hi by more than 0.025
+    return wl.Workload(name="hi-near-tie", vocab=V, hidden=H, embedding=emb.view(np.uint16),
+                       norm_weight=np.ones(H, np.float32), epsilon=1e-5, x=np.stack([z, z]),
+                       row_state=np.array([wl.STATE_UNRESTRICTED, 0], np.uint32),
+                       state_offsets=np.array([0, 2], np.uint32),
+                       state_tokens=np.array([A, B], np.uint32))
+
+
+def test_unrestricted_row_window_covers_the_hi_rounding():
+    """The table pass scores unrestricted rows on the FP16 hi of z alone, so
+    their windows must carry |z - hi| <= 2^-11 |z| (the hi-only bound, as for
+    the candidates); with the hi+lo bound the exact winner A falls outside
+    the window and B is returned."""
+    w = _hi_rounding_near_tie()
+    exp = _oracle(w)
+    assert exp[0].tolist() == [10, 10]
+    _same(_run(w), exp)
