@@ -392,6 +392,49 @@ def reference_bench() -> dict:
     }
 
 
+def secondary_benches() -> dict:
+    """The reference's restricted-greedy and RMSNorm benchmarks
+    (src/tools/cuda_restricted_greedy_bench.cu, cuda_rmsnorm_bench.cu) run
+    by the C++ tools market_sim_amd/bench/restricted_greedy_bench (on the
+    market-action grammar of tests/golden/market_dfa.npz) and rmsnorm_bench
+    with the reference's iteration counts; each document is checked against
+    the reference schema and each tool checks its outputs (exit status)."""
+    import subprocess
+    import tempfile
+    from market_sim_amd import schema
+    from market_sim_amd.dfa import DfaTables, write_tables
+    out = {}
+    bdir = os.path.join(ROOT, "market_sim_amd", "bench", "_build")
+    d = np.load(os.path.join(ROOT, "tests", "golden", "market_dfa.npz"))
+    tables = DfaTables.from_arrays(d["offsets"], d["tokens"], d["next"], d["terminal"],
+                                   vocab=49152)
+    with tempfile.TemporaryDirectory() as tmp:
+        path = os.path.join(tmp, "market.dfa")
+        write_tables(tables, path)
+        for name, cmd, check in (
+                ("restricted_greedy", ["restricted_greedy_bench", "--dfa", path],
+                 schema.check_restricted_greedy_benchmark),
+                ("rms_norm", ["rmsnorm_bench"], schema.check_rmsnorm_benchmark)):
+            tool = os.path.join(bdir, cmd[0])
+            if not os.path.exists(tool):
+                out[name] = {"error": "tool not built (make -C market_sim_amd/bench)"}
+                continue
+            r = subprocess.run([tool] + cmd[1:], capture_output=True, text=True, timeout=300)
+            if r.returncode != 0:
+                out[name] = {"error": f"exit {r.returncode}: {r.stderr.strip()[-300:]}"}
+                continue
+            doc = json.loads(r.stdout)
+            check(doc)
+            rate = "candidate_gib_per_second" if name == "restricted_greedy" \
+                else "logical_gib_per_second"
+            out[name] = {"checked": True, "columns": ["rows", "average_microseconds", rate],
+                         "cells": [[m["rows"], m["average_microseconds"], m[rate]]
+                                   for m in doc["measurements"]]}
+            if name == "restricted_greedy":
+                out[name]["seqs_per_s_at_256"] = doc["measurements"][-1]["sequences_per_second"]
+    return out
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -555,6 +598,7 @@ def main() -> int:
         result["vs_vendor_gemm"] = round(result["vendor_gemm"]["ms"] / total_ms, 3)
     if not args.no_reference_bench:
         result["reference_bench"] = reference_bench()
+        result["secondary_benches"] = secondary_benches()
     if not args.no_cpu:
         cb = cpu_baseline(w, args.cpu_seconds)
         etok, esc, enx = cb.pop("_outputs")

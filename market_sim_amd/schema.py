@@ -139,6 +139,80 @@ def check_output_head_benchmark(doc, gpu_name_contains: str = "",
         raise SchemaError("benchmark.measurements: a cell is repeated")
 
 
+# ---- restricted-greedy and RMSNorm benchmarks --------------------------------
+
+# The documents of the reference's restricted-greedy benchmark
+# (src/tools/cuda_restricted_greedy_bench.cu:262-296, validated by
+# tools/modal/vllm_modal_app.py:359-427) and RMSNorm benchmark
+# (src/tools/cuda_rmsnorm_bench.cu:155-175, vllm_modal_app.py:283-356):
+# exactly these fields, positive counts, positive finite rates.
+_GREEDY_BENCH_KEYS = ("schema_version", "result", "operator", "grammar", "vocabulary_size",
+                      "grammar_states", "grammar_arcs", "maximum_allowed_tokens", "gpu",
+                      "measurements")
+_GREEDY_CELL_KEYS = ("rows", "total_allowed_candidates", "iterations", "average_microseconds",
+                     "sequences_per_second", "candidate_gib_per_second")
+GREEDY_BENCH_ROWS = (1, 16, 256)
+_NORM_BENCH_KEYS = ("schema_version", "result", "operator", "model_shape", "gpu", "measurements")
+_NORM_CELL_KEYS = ("rows", "hidden_size", "iterations", "average_microseconds",
+                   "logical_gib_per_second")
+NORM_BENCH_ROWS = (1, 16, 256, 1024)
+
+
+def check_restricted_greedy_benchmark(doc) -> None:
+    """Raises SchemaError unless ``doc`` is a restricted-greedy benchmark
+    document with the reference's fields and values (apart from the GPU
+    identity, which names the device it ran on)."""
+    root = _object(doc, _GREEDY_BENCH_KEYS, "benchmark")
+    if (root["schema_version"] != SCHEMA_VERSION or root["result"] != "pass"
+            or root["operator"] != "restricted_greedy_f16"
+            or root["grammar"] != "smollm2_market_action_v1"
+            or root["vocabulary_size"] != HEAD_BENCH_VOCAB):
+        raise SchemaError("benchmark: identity fields do not match")
+    for k in ("grammar_states", "grammar_arcs", "maximum_allowed_tokens"):
+        _int(root[k], f"benchmark.{k}", 1)
+    gpu = _object(root["gpu"], ("name", "compute_capability"), "benchmark.gpu")
+    _text(gpu["name"], "gpu.name")
+    _text(gpu["compute_capability"], "gpu.compute_capability")
+    cells = root["measurements"]
+    if type(cells) is not list or len(cells) != len(GREEDY_BENCH_ROWS):
+        raise SchemaError("benchmark.measurements: expected 3 cases")
+    for i, raw in enumerate(cells):
+        where = f"measurements[{i}]"
+        cell = _object(raw, _GREEDY_CELL_KEYS, where)
+        if _int(cell["rows"], where + ".rows", 1) != GREEDY_BENCH_ROWS[i]:
+            raise SchemaError(f"{where}: rows {cell['rows']} out of order")
+        _int(cell["total_allowed_candidates"], where + ".total_allowed_candidates", 1)
+        _int(cell["iterations"], where + ".iterations", 1)
+        for k in ("average_microseconds", "sequences_per_second", "candidate_gib_per_second"):
+            _float(cell[k], f"{where}.{k}", positive=True)
+
+
+def check_rmsnorm_benchmark(doc) -> None:
+    """Raises SchemaError unless ``doc`` is an RMSNorm benchmark document
+    with the reference's fields and values (apart from the GPU identity)."""
+    root = _object(doc, _NORM_BENCH_KEYS, "benchmark")
+    if (root["schema_version"] != SCHEMA_VERSION or root["result"] != "pass"
+            or root["operator"] != "rms_norm_f32"
+            or root["model_shape"] != "SmolLM2-135M hidden_size=576"):
+        raise SchemaError("benchmark: identity fields do not match")
+    gpu = _object(root["gpu"], ("name", "compute_capability"), "benchmark.gpu")
+    _text(gpu["name"], "gpu.name")
+    _text(gpu["compute_capability"], "gpu.compute_capability")
+    cells = root["measurements"]
+    if type(cells) is not list or len(cells) != len(NORM_BENCH_ROWS):
+        raise SchemaError("benchmark.measurements: expected 4 cases")
+    for i, raw in enumerate(cells):
+        where = f"measurements[{i}]"
+        cell = _object(raw, _NORM_CELL_KEYS, where)
+        if _int(cell["rows"], where + ".rows", 1) != NORM_BENCH_ROWS[i]:
+            raise SchemaError(f"{where}: rows {cell['rows']} out of order")
+        if cell["hidden_size"] != HEAD_BENCH_HIDDEN:
+            raise SchemaError(f"{where}: hidden_size is not 576")
+        _int(cell["iterations"], where + ".iterations", 1)
+        for k in ("average_microseconds", "logical_gib_per_second"):
+            _float(cell[k], f"{where}.{k}", positive=True)
+
+
 def compare_with_l4(doc) -> List[dict]:
     """Per cell: this run's restricted and full times next to the reference's
     published L4 times, and the ratios (L4 time / this time)."""

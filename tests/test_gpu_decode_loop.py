@@ -318,3 +318,45 @@ def test_decoder_one_kernel_tail_equals_separate_kernels(market):
     assert np.array_equal(out[0][0], out[1][0])
     assert np.array_equal(out[0][1].view(np.uint32), out[1][1].view(np.uint32))
     assert np.array_equal(out[0][2], out[1][2])
+
+
+def test_restricted_greedy_bench_tool(tmp_path, market):
+    """The reference's restricted-greedy benchmark on the market grammar
+    (shortened iteration counts): a document in the reference's fields, and
+    the tool's own token check against the host selection passes (exit 0)."""
+    import json
+    import os
+    import subprocess
+    from market_sim_amd import schema
+    from market_sim_amd.dfa import write_tables
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    tool = os.path.join(root, "market_sim_amd", "bench", "_build", "restricted_greedy_bench")
+    assert os.path.exists(tool), "market_sim_amd/bench is not built: run __graft_entry__.build()"
+    path = str(tmp_path / "market.dfa")
+    write_tables(market, path)
+    r = subprocess.run([tool, "--dfa", path, "--iterations-divisor", "20"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
+    doc = json.loads(r.stdout)
+    schema.check_restricted_greedy_benchmark(doc)
+    assert doc["grammar_states"] == market.states and doc["grammar_arcs"] == market.arcs
+    lens = np.diff(market.offsets.astype(np.int64))
+    assert doc["maximum_allowed_tokens"] == int(lens.max())
+    assert doc["measurements"][0]["total_allowed_candidates"] == int(lens[lens > 0][0])
+
+
+def test_rmsnorm_bench_tool():
+    """The reference's RMSNorm benchmark (shortened): a document in the
+    reference's fields, and the tool's bit-exact check of every case
+    against the reference CPU order passes (exit 0)."""
+    import json
+    import os
+    import subprocess
+    from market_sim_amd import schema
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    tool = os.path.join(root, "market_sim_amd", "bench", "_build", "rmsnorm_bench")
+    assert os.path.exists(tool), "market_sim_amd/bench is not built: run __graft_entry__.build()"
+    r = subprocess.run([tool, "--iterations-divisor", "20"], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
+    schema.check_rmsnorm_benchmark(json.loads(r.stdout))

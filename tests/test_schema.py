@@ -142,3 +142,42 @@ def test_output_head_benchmark_rejects_mutations(mutate):
     mutate(doc)
     with pytest.raises(schema.SchemaError):
         schema.check_output_head_benchmark(doc, "gfx950", "9.5")
+
+
+def _greedy_doc():
+    return {"schema_version": 1, "result": "pass", "operator": "restricted_greedy_f16",
+            "grammar": "smollm2_market_action_v1", "vocabulary_size": 49152,
+            "grammar_states": 3230, "grammar_arcs": 3229, "maximum_allowed_tokens": 11,
+            "gpu": {"name": "AMD gfx950", "compute_capability": "9.5"},
+            "measurements": [{"rows": r, "total_allowed_candidates": 3 * r, "iterations": 10,
+                              "average_microseconds": 9.5, "sequences_per_second": 1e5,
+                              "candidate_gib_per_second": 0.01} for r in (1, 16, 256)]}
+
+
+def _norm_doc():
+    return {"schema_version": 1, "result": "pass", "operator": "rms_norm_f32",
+            "model_shape": "SmolLM2-135M hidden_size=576",
+            "gpu": {"name": "AMD gfx950", "compute_capability": "9.5"},
+            "measurements": [{"rows": r, "hidden_size": 576, "iterations": 10,
+                              "average_microseconds": 4.0, "logical_gib_per_second": 1.5}
+                             for r in (1, 16, 256, 1024)]}
+
+
+def test_secondary_benchmark_documents_accepted_and_rejected():
+    """The reference validator's rules (vllm_modal_app.py:283-427): exactly
+    the reference fields, the fixed identity, the case order, positive
+    finite rates."""
+    schema.check_restricted_greedy_benchmark(_greedy_doc())
+    schema.check_rmsnorm_benchmark(_norm_doc())
+    bad = []
+    d = _greedy_doc(); d["measurements"][0]["token_parity"] = True; bad.append((schema.check_restricted_greedy_benchmark, d))
+    d = _greedy_doc(); d["grammar"] = "other"; bad.append((schema.check_restricted_greedy_benchmark, d))
+    d = _greedy_doc(); d["measurements"][2]["candidate_gib_per_second"] = 0.0; bad.append((schema.check_restricted_greedy_benchmark, d))
+    d = _greedy_doc(); d["measurements"] = d["measurements"][::-1]; bad.append((schema.check_restricted_greedy_benchmark, d))
+    d = _norm_doc(); del d["measurements"][1]["iterations"]; bad.append((schema.check_rmsnorm_benchmark, d))
+    d = _norm_doc(); d["measurements"][0]["hidden_size"] = 2048; bad.append((schema.check_rmsnorm_benchmark, d))
+    d = _norm_doc(); d["measurements"][3]["average_microseconds"] = float("inf"); bad.append((schema.check_rmsnorm_benchmark, d))
+    d = _norm_doc(); d["operator"] = "rms_norm_f16"; bad.append((schema.check_rmsnorm_benchmark, d))
+    for fn, doc in bad:
+        with pytest.raises(schema.SchemaError):
+            fn(doc)
