@@ -270,32 +270,60 @@ def read_floor(tail, launches: int, copies: int) -> dict:
 
 def vendor_gemm(w, tail, launches: int) -> dict:
     """For scale beside the full-vocabulary comparator (which scores on this
-    library's own MFMA projection kernel): the vendor FP16 GEMM of the
-    reference's full path (linear.cu:92-102, FP16 inputs and logits) for the
-    same shape, torch.matmul on hipBLASLt, timed back to back."""
+    library's own MFMA projection kernel): the reference's full-path GEMM
+    (linear.cu:92-102, FP16 inputs and logits) for the same shape, once as
+    the vendor's torch.matmul on hipBLASLt and once as this library's
+    mf_linear_f16 (the projection kernel), each timed back to back on the
+    launch stream.  Both outputs are compared (FP16 logits, at most one ulp
+    apart: FP32 accumulation in different orders)."""
     import torch
+    from market_sim_amd import abi, ops
     dev = tail.tables[0].device
-    a = torch.randn(w.rows, w.hidden, device=dev, dtype=torch.float32).to(torch.float16)
+    g = torch.Generator(device="cpu").manual_seed(5)
+    a = torch.randn(w.rows, w.hidden, generator=g).to(torch.float16).to(dev)
     e = tail.tables[0].view(torch.float16).reshape(w.vocab, w.hidden)
     out = torch.empty(w.rows, w.vocab, device=dev, dtype=torch.float16)
+    own = torch.empty_like(out)
     s = tail.stream
+    n = max(10, launches // 4)
+    flops = 2.0 * w.rows * w.hidden * w.vocab
+
+    def vendor_launch(_):
+        torch.matmul(a, e.t(), out=out)
+
+    args = (ops.DeviceBuffer.of(a).c(), ops.DeviceBuffer.of(e).c(), ops.DeviceBuffer.of(own).c(),
+            w.rows, w.hidden, w.vocab, s.cuda_stream)
+
+    def own_launch(_):
+        abi.check("mf_linear_f16", abi.lib().mf_linear_f16(*args))
+
     with torch.cuda.stream(s):
         for _ in range(5):
-            torch.matmul(a, e.t(), out=out)
+            vendor_launch(0)
+            own_launch(0)
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
-    n = max(10, launches // 4)
     with torch.cuda.stream(s):
         start.record(s)
         for _ in range(n):
-            torch.matmul(a, e.t(), out=out)
+            vendor_launch(0)
         stop.record(s)
     torch.cuda.synchronize()
     ms = start.elapsed_time(stop) / n
-    return {"op": f"torch.matmul FP16 [{w.rows}x{w.hidden}] x [{w.hidden}x{w.vocab}] -> FP16 logits",
-            "ms": round(ms, 4),
-            "TFLOPs": round(2.0 * w.rows * w.hidden * w.vocab / (ms * 1e-3) / 1e12, 1)}
+    own_ms = back_to_back_ms(s, own_launch, n)
+    ob = own.view(torch.int16).to(torch.int32)
+    vb = out.view(torch.int16).to(torch.int32)
+    # FP16 patterns as integers adjacent for adjacent floats across zero
+    ob = torch.where(ob < 0, -(ob & 0x7FFF), ob)
+    vb = torch.where(vb < 0, -(vb & 0x7FFF), vb)
+    max_ulps = int((ob - vb).abs().max().item())
+    shape = f"[{w.rows}x{w.hidden}] x [{w.hidden}x{w.vocab}] -> FP16 logits"
+    return {"op": f"torch.matmul FP16 {shape}", "ms": round(ms, 4),
+            "TFLOPs": round(flops / (ms * 1e-3) / 1e12, 1),
+            "projection_kernel": {"op": f"mf_linear_f16 {shape}", "ms": round(own_ms, 4),
+                                  "TFLOPs": round(flops / (own_ms * 1e-3) / 1e12, 1),
+                                  "max_ulps_vs_vendor": max_ulps}}
 
 
 def cpu_baseline(w, budget_s: float) -> dict:

@@ -430,14 +430,13 @@ mf_status mf_linear_f16(mf_buffer input, mf_buffer weight, mf_buffer output, uin
       input.address == output.address || weight.address == output.address) {
     return status(MF_INVALID_ARGUMENT);
   }
-  const bool mfma_shape = (input_features % 64u) == 0 && (input.address % 16u) == 0 &&
+  const bool mfma_shape = (input_features % 32u) == 0 && (input.address % 16u) == 0 &&
                           (weight.address % 16u) == 0 && output_features <= kU32Max &&
                           rows <= kU32Max;
   if (mfma_shape) {
     mf::ProjArgs p{};
     p.a16 = ptr<const uint16_t>(input.address);
     p.m = static_cast<uint32_t>(rows);
-    p.rows = static_cast<uint32_t>(rows);
     p.emb = ptr<const uint16_t>(weight.address);
     p.H = static_cast<uint32_t>(input_features);
     p.V = static_cast<uint32_t>(output_features);
@@ -1106,16 +1105,14 @@ mf_status mf_decode_tail_full_f16(const mf_decode_tail_args* args, uintptr_t str
   // 1. final RMSNorm (and its FP16 split for the MFMA projection)
   hipError_t e = mf::launch_tail_norm(norm_args(a, L, ws, true, true), s);
   if (e != hipSuccess) return launch_status(e);
-  // 2. full output projection of every row: FP32 scores [rows, V] of the
-  // FP16 hi/lo split of z on the MFMA projection kernel (the hand-written
-  // replacement of the reference's library GEMM, linear.cu:92-102), and the
-  // token norm bounds the exact selection needs
+  // 2. full output projection of every row: FP32 scores [rows, V] of z's
+  // FP16 hi on the MFMA projection kernel (the hand-written replacement of
+  // the reference's library GEMM, linear.cu:92-102), and the token norm
+  // bounds the exact selection needs
   {
     mf::ProjArgs pj{};
     pj.a16 = reinterpret_cast<const uint16_t*>(ws + L.y_hi);
-    pj.a16_lo = reinterpret_cast<const uint16_t*>(ws + L.y_lo);
     pj.m = static_cast<uint32_t>(a->rows);
-    pj.rows = static_cast<uint32_t>(a->rows);
     pj.emb = ptr<const uint16_t>(a->embedding.address);
     pj.H = static_cast<uint32_t>(a->hidden);
     pj.V = static_cast<uint32_t>(a->vocab);
@@ -1124,12 +1121,13 @@ mf_status mf_decode_tail_full_f16(const mf_decode_tail_args* args, uintptr_t str
     e = mf::launch_projection(pj, s);
     if (e != hipSuccess) return launch_status(e);
   }
-  // 3. restricted selection over the scores (unrestricted rows: every id)
+  // 3. restricted selection over the scores (unrestricted rows: every id),
+  // windows from the bound of a score on the FP16 hi alone
   mf::GatherArgs g = gather_args(a, L, ws);
   g.scores = scores;
   g.row_norm = reinterpret_cast<const float*>(ws + L.row_norm);
   g.tok_norm = tok_norm;
-  mfma_bound_coefs(a->hidden, g.coef, g.coef2);
+  pass_bound_coefs(a->hidden, g.coef, g.coef2);
   g.groups = device_cus();
   e = mf::launch_gather(ScoreSource::kLookup, g, s);
   if (e != hipSuccess) return launch_status(e);

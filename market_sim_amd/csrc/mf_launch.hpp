@@ -269,25 +269,18 @@ hipError_t launch_gather(ScoreSource source, const GatherArgs& args, hipStream_t
 hipError_t launch_gather_mfma(const GatherArgs& args, hipStream_t stream);  // mf_gather.hip
 hipError_t launch_finalize(const FinalizeArgs& args, hipStream_t stream);
 
-// ---- MFMA projection (mf_mfma.hip) ----------------------------------------
+// ---- MFMA projection (mf_gemm.hip) ----------------------------------------
 
 struct ProjArgs {
-  // A operand rows: FP32 normalized hidden y[rows] selected through row_index
-  // (null: identity) and split on the fly into FP16 hi + lo parts, or FP16
-  // input rows used as they are (a16).
-  const float* y;
-  const uint16_t* a16;
-  const uint16_t* a16_lo;  // with a16: FP16 lo parts of a split pair (a16 = hi)
-  const uint32_t* row_index;
+  const uint16_t* a16; // [m, H] FP16 A operand rows
   uint32_t m;          // number of A rows
-  uint32_t rows;       // bound of row_index entries (out-of-range rows read as 0)
   const uint16_t* emb; // [V, H] B operand (row-major, token-major)
-  uint32_t H;
+  uint32_t H;          // a multiple of 32; rows 16-byte aligned
   uint32_t V;
-  // epilogues (any subset)
+  // exactly one of the two outputs
   float* out_f32;      // [m, V] FP32 scores
   uint16_t* out_f16;   // [m, V] FP16 rounded scores
-  float* tok_norm;     // [V] ||e_t|| upper bounds, written by M-tile 0
+  float* tok_norm;     // [V] ||e_t|| upper bounds, written by M-tile 0 (or null)
 };
 
 hipError_t launch_projection(const ProjArgs& args, hipStream_t stream);

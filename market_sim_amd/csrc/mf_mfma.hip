@@ -1,19 +1,9 @@
-// gfx950 MFMA kernels: dense products against the whole FP16 table.
-//
-// (1) The head of the unrestricted rows (vocab_head_*_kernel): every token's
-//     score against the rows' FP16 hi/lo split, reduced in a windowed-argmax
-//     epilogue to tile records (no logits written).
-// (2) linear_f16 (projection_kernel): FP16 logits, the reference's
-//     cublasGemmEx call.  Tiling: a 256-thread workgroup owns 32 A rows x 128
-//     tokens; each wave computes one 32x32 block with
-//     v_mfma_f32_32x32x16_f16.  K runs in chunks of 64 features; per chunk
-//     the workgroup stages the 128 x 64 FP16 slice of E and the 32 x 64 A
-//     slice in LDS (double-buffered, rows padded to 144 bytes so b128 reads
-//     are bank-conflict free), with four chunks' global loads in flight.
-//
-// FP32 hidden values enter as the FP16 pair hi = rne(y), lo = rne(y - hi)
-// (two MFMAs per step), so the fast score is accurate to ~2^-22 relative
-// before the reference-order rescore.
+// gfx950 MFMA kernels: the head of the unrestricted rows
+// (vocab_head_*_kernel): every token's score against the rows' FP16 hi/lo
+// split, reduced in a windowed-argmax epilogue to tile records (no logits
+// written).  The FP16 hi + lo pair of an FP32 value (two MFMAs per step)
+// makes the fast score accurate to ~2^-22 relative before the
+// reference-order rescore.
 #include <hip/hip_runtime.h>
 
 #include "mf_device.hpp"
@@ -25,211 +15,7 @@ namespace {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-constexpr int kThreads = 256;
-constexpr int kTileTokens = 128;
 constexpr int kMTile = 32;
-constexpr int kKC = 64;          // features per chunk
-constexpr int kRowHalves = 72;   // padded LDS row: 64 + 8 halves = 144 B
-
-struct ProjShared {
-  union {
-    struct {
-      _Float16 b[2][kTileTokens][kRowHalves];   // 36,864 B
-      _Float16 a[2][2][kMTile][kRowHalves];     // [buf][hi|lo] 18,432 B
-    } k;
-    struct {
-      float g[kMTile][kTileTokens];
-      float b[kMTile][kTileTokens];
-    } epi;                                      // 32,768 B
-  };
-};
-
-enum class ASrc { kF32Split, kF16Pair, kF16 };
-
-struct AView {
-  const float* y;           // kF32Split
-  const uint16_t* hi;       // kF16Pair, kF16
-  const uint16_t* lo;       // kF16Pair
-  const uint32_t* row_index;
-  uint32_t m;
-  uint32_t rows;
-  uint32_t H;
-};
-
-// Source row of A row m (row_index applied; 0xFFFFFFFF reads as zeros).
-__device__ __forceinline__ uint32_t a_source_row(const AView& A, uint32_t m) {
-  if (m >= A.m) return 0xFFFFFFFFu;
-  return A.row_index != nullptr ? A.row_index[m] : m;
-}
-
-// Per-thread registers holding one chunk in flight: 4 B pieces (16 B each)
-// and the A piece (hi and lo, 16 B each).
-struct ChunkRegs {
-  uint4 b[4];
-  uint4 ahi;
-  uint4 alo;
-};
-
-template <ASrc kA>
-__device__ __forceinline__ void load_chunk(const AView& A, const uint16_t* emb, uint32_t V,
-                                           uint32_t tok0, uint32_t row, uint32_t c,
-                                           ChunkRegs& r) {
-  const uint32_t t = threadIdx.x;
-  const uint32_t part = t % 8;
-  const uint32_t f = c * kKC + part * 8;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const uint32_t token = tok0 + t / 8 + 32 * j;
-    r.b[j] = token < V ? *reinterpret_cast<const uint4*>(emb + static_cast<uint64_t>(token) * A.H + f)
-                       : uint4{0u, 0u, 0u, 0u};
-  }
-  // A: 32 rows x 8 pieces = 256 pieces, one per thread (row resolved by
-  // the caller once per kernel)
-  r.ahi = uint4{0u, 0u, 0u, 0u};
-  r.alo = uint4{0u, 0u, 0u, 0u};
-  if (row < A.rows) {
-    const uint64_t o = static_cast<uint64_t>(row) * A.H + f;
-    if constexpr (kA == ASrc::kF32Split) {
-      const float4* src = reinterpret_cast<const float4*>(A.y + o);
-      const float4 v0 = src[0];
-      const float4 v1 = src[1];
-      const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-      half8_t hi, lo;
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const _Float16 h = static_cast<_Float16>(v[k]);
-        hi[k] = h;
-        lo[k] = static_cast<_Float16>(v[k] - static_cast<float>(h));
-      }
-      r.ahi = __builtin_bit_cast(uint4, hi);
-      r.alo = __builtin_bit_cast(uint4, lo);
-    } else {
-      r.ahi = *reinterpret_cast<const uint4*>(A.hi + o);
-      if constexpr (kA == ASrc::kF16Pair) r.alo = *reinterpret_cast<const uint4*>(A.lo + o);
-    }
-  }
-}
-
-__device__ __forceinline__ void store_chunk(ProjShared& sh, int buf, const ChunkRegs& r) {
-  const uint32_t t = threadIdx.x;
-  const uint32_t part = t % 8;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    *reinterpret_cast<uint4*>(&sh.k.b[buf][t / 8 + 32 * j][part * 8]) = r.b[j];
-  }
-  *reinterpret_cast<uint4*>(&sh.k.a[buf][0][t / 8][part * 8]) = r.ahi;
-  *reinterpret_cast<uint4*>(&sh.k.a[buf][1][t / 8][part * 8]) = r.alo;
-}
-
-// MFMAs of one staged chunk (LDS buffer buf): the hi and lo halves of A
-// accumulate separately (two independent MFMA chains) and are added once at
-// the end.
-template <ASrc kA>
-__device__ __forceinline__ void mma_chunk(const ProjShared& sh, int buf, floatx16& acc_hi,
-                                          floatx16& acc_lo, float& tok_sq) {
-  const int lane = threadIdx.x % 64;
-  const int wave = threadIdx.x / 64;
-  const int g = lane / 32;
-  const int i = lane % 32;
-#pragma unroll
-  for (int s = 0; s < kKC / 16; ++s) {
-    const half8_t b = *reinterpret_cast<const half8_t*>(&sh.k.b[buf][wave * 32 + i][s * 16 + g * 8]);
-    const half8_t ahi = *reinterpret_cast<const half8_t*>(&sh.k.a[buf][0][i][s * 16 + g * 8]);
-    acc_hi = __builtin_amdgcn_mfma_f32_32x32x16_f16(ahi, b, acc_hi, 0, 0, 0);
-    if constexpr (kA != ASrc::kF16) {
-      const half8_t alo = *reinterpret_cast<const half8_t*>(&sh.k.a[buf][1][i][s * 16 + g * 8]);
-      acc_lo = __builtin_amdgcn_mfma_f32_32x32x16_f16(alo, b, acc_lo, 0, 0, 0);
-    }
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const float e = static_cast<float>(b[k]);
-      tok_sq = __builtin_fmaf(e, e, tok_sq);
-    }
-  }
-}
-
-// Step c of the pipeline (chunk k travels through register set k % 4): the
-// load of chunk c + 4 into the set chunk c left, the MFMAs of chunk c, then
-// chunk c + 1 into the other LDS buffer.  Four chunks are in flight from
-// HBM while one is multiplied.
-template <ASrc kA>
-__device__ __forceinline__ void pipeline_step(const AView& A, const uint16_t* emb, uint32_t V,
-                                              uint32_t tok0, uint32_t arow, uint32_t c,
-                                              uint32_t chunks, ChunkRegs& free_set,
-                                              const ChunkRegs& next_set, ProjShared& sh,
-                                              floatx16& acc_hi, floatx16& acc_lo,
-                                              float& tok_sq) {
-  if (c >= chunks) return;
-  if (c + 4 < chunks) load_chunk<kA>(A, emb, V, tok0, arow, c + 4, free_set);
-  mma_chunk<kA>(sh, c & 1, acc_hi, acc_lo, tok_sq);
-  if (c + 1 < chunks) store_chunk(sh, (c + 1) & 1, next_set);
-  __syncthreads();
-}
-
-// The wave's 32 x 32 block (rows m0.., tokens tok0 + 32 * wave ..).  Returns
-// the accumulator and the lane's sum of squares of its B values; combined
-// across the two lane groups that is ||e_token||^2 of token lane % 32.
-template <ASrc kA>
-__device__ floatx16 project_block(const AView& A, const uint16_t* emb, uint32_t V,
-                                  uint32_t m0, uint32_t tok0, ProjShared& sh, float& tok_sq) {
-  floatx16 acc_hi, acc_lo;
-#pragma unroll
-  for (int v = 0; v < 16; ++v) {
-    acc_hi[v] = 0.0f;
-    acc_lo[v] = 0.0f;
-  }
-  tok_sq = 0.0f;
-  const uint32_t chunks = A.H / kKC;
-  const uint32_t arow = a_source_row(A, m0 + threadIdx.x / 8);
-  ChunkRegs r0, r1, r2, r3;
-  load_chunk<kA>(A, emb, V, tok0, arow, 0, r0);
-  if (chunks > 1) load_chunk<kA>(A, emb, V, tok0, arow, 1, r1);
-  if (chunks > 2) load_chunk<kA>(A, emb, V, tok0, arow, 2, r2);
-  if (chunks > 3) load_chunk<kA>(A, emb, V, tok0, arow, 3, r3);
-  store_chunk(sh, 0, r0);
-  __syncthreads();
-  for (uint32_t c = 0; c < chunks; c += 4) {
-    pipeline_step<kA>(A, emb, V, tok0, arow, c, chunks, r0, r1, sh, acc_hi, acc_lo, tok_sq);
-    pipeline_step<kA>(A, emb, V, tok0, arow, c + 1, chunks, r1, r2, sh, acc_hi, acc_lo, tok_sq);
-    pipeline_step<kA>(A, emb, V, tok0, arow, c + 2, chunks, r2, r3, sh, acc_hi, acc_lo, tok_sq);
-    pipeline_step<kA>(A, emb, V, tok0, arow, c + 3, chunks, r3, r0, sh, acc_hi, acc_lo, tok_sq);
-  }
-  tok_sq += __shfl_xor(tok_sq, 32);
-  if constexpr (kA == ASrc::kF16) return acc_hi;
-  return acc_hi + acc_lo;
-}
-
-// Accumulator element v of lane l holds D[row][col] with col = l % 32 and
-// row = 8 * (v / 4) + 4 * (l / 32) + v % 4 (the 32x32 MFMA output layout).
-__device__ __forceinline__ int acc_row(int v, int lane) {
-  return 8 * (v / 4) + 4 * (lane / 32) + (v % 4);
-}
-
-template <ASrc kA>
-__global__ __launch_bounds__(kThreads) void projection_kernel(ProjArgs p) {
-  __shared__ ProjShared sh;
-  const uint32_t m0 = blockIdx.y * kMTile;
-  const int lane = threadIdx.x % 64;
-  const int wave = threadIdx.x / 64;
-  const uint32_t tok0 = blockIdx.x * kTileTokens;
-  const uint32_t token = tok0 + wave * 32 + (lane % 32);
-  const AView A{p.y, p.a16, p.a16_lo, p.row_index, p.m, p.rows, p.H};
-  float tok_sq;
-  const floatx16 acc = project_block<kA>(A, p.emb, p.V, m0, tok0, sh, tok_sq);
-  if (token >= p.V) return;
-  if (p.tok_norm != nullptr && blockIdx.y == 0 && lane < 32) {
-    p.tok_norm[token] = __fsqrt_rn(tok_sq) * (1.0f + 0x1p-7f);
-  }
-#pragma unroll
-  for (int v = 0; v < 16; ++v) {
-    const uint32_t row = m0 + acc_row(v, lane);
-    if (row < p.m) {
-      const uint64_t o = static_cast<uint64_t>(row) * p.V + token;
-      if (p.out_f32 != nullptr) p.out_f32[o] = acc[v];
-      if (p.out_f16 != nullptr) p.out_f16[o] = float_to_half_rne(acc[v]);
-    }
-  }
-}
 
 // Reductions over the 8 consecutive lanes that share one row.
 __device__ __forceinline__ float group8_max(float v) {
@@ -466,19 +252,6 @@ __global__ __launch_bounds__(kWideWaves * 64) void vocab_head_wide_kernel(Fallba
 
 uint32_t fallback_tiles(uint32_t vocab) {
   return (vocab + kHeadTileTokens - 1) / kHeadTileTokens;
-}
-
-hipError_t launch_projection(const ProjArgs& args, hipStream_t stream) {
-  if (args.H % kKC != 0) return hipErrorInvalidValue;
-  const dim3 grid((args.V + kTileTokens - 1) / kTileTokens, (args.m + kMTile - 1) / kMTile);
-  if (args.a16 != nullptr && args.a16_lo != nullptr) {
-    hipLaunchKernelGGL((projection_kernel<ASrc::kF16Pair>), grid, dim3(kThreads), 0, stream, args);
-  } else if (args.a16 != nullptr) {
-    hipLaunchKernelGGL((projection_kernel<ASrc::kF16>), grid, dim3(kThreads), 0, stream, args);
-  } else {
-    hipLaunchKernelGGL((projection_kernel<ASrc::kF32Split>), grid, dim3(kThreads), 0, stream, args);
-  }
-  return hipGetLastError();
 }
 
 // Narrow-row variant per H = 32 kSteps (H % 64 == 0, panel tile <= 76 KiB).

@@ -91,6 +91,17 @@ def test_cfg3_full_size_b256():
     _same(_run(w, full=True), exp)
 
 
+@pytest.mark.parametrize("vocab,rows", [(1001, 300), (4096, 257)])
+def test_full_comparator_tile_edges(vocab, rows):
+    """The full-vocabulary comparator where its projection tiles are cut: a
+    vocabulary that is not a multiple of 8 (the scores leave element by
+    element) or of 192 (a partial token tile), and more than 256 rows (two
+    row tiles; the token norms come from the first)."""
+    w = wl.config(3, seed=7, scale_vocab=vocab, scale_rows=rows)
+    exp = _oracle(w, threads=16)
+    _same(_run(w, full=True), exp)
+
+
 def test_cfg3_full_size_mul_add_order():
     w = wl.config(3, seed=1)
     _same(_run(w, order=abi.ORDER_MUL_ADD_CHAIN),
@@ -411,8 +422,10 @@ def test_unrestricted_row_window_covers_the_hi_rounding():
     """The table pass scores unrestricted rows on the FP16 hi of z alone, so
     their windows must carry |z - hi| <= 2^-11 |z| (the hi-only bound, as for
     the candidates); with the hi+lo bound the exact winner A falls outside
-    the window and B is returned."""
+    the window and B is returned.  The full-vocabulary comparator projects
+    the FP16 hi alone as well and takes the same bound."""
     w = _hi_rounding_near_tie()
     exp = _oracle(w)
     assert exp[0].tolist() == [10, 10]
     _same(_run(w), exp)
+    _same(_run(w, full=True), exp)

@@ -267,6 +267,32 @@ def test_linear_f16_matches_reference_test(rows, inf, outf):
         assert ulps.max() <= 1
 
 
+@pytest.mark.parametrize("rows,inf,outf", [(1, 32, 5), (300, 64, 400), (257, 96, 193),
+                                           (256, 960, 4800), (512, 128, 192)])
+def test_linear_f16_mfma_tiles_random(rows, inf, outf):
+    """The MFMA projection over random FP16 data at shapes that cut its
+    256-row x 192-token tiles and its 32-feature chunks (one chunk, two,
+    three; several row tiles; a partial token tile): every output within
+    half an FP16 ulp plus the FP32 accumulation bound 2 H 2^-24 sum |x w|
+    of the exact product (float64)."""
+    from market_sim_amd import ops
+    rng = np.random.default_rng(rows * 7 + inf)
+    x = rng.uniform(-1.0, 1.0, (rows, inf)).astype(np.float16)
+    w = rng.uniform(-1.0, 1.0, (outf, inf)).astype(np.float16)
+    out = empty(rows * outf, np.uint16)
+    xd, wd = dev(x.view(np.uint16)), dev(w.view(np.uint16))
+    ok(ops.linear_f16(B(xd), B(wd), B(out), rows, inf, outf, stream()))
+    got = host(out, np.uint16).reshape(rows, outf).view(np.float16).astype(np.float64)
+    x64, w64 = x.astype(np.float64), w.astype(np.float64)
+    exact = x64 @ w64.T
+    mag = np.abs(x64) @ np.abs(w64).T
+    half_ulp = np.spacing(np.maximum(np.abs(got), np.abs(exact)).astype(np.float16)).astype(
+        np.float64) / 2
+    err = np.abs(got - exact)
+    assert np.all(err <= half_ulp + 2.0 * inf * 2.0 ** -24 * mag), float(
+        np.max(err - half_ulp))
+
+
 def _ordered(bits: np.ndarray) -> np.ndarray:
     """FP16 bit patterns mapped to integers that are adjacent for adjacent
     floats across the sign boundary."""

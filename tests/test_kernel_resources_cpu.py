@@ -73,5 +73,6 @@ def test_no_kernel_uses_scratch(tmp_path):
     assert any("head_kernel" in k for k in kernels)
     assert any("pass_kernel" in k for k in kernels)
     assert any("dense_kernel" in k for k in kernels)
+    assert any("projection_kernel" in k for k in kernels)
     with_scratch = {k: v for k, v in kernels.items() if v != 0}
     assert not with_scratch, with_scratch
