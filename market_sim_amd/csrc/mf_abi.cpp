@@ -461,6 +461,8 @@ struct TailLayout {
       fb_panel, fb_slot_row, fb_slot_norm, fb_slot_slack, scores, tok_norm, range_index,
       row_tiles, dense_spans, dense_flag, total;
   uint32_t tile, max_tiles, fb_tiles, fb_rows;
+  uint64_t short_counts, short_records;
+  uint32_t short_per_part, short_parts;
   bool pass;   // the table pass serves both kinds of rows
   bool fused;  // the one-kernel tail (short lists)
   bool dense;  // the dense head serves unrestricted rows and long ascending lists
@@ -500,16 +502,38 @@ bool table_pass(const mf_decode_tail_args* a) {
          mf::panel_tile_bytes(a->hidden) <= mf::kPanelLdsMaxBytes && a->rows <= mf::kPassRowsMax;
 }
 
-// The one-kernel tail: short lists (two rounds of the workgroup's stage of
-// candidate rows at most), no unrestricted rows, not switched off.
-bool fused_tail(const mf_decode_tail_args* a) {
-  if ((a->flags & MF_TAIL_NO_FUSED) || a->unrestricted_count > 0 ||
-      a->max_count > mf::kShortListMax || a->hidden % 8u != 0 || a->hidden > 65535u) {
+// The one-kernel tail: no unrestricted rows, not switched off, and every
+// list within kShortPartsMax parts of a workgroup's stage of candidate rows
+// (at most kShortListMax); a pack whose rows need more than one part each
+// must fit two workgroups per compute unit of an MI355X (256 CUs), beyond
+// which the gather's MFMA scores cost less than rescoring every candidate.
+// The parts then shrink (to no fewer than 32 candidates) while the pack
+// stays within two workgroups per compute unit: a compute unit moves only
+// so many bytes per microsecond, and smaller parts spread the staging.  Fixed numbers, not the device's: the
+// workspace layout must not depend on where it is sized.
+constexpr uint64_t kShortPlanCUs = 256;
+bool short_plan(const mf_decode_tail_args* a, uint32_t& per_part, uint32_t& parts) {
+  if ((a->flags & MF_TAIL_NO_FUSED) || a->unrestricted_count > 0 || a->hidden % 8u != 0 ||
+      a->hidden > 65535u) {
     return false;
   }
-  const uint32_t stage = mf::short_stage_rows(static_cast<uint32_t>(a->hidden),
-                                              static_cast<uint32_t>(a->max_count));
-  return stage > 0 && 2u * static_cast<uint64_t>(stage) >= a->max_count;
+  const uint32_t cap = mf::short_stage_rows(static_cast<uint32_t>(a->hidden), mf::kShortListMax);
+  if (cap == 0) return false;
+  const uint64_t lists = a->max_count == 0 ? 1u : a->max_count;
+  auto parts_of = [lists](uint64_t per) { return (lists + per - 1u) / per; };
+  if (parts_of(cap) > mf::kShortPartsMax) return false;
+  if (parts_of(cap) > 1u &&
+      (a->rows * parts_of(cap) > 2u * kShortPlanCUs || a->rows > mf::kShortCountRows)) {
+    return false;
+  }
+  uint64_t per = cap;
+  while (per >= 64u && a->rows * parts_of(per / 2u) <= 2u * kShortPlanCUs &&
+         parts_of(per / 2u) <= mf::kShortPartsMax) {
+    per /= 2u;
+  }
+  per_part = static_cast<uint32_t>(per);
+  parts = static_cast<uint32_t>(parts_of(per));
+  return true;
 }
 
 // The dense head (mf_dense.hip): lists declared ascending, a hidden size of
@@ -629,7 +653,7 @@ mf_status validate_tail(const mf_decode_tail_args* a, bool full, TailLayout& L) 
   L.fb_tiles = mf::fallback_tiles(static_cast<uint32_t>(a->vocab));
   // table pass: one record per (row, 192-token range) holding its ids
   L.pass = !full && table_pass(a);
-  L.fused = !full && !L.pass && fused_tail(a);
+  L.fused = !full && !L.pass && short_plan(a, L.short_per_part, L.short_parts);
   L.dense = !full && !L.pass && !L.fused && dense_head(a);
   if (L.pass) {
     const uint64_t longest = a->max_count == 0 ? 1 : a->max_count;
@@ -648,6 +672,13 @@ mf_status validate_tail(const mf_decode_tail_args* a, bool full, TailLayout& L) 
     off = align256(off + bytes);
     return at;
   };
+  // the one-kernel tail's arrival counters: at the start of every layout,
+  // which no other path writes, so they stay zero between calls whatever
+  // the calls' shapes
+  L.short_counts = take(mf::kShortCountRows * 4u);
+  L.short_records = take(L.fused && L.short_parts > 1u
+                             ? rows * L.short_parts * sizeof(mf::ShortPartRecord)
+                             : 0u);
   L.y = take(xe * 4u);
   L.row_inv = take(rows * 4u);
   L.row_norm = take(rows * 4u);
@@ -885,7 +916,13 @@ mf_status decode_tail_stage(const mf_decode_tail_args* args, uintptr_t stream, S
   switch (stage) {
     case Stage::kPrepare:
       if (L.fused) {
-        e = mf::launch_short(norm_args(a, L, ws, false, true), finalize_args(a, L, ws, false), s);
+        mf::ShortSplit sp{};
+        sp.records = reinterpret_cast<mf::ShortPartRecord*>(ws + L.short_records);
+        sp.counts = reinterpret_cast<uint32_t*>(ws + L.short_counts);
+        sp.per_part = L.short_per_part;
+        sp.parts = L.short_parts;
+        e = mf::launch_short(norm_args(a, L, ws, false, true), finalize_args(a, L, ws, false), sp,
+                             s);
         break;
       }
       e = mf::launch_tail_norm(

@@ -184,10 +184,14 @@ __host__ __device__ constexpr uint32_t panel_tiles(uint32_t m) {
 constexpr uint32_t kHeadTileTokens = 192;
 // Rows the table pass plans in LDS (one per thread of its workgroup).
 constexpr uint32_t kPassRowsMax = 256;
-// The one-kernel tail for short lists: longest list, and the LDS its
-// workgroup may take for x, the weight and the staged candidate rows.
+// The one-kernel tail for short lists: candidates per workgroup (one part
+// of a row's list), parts per row, the LDS a workgroup may take for x, the
+// weight and the staged candidate rows, and the rows whose arrival counters
+// the workspace keeps at its start.
 constexpr uint32_t kShortListMax = 128;
+constexpr uint32_t kShortPartsMax = 16;
 constexpr uint32_t kShortLdsBytes = 156u * 1024u;
+constexpr uint32_t kShortCountRows = 4096;
 constexpr uint32_t kPanelLdsMaxBytes = 76u * 1024u;
 
 struct GatherArgs {
@@ -362,9 +366,30 @@ struct DenseArgs {
 };
 // Slots one launch serves: (groups / 8) panels of kDensePanelSlots.
 hipError_t launch_dense(const DenseArgs& args, hipStream_t stream);
-// mf_short.hip: candidate rows one workgroup stages per round (0: H does
-// not fit), and the one-kernel tail
+// mf_short.hip: candidate rows one workgroup can stage (0: H does not
+// fit), and the one-kernel tail.  A row's list is cut into parts of
+// per_part candidates, one workgroup each; when a row has several, each
+// part leaves its selection in records[row * parts + part] and the last to
+// arrive on counts[row] (zero between calls: that part sets it back) merges
+// them.
+struct ShortPartRecord {
+  float score;
+  uint32_t token;
+  uint32_t pos;
+  uint32_t next;       // next state of the best candidate
+  uint32_t min_token;  // lowest id (an all-NaN row's selection)
+  uint32_t min_pos;
+  uint32_t min_next;
+  uint32_t invalid;
+};
+struct ShortSplit {
+  ShortPartRecord* records;  // [rows, parts]
+  uint32_t* counts;          // [rows]
+  uint32_t per_part;         // <= short_stage_rows(H, ...)
+  uint32_t parts;            // ceil(max_count / per_part) <= kShortPartsMax
+};
 uint32_t short_stage_rows(uint32_t H, uint32_t max_count);
-hipError_t launch_short(const TailNormArgs& norm, const FinalizeArgs& fin, hipStream_t stream);
+hipError_t launch_short(const TailNormArgs& norm, const FinalizeArgs& fin, const ShortSplit& split,
+                        hipStream_t stream);
 
 } // namespace mf

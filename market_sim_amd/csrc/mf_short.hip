@@ -1,15 +1,22 @@
-// One-kernel decode tail for packs of short lists (every list at most
-// kShortListMax ids, no unrestricted rows): the decode loop's case.
+// One-kernel decode tail for packs of short lists (no unrestricted rows):
+// the decode loop's case, and small packs of lists up to kShortPartsMax
+// parts of a workgroup's stage.
 //
-// One workgroup of four waves per row; every thread rescores one candidate
-// in the reference order (greedy.cu:171-176), so every score is exact and
-// no window, bound or record is needed.  Wave 0 runs the norm's
-// reference-order chain (operators.cpp:520-534) while waves 1-3 stage the
-// first round of candidate rows in LDS (every list of at most 128 ids in
-// one round at H <= 576; 24 pieces of 16 bytes per lane in flight).  The workgroup selects by
-// the reference rule (greedy.cu:84-100, 177-211: highest score, lowest id on
-// ties, NaN never wins, an all-NaN row takes its lowest id) and advances the
-// DFA.  The arithmetic is that of the multi-kernel path (row_list,
+// A row's list is cut into parts of per_part candidates, one workgroup of
+// four waves each; every thread rescores one candidate in the reference
+// order (greedy.cu:171-176), so every score is exact and no window, bound or
+// record of fast scores is needed.  Wave 0 runs the norm's reference-order
+// chain (operators.cpp:520-534) while waves 1-3 stage the part's candidate
+// rows in LDS (24 pieces of 16 bytes per lane in flight).  The workgroup
+// selects by the reference rule (greedy.cu:84-100, 177-211: highest score,
+// lowest id on ties, NaN never wins, an all-NaN row takes its lowest id).
+// With one part the workgroup writes the row's outputs and advances the
+// DFA; with several, each part leaves its selection in a record and the last
+// part to arrive merges the records (the same rule: the merge of the parts'
+// selections is the selection over the whole list) and finishes the row.
+// Records and counters are read and written with device-coherent accesses
+// only, so no part writes back or invalidates an L2.
+// The arithmetic is that of the multi-kernel path (row_list,
 // sequential_sum, norm_inverse, chain_lds), so both give identical bits.
 #include <hip/hip_runtime.h>
 
@@ -24,6 +31,18 @@ namespace {
 constexpr uint32_t kShortWaves = 4;
 constexpr uint32_t kShortThreads = kShortWaves * kWave;
 
+// The selection of a list (or part of one): the best candidate, the lowest
+// id and its position (for an all-NaN list), and whether an id lay outside
+// the vocabulary.
+struct ShortSel {
+  Best best;
+  uint32_t next;   // the best candidate's next state
+  uint32_t mt;
+  uint32_t mp;
+  uint32_t mnext;  // the lowest id's next state
+  uint32_t invalid;
+};
+
 struct ShortShared {
   RowMeta meta;
   uint32_t q;
@@ -35,6 +54,8 @@ struct ShortShared {
   uint32_t mt[kShortWaves];
   uint32_t mp[kShortWaves];
   uint32_t cand[kShortListMax];
+  uint32_t nx[kShortListMax];  // each candidate's next state
+  ShortSel parts[kShortPartsMax];  // the last part's copy of every part's record
 };
 
 // Stages candidates base + j of the row, j = part, part + parts, ... < m,
@@ -77,66 +98,65 @@ __device__ inline void stage_part(const TailNormArgs& n, const FinalizeArgs& f, 
   }
 }
 
-// Writes row r's outputs from the workgroup's per-wave results (thread 0).
-__device__ inline void short_select(const TailNormArgs& n, const FinalizeArgs& f,
-                                    const ShortShared& sh, const float* ys, uint32_t r,
-                                    const RowMeta& meta) {
+__device__ __forceinline__ ShortSel merge_sel(ShortSel a, const ShortSel& b) {
+  const Best m = best_of(a.best, b.best);
+  if (m.token != a.best.token || m.pos != a.best.pos) a.next = b.next;
+  a.best = m;
+  if (b.mt < a.mt || (b.mt == a.mt && b.mp < a.mp)) {
+    a.mt = b.mt;
+    a.mp = b.mp;
+    a.mnext = b.mnext;
+  }
+  a.invalid |= b.invalid;
+  return a;
+}
+
+// Writes row r's outputs from the selection over its whole list (one thread).
+__device__ inline void short_finish(const TailNormArgs& n, const FinalizeArgs& f, const float* ys,
+                                    uint32_t r, const RowMeta& meta, const ShortSel& sel) {
   const uint32_t H = n.H;
   uint32_t* slot = next_state_slot(n.out_next, n.row_sequence, n.capacity, r);
-  if (sh.invalid) {
+  if (sel.invalid) {
     // an id outside the vocabulary makes the row invalid (greedy.cu:163-166)
     f.out_token[r] = kInvalidToken;
     if (f.out_score != nullptr) f.out_score[r] = __builtin_nanf("");
     if (slot != nullptr) *slot = kInvalidToken;
     return;
   }
-  Best b = sh.best[0];
-  uint32_t mt = sh.mt[0];
-  uint32_t mp = sh.mp[0];
-  for (uint32_t w = 1; w < kShortWaves; ++w) {
-    b = best_of(b, sh.best[w]);
-    if (sh.mt[w] < mt || (sh.mt[w] == mt && sh.mp[w] < mp)) {
-      mt = sh.mt[w];
-      mp = sh.mp[w];
-    }
-  }
-  uint32_t token = b.token;
-  uint32_t pos = b.pos;
-  float score = b.score;
+  uint32_t token = sel.best.token;
+  uint32_t next = sel.next;
+  float score = sel.best.score;
   if (token == kInvalidToken) {
     // every score is NaN: the lowest id, with its own reference-order score
-    token = mt;
-    pos = mp;
+    token = sel.mt;
+    next = sel.mnext;
     const uint16_t* row = f.emb + static_cast<uint64_t>(token) * H;
     score = f.order == 1 ? chain_lds<true>(ys, row, H) : chain_lds<false>(ys, row, H);
   }
-  uint32_t next = kInvalidToken;
-  if (f.state_next != nullptr) {
-    next = f.state_next[meta.list_begin + pos];
-  } else if (f.next_table != nullptr) {
-    next = static_cast<uint32_t>(f.next_table[static_cast<uint64_t>(meta.state) * f.V + token]);
-  }
+  (void)meta;
   f.out_token[r] = token;
   if (f.out_score != nullptr) f.out_score[r] = score;
   if (slot != nullptr) *slot = next;
 }
 
 __global__ __launch_bounds__(kShortThreads) void short_tail_kernel(TailNormArgs n, FinalizeArgs f,
-                                                                   uint32_t stage_rows) {
+                                                                   ShortSplit split) {
   extern __shared__ __align__(16) float lds[];
   __shared__ ShortShared sh;
   const uint32_t H = n.H;
   const uint32_t tid = threadIdx.x;
   const uint32_t wave = tid / kWave;
   const uint32_t lane = tid % kWave;
-  const uint32_t r = blockIdx.x;
+  const uint32_t part = blockIdx.x;
+  const uint32_t r = blockIdx.y;
   float* xs = lds;               // x, then y in place
   float* sq = lds + H;
   float* ws = lds + 2u * H;
   uint16_t* es = reinterpret_cast<uint16_t*>(lds + 3u * H);
-  const uint32_t rs = H + 8u;
   const bool weighted = n.weight != nullptr;
 
+  // thread 0 walks the row's list while waves 1-3 bring in x (and its
+  // squares) and the weight
   if (tid == 0) {
     const RowList l = row_list(n, r);
     sh.meta = l.meta;
@@ -144,11 +164,10 @@ __global__ __launch_bounds__(kShortThreads) void short_tail_kernel(TailNormArgs 
     sh.b = l.b;
     sh.e = l.e;
     sh.invalid = 0u;
-  }
-  {
+  } else if (wave > 0) {
     const float4* x4 = reinterpret_cast<const float4*>(n.x + static_cast<uint64_t>(r) * H);
     const float4* w4 = reinterpret_cast<const float4*>(n.weight);
-    for (uint32_t q = tid; q < H / 4u; q += kShortThreads) {
+    for (uint32_t q = tid - kWave; q < H / 4u; q += kShortThreads - kWave) {
       const float4 v = x4[q];
       reinterpret_cast<float4*>(xs)[q] = v;
       reinterpret_cast<float4*>(sq)[q] = float4{v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w};
@@ -157,7 +176,13 @@ __global__ __launch_bounds__(kShortThreads) void short_tail_kernel(TailNormArgs 
   }
   __syncthreads();
   const RowMeta meta = sh.meta;
-  if (meta.kind != kRowRestricted) {
+  const bool restricted = meta.kind == kRowRestricted;
+  const uint32_t count = meta.count;
+  // the row's parts: one unless a restricted list is longer than a part
+  const uint32_t parts =
+      restricted && count > split.per_part ? (count + split.per_part - 1u) / split.per_part : 1u;
+  if (part >= parts) return;
+  if (!restricted) {
     // invalid rows, finished rows (an empty list: the state is held when
     // asked to), and unrestricted rows, which this path is never given
     if (tid == 0) {
@@ -170,13 +195,14 @@ __global__ __launch_bounds__(kShortThreads) void short_tail_kernel(TailNormArgs 
     }
     return;
   }
-  const uint32_t count = meta.count;
-  const uint32_t m0 = count < stage_rows ? count : stage_rows;
+  // this part's candidates: list positions base .. base + m - 1
+  const uint32_t base = part * split.per_part;
+  const uint32_t m = count - base < split.per_part ? count - base : split.per_part;
   if (wave == 0) {
     const float sum_squares = weighted ? sequential_sum_wave(sq, H) : 0.0f;
     if (lane == 0) sh.inv = weighted ? norm_inverse(sum_squares, H, n.epsilon) : 1.0f;
   } else {
-    stage_part(n, f, sh, es, 0u, m0, wave - 1u, kShortWaves - 1u);
+    stage_part(n, f, sh, es, base, m, wave - 1u, kShortWaves - 1u);
   }
   __syncthreads();
   // y = (x * inv) * w in the reference's roundings (operators.cpp:533-534)
@@ -189,31 +215,30 @@ __global__ __launch_bounds__(kShortThreads) void short_tail_kernel(TailNormArgs 
   Best best = best_identity();
   uint32_t mt = kInvalidToken;
   uint32_t mp = 0u;
-  uint32_t bad = 0u;
-  for (uint32_t base = 0; base < count; base += stage_rows) {
-    const uint32_t m = count - base < stage_rows ? count - base : stage_rows;
-    if (base > 0) {
-      __syncthreads();
-      stage_part(n, f, sh, es, base, m, wave, kShortWaves);
-      __syncthreads();
-    }
-    if (tid < m) {
-      const uint32_t token = sh.cand[tid];
-      const uint32_t pos = base + tid;
-      if (token >= n.V) {
-        bad = 1u;
-      } else {
-        const float s = f.order == 1 ? chain_lds<true>(xs, es + tid * rs, H)
-                                     : chain_lds<false>(xs, es + tid * rs, H);
-        best = best_of(best, best_leaf(s, token, pos));
-        if (token < mt) {
-          mt = token;
-          mp = pos;
-        }
+  if (tid < m) {
+    const uint32_t token = sh.cand[tid];
+    const uint32_t pos = base + tid;
+    if (token >= n.V) {
+      sh.invalid = 1u;
+    } else {
+      // the candidate's next state, loaded under the chain (greedy.cu
+      // leaves the advance to the caller; operators.cpp steps the DFA)
+      uint32_t nx = kInvalidToken;
+      if (f.state_next != nullptr) {
+        nx = f.state_next[meta.list_begin + pos];
+      } else if (f.next_table != nullptr) {
+        nx = static_cast<uint32_t>(f.next_table[static_cast<uint64_t>(meta.state) * f.V + token]);
       }
+      __builtin_amdgcn_sched_barrier(0);  // the load goes out before the chain
+      const uint32_t rs = H + 8u;
+      const float s = f.order == 1 ? chain_lds<true>(xs, es + tid * rs, H)
+                                   : chain_lds<false>(xs, es + tid * rs, H);
+      best = best_leaf(s, token, pos);
+      mt = token;
+      mp = pos;
+      sh.nx[tid] = nx;
     }
   }
-  if (bad) sh.invalid = 1u;
   best = wave_best(best);
   wave_min_token(mt, mp);
   if (lane == 0) {
@@ -222,7 +247,59 @@ __global__ __launch_bounds__(kShortThreads) void short_tail_kernel(TailNormArgs 
     sh.mp[wave] = mp;
   }
   __syncthreads();
-  if (tid == 0) short_select(n, f, sh, xs, r, meta);
+  if (wave != 0) return;
+  // wave 0 finishes: the part's selection (the same in every lane)
+  ShortSel sel{sh.best[0], 0u, sh.mt[0], sh.mp[0], 0u, sh.invalid};
+  for (uint32_t w = 1; w < kShortWaves; ++w) {
+    sel = merge_sel(sel, ShortSel{sh.best[w], 0u, sh.mt[w], sh.mp[w], 0u, 0u});
+  }
+  if (sel.best.token != kInvalidToken) sel.next = sh.nx[sel.best.pos - base];
+  if (sel.mt != kInvalidToken) sel.mnext = sh.nx[sel.mp - base];
+  if (parts == 1u) {
+    if (lane == 0) short_finish(n, f, xs, r, meta, sel);
+    return;
+  }
+  // The record and the arrival counter are device-coherent accesses
+  // (relaxed atomics at agent scope), so no fence has to write back or
+  // invalidate a whole L2: the record's stores are complete before this
+  // part arrives, and the last part reads the records after its arrival.
+  uint32_t* rec = reinterpret_cast<uint32_t*>(split.records + static_cast<uint64_t>(r) * split.parts);
+  constexpr uint32_t kWords = sizeof(ShortPartRecord) / 4u;
+  static_assert(kWords == 8, "a record is eight words");
+  if (lane == 0) {
+    const uint32_t mine[8] = {__float_as_uint(sel.best.score), sel.best.token, sel.best.pos,
+                              sel.next, sel.mt, sel.mp, sel.mnext, sel.invalid};
+#pragma unroll
+    for (uint32_t k = 0; k < 8u; ++k) {
+      __hip_atomic_store(rec + part * kWords + k, mine[k], __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  uint32_t arrived = 0u;
+  if (lane == 0) {
+    arrived = __hip_atomic_fetch_add(split.counts + r, 1u, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+  }
+  arrived = __builtin_amdgcn_readfirstlane(arrived);
+  if (arrived != parts - 1u) return;
+  asm volatile("" ::: "memory");
+  // the last part: every record is complete; lane k reads part k's, and the
+  // counter is zero again for the next call
+  if (lane == 0) __hip_atomic_store(split.counts + r, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (lane < parts) {
+    uint32_t x[8];
+#pragma unroll
+    for (uint32_t i = 0; i < 8u; ++i) {
+      x[i] = __hip_atomic_load(rec + lane * kWords + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    sh.parts[lane] = ShortSel{Best{__uint_as_float(x[0]), x[1], x[2]}, x[3], x[4], x[5], x[6], x[7]};
+  }
+  wave_sync();
+  if (lane != 0) return;
+  ShortSel all{best_identity(), kInvalidToken, kInvalidToken, 0u, kInvalidToken, 0u};
+  for (uint32_t k = 0; k < parts; ++k) all = merge_sel(all, sh.parts[k]);
+  short_finish(n, f, xs, r, meta, all);
 }
 
 }  // namespace
@@ -237,15 +314,20 @@ uint32_t short_stage_rows(uint32_t H, uint32_t max_count) {
   return static_cast<uint32_t>(rows < want ? rows : want);
 }
 
-hipError_t launch_short(const TailNormArgs& n, const FinalizeArgs& f, hipStream_t stream) {
-  const uint32_t stage_rows = short_stage_rows(n.H, n.max_count);
-  if (n.H % 8u != 0 || stage_rows == 0 || n.max_count > kShortListMax) {
+hipError_t launch_short(const TailNormArgs& n, const FinalizeArgs& f, const ShortSplit& split,
+                        hipStream_t stream) {
+  const uint32_t stage_rows = short_stage_rows(n.H, split.per_part);
+  if (n.H % 8u != 0 || stage_rows == 0 || split.per_part == 0 || stage_rows < split.per_part ||
+      split.per_part > kShortListMax || split.parts == 0 || split.parts > kShortPartsMax ||
+      static_cast<uint64_t>(split.per_part) * split.parts < n.max_count ||
+      (split.parts > 1u && (split.records == nullptr || split.counts == nullptr ||
+                            n.rows > kShortCountRows))) {
     return hipErrorInvalidValue;
   }
   const size_t lds = 3u * static_cast<size_t>(n.H) * sizeof(float) +
-                     static_cast<size_t>(stage_rows) * 2u * (n.H + 8u);
-  hipLaunchKernelGGL(short_tail_kernel, dim3(n.rows), dim3(kShortThreads), lds, stream, n,
-                     f, stage_rows);
+                     static_cast<size_t>(split.per_part) * 2u * (n.H + 8u);
+  hipLaunchKernelGGL(short_tail_kernel, dim3(split.parts, n.rows), dim3(kShortThreads), lds,
+                     stream, n, f, split);
   return hipGetLastError();
 }
 

@@ -239,7 +239,22 @@ def test_sorted_lists_flag_sizes_the_range_index():
     assert path_of() == abi.TAIL_PATH_FUSED
     assert path_of(flags=abi.TAIL_SORTED_LISTS) == abi.TAIL_PATH_FUSED
     assert path_of(max_count=128) == abi.TAIL_PATH_FUSED
-    assert path_of(max_count=129) == abi.TAIL_PATH_GATHER
+    # longer lists in parts of a workgroup's stage (128 candidate rows at
+    # hidden 576), up to 16 parts, while the pack fits two workgroups per
+    # compute unit (256 CUs)
+    assert path_of(max_count=129) == abi.TAIL_PATH_FUSED
+
+    def many(rows, max_count, vocab=4096):
+        return dict(rows=rows, max_count=max_count, vocab=vocab,
+                    x=b(0x10000000, rows * 576 * 4), embedding=b(0x30000000, vocab * 576 * 2),
+                    row_state=b(0x40000000, rows * 4), out_token=b(0x50000000, rows * 4),
+                    out_score=b(0x60000000, rows * 4), workspace=b(0x70000000, 1 << 30))
+
+    assert path_of(**many(256, 256)) == abi.TAIL_PATH_FUSED      # 512 workgroups
+    assert path_of(**many(257, 256)) == abi.TAIL_PATH_GATHER
+    assert path_of(**many(16, 2048)) == abi.TAIL_PATH_FUSED      # 16 parts
+    assert path_of(**many(16, 2049)) == abi.TAIL_PATH_GATHER
+    assert path_of(flags=nf, **many(16, 512)) == abi.TAIL_PATH_GATHER
     unr = dict(unrestricted_count=1, unrestricted_rows=b(0xC00000, 4))
     assert path_of(flags=abi.TAIL_SORTED_LISTS, **unr) == abi.TAIL_PATH_TABLE_PASS
     assert path_of(**unr) == abi.TAIL_PATH_GATHER

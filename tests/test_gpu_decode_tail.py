@@ -221,6 +221,51 @@ def test_invalid_rows_empty_lists_bad_ids_and_nan_hidden():
     assert got[0][restricted[3]] == abi.INVALID_TOKEN
 
 
+def test_lists_in_parts_edges():
+    """Lists of 300-900 ids: the one-kernel tail cuts them into parts of 32
+    candidates (24 rows), and the last part to finish merges the parts'
+    selections.  Rows whose whole list shares one embedding (an exact tie
+    across every part: the lowest id), an all-NaN hidden row (the lowest
+    id), an id outside the vocabulary in a list's last part (the row is
+    invalid), an empty list and a state beyond the table, all against the
+    oracle; then the same workspace again (the arrival counters reset)."""
+    w = wl.ragged_pack("parts", 41, 3000, 576, 24, "uniform", 900, 0.0, size_lo=300)
+    w.embedding = w.embedding.copy()
+    w.x = w.x.copy()
+    w.row_state = w.row_state.copy()
+    offs = w.state_offsets.astype(np.int64)
+    ids0 = w.state_tokens[offs[0]:offs[1]]
+    w.embedding[ids0] = w.embedding[ids0[-1]]
+    w.x[1] = np.nan
+    w.state_tokens = w.state_tokens.copy()
+    w.state_tokens[offs[3] - 1] = w.vocab + 3  # last id of row 2's list
+    w.row_state[3] = w.states + 5
+    s4 = int(w.row_state[4])
+    new_tokens = np.concatenate([w.state_tokens[:offs[s4]], w.state_tokens[offs[s4 + 1]:]])
+    offs[s4 + 1:] -= offs[s4 + 1] - offs[s4]
+    w.state_tokens = new_tokens.astype(np.uint32)
+    w.state_offsets = offs.astype(np.uint32)
+    exp = _oracle(w)
+    t = _tail(w)
+    got = t.run()
+    _same(got, exp)
+    assert got[0][0] == ids0.min()
+    assert got[0][2] == abi.INVALID_TOKEN and got[0][3] == abi.INVALID_TOKEN
+    assert got[0][4] == abi.INVALID_TOKEN
+    again = t.run()
+    for a, b in zip(got, again):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@pytest.mark.parametrize("rows,lo,hi", [(1, 1, 2048), (256, 129, 256), (7, 2, 1500)])
+def test_lists_in_parts_shapes(rows, lo, hi):
+    """Pack shapes at the one-kernel tail's limits: one row of up to 16
+    parts, 256 rows of two parts each (512 workgroups), a few rows with
+    lists from 2 to 1500 ids."""
+    w = wl.ragged_pack("parts", 43 + rows, 4096, 576, rows, "uniform", hi, 0.0, size_lo=lo)
+    _same(_run(w), _oracle(w))
+
+
 def test_exact_ties_pick_the_lowest_id():
     """Duplicated embedding rows give bit-identical scores in every order, so
     a row whose whole list shares one embedding must select its lowest id."""
@@ -374,8 +419,9 @@ def test_gather_tile_sizes(rows, lo, hi):
     of 64 candidates unless rows x ceil(longest / 64) < 1024, then 32 unless
     rows x ceil(longest / 32) < 1024, then 16): 16 rows of <= 512 ids take
     16-candidate tiles, 64 rows of 300-600 ids 32-candidate tiles, 128 rows
-    64-candidate tiles.  No unrestricted rows, lists above the one-kernel
-    tail's limit, so the modes without the table pass run the gather."""
+    64-candidate tiles.  No unrestricted rows: the separate mode runs the
+    gather (the automatic mode gives the first two packs to the one-kernel
+    tail, in parts)."""
     w = wl.ragged_pack("tiles", 71 + rows, 8192, 576, rows, "uniform", hi, 0.0, size_lo=lo)
     m = w.max_count
     t64 = rows * -(-m // 64)

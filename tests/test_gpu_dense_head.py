@@ -32,8 +32,12 @@ def _oracle(w, x=None, order=abi.ORDER_FMA_CHAIN, threads=16):
 
 
 def _tail(w, **kw):
+    """The decode tail without the one-kernel tail (MF_TAIL_NO_FUSED), which
+    takes small packs without unrestricted rows before the dense head is
+    considered; these tests are about the dense head and the gather."""
     from market_sim_amd.tail import DeviceTail
     kw.setdefault("sorted_lists", True)
+    kw.setdefault("fused", False)
     return DeviceTail(w, **kw)
 
 

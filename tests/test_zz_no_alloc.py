@@ -2,7 +2,8 @@
 workspace, no allocation) against mf_decode_tail_f16 with a caller workspace,
 through the C ABI: two calls in a row, the second with a smaller pack, for
 each kernel set the tail can take (table pass, gather + MFMA head, one-kernel
-tail, dense head + gather), and each against the oracle."""
+tail with whole lists and with lists in parts, dense head + gather), and each
+against the oracle."""
 import numpy as np
 import pytest
 
@@ -57,18 +58,24 @@ def _workloads(kind):
     elif kind == "dense":  # wide rows, long ascending lists
         big = wl.ragged_pack("dense", 57, 5000, 1024, 64, "log", 4000, 0.05)
         small = wl.ragged_pack("dense", 58, 4000, 1024, 24, "log", 3000, 0.1)
+    elif kind == "parts":  # one-kernel tail, lists in parts merged by the last part
+        big = wl.ragged_pack("parts", 59, 6000, 576, 24, "uniform", 900, 0.0, size_lo=300)
+        small = wl.ragged_pack("parts", 60, 3000, 576, 8, "uniform", 400, 0.0, size_lo=100)
     else:  # one-kernel tail: short lists, no unrestricted rows
         big = wl.synthetic_dfa_tail("short", 55, 8192, 576, 96, 32, 2, 100, 1)
         small = wl.synthetic_dfa_tail("short", 56, 4096, 576, 20, 16, 2, 60, 1)
     return big, small
 
 
-@pytest.mark.parametrize("kind", ["table_pass", "gather", "fused", "dense"])
+@pytest.mark.parametrize("kind", ["table_pass", "gather", "fused", "parts", "dense"])
 def test_noalloc_equals_workspace_entry_point_on_two_calls(kind):
     want_path = {"table_pass": abi.TAIL_PATH_TABLE_PASS, "gather": abi.TAIL_PATH_GATHER,
-                 "fused": abi.TAIL_PATH_FUSED, "dense": abi.TAIL_PATH_DENSE}[kind]
+                 "fused": abi.TAIL_PATH_FUSED, "parts": abi.TAIL_PATH_FUSED,
+                 "dense": abi.TAIL_PATH_DENSE}[kind]
     for w in _workloads(kind):
-        t = DeviceTail(w, sorted_lists=kind in ("table_pass", "dense"))
+        # (the gather kind switches the one-kernel tail off: its small pack
+        # would fit it)
+        t = DeviceTail(w, sorted_lists=kind in ("table_pass", "dense"), fused=kind != "gather")
         assert ops.decode_tail_path(t.args()) == want_path
         assert ops.decode_tail_workspace_bytes(t.args()) <= ops.decode_tail_noalloc_max_bytes()
         ref = _bits(t.run())
