@@ -225,18 +225,20 @@ mf_status mf_linear_f16(mf_buffer input, mf_buffer weight, mf_buffer output,
  * MF_TAIL_NO_DENSE keeps every restricted row on the gather.  The results
  * are the same.
  *
- * Short lists: a call with no unrestricted rows, max_count <= 128,
- * hidden % 8 == 0 and max_count within two rounds of one workgroup's LDS
- * stage of candidate rows (one round at hidden <= 576) runs as
- * ONE kernel in the prepare stage (norm,
- * exact reference-order scores of every candidate, selection and DFA
- * advance; the other three stages do nothing), unless the table pass is
- * chosen above or flags hold MF_TAIL_NO_FUSED.  The results are the same.
+ * Short lists: a call with no unrestricted rows, hidden % 8 == 0 and every
+ * list within 16 parts of one workgroup's LDS stage of candidate rows (128
+ * at hidden <= 576) runs as ONE kernel in the prepare stage (norm, exact
+ * reference-order scores of every candidate, selection and DFA advance; the
+ * other three stages do nothing), unless the table pass is chosen above or
+ * flags hold MF_TAIL_NO_FUSED.  When a list takes more than one part, the
+ * pack must also fit rows x parts <= 512 workgroups and rows <= 4096; the
+ * last part of a row to finish merges the parts.  The results are the same.
  *
  * Workspace: caller-allocated device memory of mf_decode_tail_workspace_bytes
- * bytes, zero-filled once by mf_workspace_init before first use.  Every call
- * leaves it ready for the next one; calls that overlap in time on the same
- * workspace race. */
+ * bytes, zero-filled once by mf_workspace_init before first use.  It starts
+ * with the one-kernel tail's per-row arrival counters, which every call of
+ * any shape leaves at zero; the rest is scratch.  Every call leaves it ready
+ * for the next one; calls that overlap in time on the same workspace race. */
 typedef struct mf_decode_tail_args {
   mf_buffer x;                 /* f32 [rows, hidden] (pre-norm hidden) */
   mf_buffer norm_weight;       /* f32 [hidden]; address 0: x is already normalized */
