@@ -70,7 +70,8 @@ def algorithmic_bytes(w) -> dict:
              B_u rows leave in their panels of 256 slots, then whole panels
              while a panel's lists hold 5 V / 2 ids); flops 2 S H V; the
              gather then moves the other restricted rows' bytes
-             (gather_rest)."""
+             (gather_rest: their distinct ids' rows; gather_rest_logical:
+             every candidate's row, the bytes its waves fetch)."""
     H, V = w.hidden, w.vocab
     counts = w.row_counts()
     restricted = w.row_state < w.states
@@ -96,9 +97,13 @@ def algorithmic_bytes(w) -> dict:
     U_rest = w.distinct_restricted_ids(rest)
     B_rest = int(rest.sum())
     gather_rest = 2 * H * U_rest + 4 * N_rest + 4 * H * B_rest + 4 * (B_rest + 1) + 12 * B_rest
+    # the same with every candidate's row (a duplicate id read once per row)
+    gather_rest_logical = (2 * H * N_rest + 4 * N_rest + 4 * H * B_rest + 4 * (B_rest + 1) +
+                           12 * B_rest)
     return dict(gather=gather, gather_logical=logical, N=N, U=U, B_r=B_r, B_u=B_u,
                 D=D, dense_bytes=2 * V * H + 2 * H * S, dense_flops=2 * S * H * V,
-                gather_rest=gather_rest, B_rest=B_rest,
+                gather_rest=gather_rest, gather_rest_logical=gather_rest_logical,
+                B_rest=B_rest,
                 fallback_bytes=2 * V * H + 4 * H * B_u + 8 * B_u,
                 fallback_flops=2 * B_u * H * V,
                 pass_bytes=2 * H * T + 4 * N + 4 * H * B + 4 * (B_r + 1) + 12 * B,
@@ -516,7 +521,9 @@ def main() -> int:
               "mfma_util": round(alg["dense_flops"] / (main_ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
               "gather_rest": {"kernel": "gather_mfma_kernel (the other restricted rows)",
                               "rows": alg["B_rest"], "avg_launch_us": round(rest_ms * 1e3, 2),
-                              "hbm_frac": round(alg["gather_rest"] / (rest_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}}
+                              "hbm_frac": round(alg["gather_rest"] / (rest_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                              "logical_frac": round(alg["gather_rest_logical"] / (rest_ms * 1e-3) / 1e9 /
+                                                    HBM_PEAK_GBS, 4)}}
     elif fused:
         # the same bytes as the gather: each distinct candidate row, the ids,
         # the hidden rows, the offsets and the outputs
