@@ -259,9 +259,12 @@ __global__ __launch_bounds__(kThreads) void dense_kernel(DenseArgs a) {
       for (uint32_t s = 0; s < steps; ++s) {
         // step s's copies have landed (later steps' may be in flight); then
         // every wave's copies are visible, and the stage step s - 1 used is
-        // free for step s + kStages - 1
+        // free for step s + kStages - 1 (this wave's LDS reads of it have
+        // returned).  A barrier without __syncthreads' release fence: that
+        // fence waits for every LDS-DMA copy in flight (vmcnt(0)), which
+        // would drain the later steps' copies each step.
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"((kStages - 2) * kDmaPerWave) : "memory");
-        __syncthreads();
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         issue(s + kStages - 1 < steps ? s + kStages - 1 : steps - 1u);
         const unsigned char* st = dyn + (s % kStages) * kStageBytes;
         half8_t fa[kRBw], fb[kTBw];
