@@ -69,19 +69,25 @@ __global__ __launch_bounds__(kWalkWaves * kWave) void tail_norm_kernel(TailNormA
 // in their panels (which read the table anyway) is filled for free, and a
 // further panel is added only while the lists it would take hold at least
 // dense_panel_ids ids (a panel's pass over the table costs about as much
-// as gathering that many candidate rows).  One workgroup; dynamic LDS:
-// dense_sort 4-byte keys, dense_sort the power of two >= rows.
-__global__ __launch_bounds__(kThreads) void dense_choose_kernel(TailNormArgs a) {
+// as gathering that many candidate rows).  One workgroup of kChooseThreads;
+// dynamic LDS: dense_sort 4-byte keys, dense_sort the power of two >= rows.
+// Up to kChooseThreads candidates are ranked by counting (thread i counts
+// the keys above key i and stores it at that rank: one barrier), more by a
+// bitonic sort (a barrier per stage).
+constexpr int kChooseThreads = 1024;
+__global__ __launch_bounds__(kChooseThreads) void dense_choose_kernel(TailNormArgs a) {
   // 32-bit keys (count << 13) | (8191 - row): descending order is longest
-  // first, then by row (rows < 8192, counts < 2^19 here)
+  // first, then by row (rows < 8192, counts < 2^19 here), all distinct
   extern __shared__ uint32_t keys[];
-  __shared__ uint32_t wave_part[kThreads / kWave];
-  __shared__ uint64_t wave_ids[kThreads / kWave];
+  constexpr uint32_t kChooseWaves = kChooseThreads / kWave;
+  __shared__ uint32_t wave_part[kChooseWaves];
+  __shared__ uint64_t wave_ids[kChooseWaves];
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid % kWave;
   const uint32_t wave = tid / kWave;
-  // the candidates, compacted in row order: thread segments and a block scan
-  const uint32_t per = (a.rows + kThreads - 1u) / kThreads;
+  // the candidates, compacted in row order: thread segments and a block
+  // scan (a segment's flags and counts loaded together)
+  const uint32_t per = (a.rows + kChooseThreads - 1u) / kChooseThreads;
   const uint32_t r0 = tid * per < a.rows ? tid * per : a.rows;
   const uint32_t r1 = r0 + per < a.rows ? r0 + per : a.rows;
   uint32_t local = 0u;
@@ -96,33 +102,44 @@ __global__ __launch_bounds__(kThreads) void dense_choose_kernel(TailNormArgs a) 
   __syncthreads();
   uint32_t at = incl - local;
   uint32_t nc = 0u;
-  for (uint32_t w = 0; w < kThreads / kWave; ++w) {
+  for (uint32_t w = 0; w < kChooseWaves; ++w) {
     at += w < wave ? wave_part[w] : 0u;
     nc += wave_part[w];
   }
   if (nc == 0u) return;
   for (uint32_t r = r0; r < r1; ++r) {
-    if (a.dense_flag[r] != 0u) keys[at++] = (a.row_meta[r].count << 13) | (8191u - r);
+    const uint32_t count = a.row_meta[r].count;
+    if (a.dense_flag[r] != 0u) keys[at++] = (count << 13) | (8191u - r);
   }
   uint32_t n2 = 1u;
   while (n2 < nc) n2 <<= 1;
-  for (uint32_t i = nc + tid; i < n2; i += kThreads) keys[i] = 0u;
+  for (uint32_t i = nc + tid; i < n2; i += kChooseThreads) keys[i] = 0u;
   __syncthreads();
-  // bitonic sort, descending: n2 / 2 compare-exchanges per stage
-  for (uint32_t k = 2; k <= n2; k <<= 1) {
-    for (uint32_t j = k >> 1; j > 0; j >>= 1) {
-      for (uint32_t p = tid; p < n2 / 2u; p += kThreads) {
-        const uint32_t i = (p / j) * 2u * j + (p % j);
-        const uint32_t l = i + j;
-        const uint32_t x = keys[i];
-        const uint32_t y = keys[l];
-        const bool descending = (i & k) == 0u;
-        if (descending ? x < y : x > y) {
-          keys[i] = y;
-          keys[l] = x;
+  if (nc <= static_cast<uint32_t>(kChooseThreads)) {
+    // rank of key tid: the keys above it (every lane reads the same key)
+    const uint32_t mine = tid < nc ? keys[tid] : 0u;
+    uint32_t rank = 0u;
+    for (uint32_t i = 0; i < nc; ++i) rank += keys[i] > mine ? 1u : 0u;
+    __syncthreads();
+    if (tid < nc) keys[rank] = mine;
+    __syncthreads();
+  } else {
+    // bitonic sort, descending: n2 / 2 compare-exchanges per stage
+    for (uint32_t k = 2; k <= n2; k <<= 1) {
+      for (uint32_t j = k >> 1; j > 0; j >>= 1) {
+        for (uint32_t p = tid; p < n2 / 2u; p += kChooseThreads) {
+          const uint32_t i = (p / j) * 2u * j + (p % j);
+          const uint32_t l = i + j;
+          const uint32_t x = keys[i];
+          const uint32_t y = keys[l];
+          const bool descending = (i & k) == 0u;
+          if (descending ? x < y : x > y) {
+            keys[i] = y;
+            keys[l] = x;
+          }
         }
+        __syncthreads();
       }
-      __syncthreads();
     }
   }
   // D: the free room of the unrestricted rows' panels, then whole panels
@@ -134,7 +151,7 @@ __global__ __launch_bounds__(kThreads) void dense_choose_kernel(TailNormArgs a) 
   while (D < nc) {
     const uint32_t end = D + kDensePanelSlots < nc ? D + kDensePanelSlots : nc;
     uint64_t ids = 0u;
-    for (uint32_t i = D + tid; i < end; i += kThreads) ids += keys[i] >> 13;
+    for (uint32_t i = D + tid; i < end; i += kChooseThreads) ids += keys[i] >> 13;
 #pragma unroll
     for (int m = kWave / 2; m > 0; m >>= 1) {
       const uint32_t lo = static_cast<uint32_t>(__shfl_xor(static_cast<int>(ids & 0xFFFFFFFFu), m));
@@ -144,12 +161,12 @@ __global__ __launch_bounds__(kThreads) void dense_choose_kernel(TailNormArgs a) 
     if (lane == 0) wave_ids[wave] = ids;
     __syncthreads();
     uint64_t total = 0u;
-    for (uint32_t w = 0; w < kThreads / kWave; ++w) total += wave_ids[w];
+    for (uint32_t w = 0; w < kChooseWaves; ++w) total += wave_ids[w];
     __syncthreads();
     if (total < a.dense_panel_ids) break;
     D = end;
   }
-  for (uint32_t i = tid; i < D; i += kThreads) {
+  for (uint32_t i = tid; i < D; i += kChooseThreads) {
     const uint32_t r = 8191u - (keys[i] & 8191u);
     a.row_meta[r].kind |= kRowDense;
   }
@@ -460,7 +477,7 @@ hipError_t launch_tail_norm(const TailNormArgs& args, hipStream_t stream) {
   hipLaunchKernelGGL(tail_norm_kernel, dim3(args.rows + slots + walks), dim3(threads),
                      norm_lds > walk_lds ? norm_lds : walk_lds, stream, args);
   if (args.dense_spans != nullptr) {
-    hipLaunchKernelGGL(dense_choose_kernel, dim3(1), dim3(kThreads),
+    hipLaunchKernelGGL(dense_choose_kernel, dim3(1), dim3(kChooseThreads),
                        static_cast<size_t>(args.dense_sort) * sizeof(uint32_t), stream, args);
   }
   return hipGetLastError();

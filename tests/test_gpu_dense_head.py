@@ -242,6 +242,18 @@ def test_long_lists_take_a_second_panel():
     _dense_and_gather(w)
 
 
+def test_more_candidate_lists_than_the_ranking_threads():
+    """1100 ascending lists of 300-600 ids, every one long enough for the
+    dense head: more candidates than the row choice ranks by counting
+    (1024), so it sorts them (bitonic); the longest fill whole panels while
+    a panel's lists hold 5/2 vocab ids (five panels here); exact against the
+    oracle and the gather."""
+    w = _pack(14, 6000, 1024, 1100, 600, 0.0, size_kind="uniform", size_lo=300)
+    lens = np.diff(w.state_offsets.astype(np.int64))[w.row_state]
+    assert (lens >= max(64, w.vocab // 256)).sum() > 1024
+    _dense_and_gather(w)
+
+
 def test_decode_steps_with_device_states():
     """A DFA tail at hidden 1024 with long lists: states carried on the device
     from step to step, every step exact."""
