@@ -420,6 +420,15 @@ __global__ __launch_bounds__(kThreads) void gather_planned_kernel(GatherArgs a) 
 // ---------------------------------------------------------------------------
 
 constexpr uint32_t kStage = 8;  // embedding rows staged in LDS per rescore pass
+// The rescoring keeps its operands in registers (rescore_segmented) when H
+// is a multiple of kChainSeg of at most kWave segments and the table is
+// 16-byte aligned; LDS then stages one embedding row (the all-NaN rows'
+// lowest id) instead of kStage, which lets more rows share a compute unit.
+__host__ __device__ inline uint32_t finalize_stage_rows(uint32_t H, const void* emb) {
+  const bool segmented = H % kChainSeg == 0u && H <= kChainSeg * kWave &&
+                         (reinterpret_cast<uintptr_t>(emb) & 15u) == 0;
+  return segmented ? 1u : kStage;
+}
 constexpr uint32_t kCandMax = 2 * kWave * kTileMembers;
 
 template <uint32_t kYRegs>
@@ -428,8 +437,8 @@ __global__ __launch_bounds__(kWave) void finalize_kernel(FinalizeArgs a) {
   __shared__ uint32_t cand_token[kCandMax];
   __shared__ uint32_t cand_pos[kCandMax];
   __shared__ FinalizeWords words;
-  const FinalizeLds L{lds, reinterpret_cast<uint16_t*>(lds + a.H), kStage, cand_token, cand_pos,
-                      kCandMax, &words};
+  const FinalizeLds L{lds, reinterpret_cast<uint16_t*>(lds + a.H), finalize_stage_rows(a.H, a.emb),
+                      cand_token, cand_pos, kCandMax, &words};
   const uint32_t r = blockIdx.x;
   const uint32_t lane = threadIdx.x;
   const RowMeta meta = a.row_meta[r];
@@ -526,7 +535,7 @@ hipError_t launch_gather(ScoreSource source, const GatherArgs& a, hipStream_t st
 
 hipError_t launch_finalize(const FinalizeArgs& a, hipStream_t stream) {
   const size_t lds = static_cast<size_t>(a.H) * sizeof(float) +
-                     static_cast<size_t>(kStage) * a.H * sizeof(uint16_t);
+                     static_cast<size_t>(finalize_stage_rows(a.H, a.emb)) * a.H * sizeof(uint16_t);
   if (a.H % 4u == 0 && a.H <= 4u * kWave * 4u) {
     hipLaunchKernelGGL(finalize_kernel<4>, dim3(a.rows), dim3(kWave), lds, stream, a);
   } else if (a.H % 4u == 0 && a.H <= 4u * kWave * 8u) {
