@@ -387,17 +387,17 @@ __device__ inline void finalize_row(const FinalizeArgs& a, uint32_t r, const Row
   }
 
   // ordinary tiles: members whose upper bound reaches lg (at most
-  // kTileMembers per tile), collected over all tiles without a barrier per
-  // sweep, then rescored together.  If the buffer would overflow, the
-  // collection is redone below in flushed sweeps.
-  wave_sync();
-  if (lane == 0) L.w->n_cand = 0u;
-  wave_sync();
-  uint32_t overflow = 0u;
+  // kTileMembers per tile), collected over all tiles, then rescored
+  // together.  Per block of tiles, the further members of every tile that
+  // reaches the window are loaded at once (one round trip), then appended in
+  // lane order by ballot: no LDS atomic, whose returned slot would cost a
+  // round trip per member.  If the buffer would overflow, the collection is
+  // redone below in flushed sweeps.
+  const uint64_t below = (1ull << lane) - 1ull;
+  uint32_t nc = 0u;
   for (uint32_t base = 0; base < ntiles; base += kWave * kRecBlock) {
     // a row with more blocks reloads each block's flags, member counts and
-    // first member (one round trip); the (rare) further members are read
-    // afterwards
+    // first member (one round trip)
     if (!resident) {
 #pragma unroll
       for (uint32_t u = 0; u < kRecBlock; ++u) {
@@ -408,18 +408,54 @@ __device__ inline void finalize_row(const FinalizeArgs& a, uint32_t r, const Row
         m0[u] = in ? recs[t].m[0] : TileMember{0u, 0u, 0.0f, -__builtin_huge_valf()};
       }
     }
+    // appends the members whose lanes have p set, in lane order
+    auto append = [&](bool p, const TileMember& mm) {
+      const uint64_t m = __ballot(p);
+      if (m == 0ull) return;
+      const uint32_t slot = nc + static_cast<uint32_t>(__popcll(m & below));
+      if (p && slot < L.cand_max) {
+        L.cand_token[slot] = mm.token;
+        L.cand_pos[slot] = mm.pos;
+      }
+      nc += static_cast<uint32_t>(__popcll(m));
+    };
+    uint32_t nm[kRecBlock];
+    uint32_t multi = 0u;
 #pragma unroll
     for (uint32_t u = 0; u < kRecBlock; ++u) {
       const uint32_t t = base + u * kWave + lane;
-      if (h[u].y != 0u || t >= ntiles) continue;
       // no member of a tile whose best upper bound is below the window
-      if (__uint_as_float(c[u].w) < lg) continue;
-      overflow |= collect_members(recs, t, c[u].z, m0[u], lg, L);
+      const bool take = h[u].y == 0u && t < ntiles && !(__uint_as_float(c[u].w) < lg);
+      nm[u] = take ? (c[u].z < kTileMembers ? c[u].z : static_cast<uint32_t>(kTileMembers)) : 0u;
+      multi |= nm[u] > 1u ? 1u : 0u;
+    }
+    if (__ballot(multi != 0u) == 0ull) {
+      // the common case, every tile in the window holds one member: a short
+      // path (one wave runs it, so its instruction count is its time)
+#pragma unroll
+      for (uint32_t u = 0; u < kRecBlock; ++u) append(nm[u] != 0u && m0[u].upper >= lg, m0[u]);
+      continue;
+    }
+    TileMember ms[kRecBlock][kTileMembers];
+#pragma unroll
+    for (uint32_t u = 0; u < kRecBlock; ++u) {
+      const uint32_t t = base + u * kWave + lane;
+      ms[u][0] = m0[u];
+#pragma unroll
+      for (uint32_t j = 1; j < static_cast<uint32_t>(kTileMembers); ++j) {
+        ms[u][j] = j < nm[u] ? recs[t].m[j] : TileMember{0u, 0u, 0.0f, -__builtin_huge_valf()};
+      }
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < kRecBlock; ++u) {
+#pragma unroll
+      for (uint32_t j = 0; j < static_cast<uint32_t>(kTileMembers); ++j) {
+        append(j < nm[u] && ms[u][j].upper >= lg, ms[u][j]);
+      }
     }
   }
   wave_sync();
-  if (wave_sum_u32(overflow) == 0u) {
-    const uint32_t nc = L.w->n_cand;
+  if (nc <= L.cand_max) {
     if (nc > 0) best = best_of(best, rescore_candidates(a, L, nc));
   } else {
     // flushed sweeps: a sweep of sw tiles adds at most sw kTileMembers =
@@ -436,10 +472,10 @@ __device__ inline void finalize_row(const FinalizeArgs& a, uint32_t r, const Row
         if (q.flags == 0u) collect_members(recs, t, q.n_members, q.m[0], lg, L);
       }
       wave_sync();
-      const uint32_t nc = L.w->n_cand;
+      const uint32_t n = L.w->n_cand;
       // flush when the next sweep could overflow the buffer, and at the end
-      if (nc > 0 && (nc > L.cand_max / 2u || t0 + sw >= ntiles)) {
-        best = best_of(best, rescore_candidates(a, L, nc));
+      if (n > 0 && (n > L.cand_max / 2u || t0 + sw >= ntiles)) {
+        best = best_of(best, rescore_candidates(a, L, n));
         wave_sync();
         if (lane == 0) L.w->n_cand = 0u;
         wave_sync();
