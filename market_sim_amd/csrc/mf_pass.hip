@@ -28,13 +28,14 @@
 // bottleneck: loads complete in issue order, and a wave issuing more than
 // the pipeline holds stalls until earlier loads drain, so the order of the
 // loads is the schedule:
-//   1. the plan's per-row values, then the tile's first block of table
-//      rows (it streams while the plan is scanned);
-//   2. (plan landed) scans over the rows, each candidate's row, then the
-//      rows of z to stage (copies straight into LDS) and the candidate ids;
-//   3. (all landed) the second block; buckets; block 0's token norms and
-//      candidates; the third block is issued; block 1's, then block 2's
-//      candidates, each as its rows land;
+//   1. the plan's per-row values, then the first half of the tile's first
+//      block of table rows (it streams while the plan is scanned);
+//   2. (plan landed) scans over the rows; the block's second half; each
+//      candidate's row, then the rows of z to stage (copies straight into
+//      LDS) and the candidate ids;
+//   3. (all landed) the second block's first half; buckets; its second
+//      half; block 0's token norms and candidates; the third block is
+//      issued; block 1's, then block 2's candidates, each as its rows land;
 //   4. the head's A rows are staged in LDS while the candidates' records
 //      are written; the head runs against the three blocks still in
 //      registers and writes its records.
@@ -263,12 +264,19 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
   const uint32_t kb = lane / 16;
 
   half8_t bt[kBlocks][kSteps];
-  auto load_block = [&](uint32_t t, int tb) {
+  // steps [s0, s1) of block tb's K range.  A whole block from all four waves
+  // (4 x 18 KiB at H = 576) is more than the compute unit keeps in flight,
+  // so the last wave's issue would stall until the first loads return; the
+  // blocks that precede a workgroup barrier are issued in two halves, the
+  // second after the barrier.
+  auto load_steps = [&](uint32_t t, int tb, int s0, int s1) {
     const uint32_t token = t * kHeadTileTokens + (wave * kBlocks + tb) * 16u + col;
     const uint16_t* src = f.emb + static_cast<uint64_t>(token < f.V ? token : 0u) * H + kb * 8u;
 #pragma unroll
-    for (int s = 0; s < kSteps; ++s) bt[tb][s] = *reinterpret_cast<const half8_t*>(src + s * 32);
+    for (int s = s0; s < s1; ++s) bt[tb][s] = *reinterpret_cast<const half8_t*>(src + s * 32);
   };
+  constexpr int kFirstHalf = kSteps / 2;
+  auto load_block = [&](uint32_t t, int tb) { load_steps(t, tb, 0, kSteps); };
   // The head's A operand: a panel tile's hi rows staged in LDS (slot j in
   // LDS slot j); its MFMAs against every block of the tile
   // (only the tile's real rows; the A rows of the others read whatever the
@@ -325,12 +333,14 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
     const uint4 ix = p.range_index[static_cast<uint64_t>(tile) * rows + ri];
     const float norm_r = p.row_norm[ri];
     const float slack_r = p.row_slack[ri];
-    // panel tile 0's slots (stored once the plan has landed)
+    // panel tile 0's slots (stored just before the head: they land well
+    // after the plan, and nothing earlier reads them)
     const HeadSlotLoad slot0 = head_slot_load(f, 0u, p.row_norm);
     __builtin_amdgcn_sched_barrier(0);
     // the tile's first block of table rows, behind the small loads: it
-    // streams while the plan is scanned and the rows of z are staged
-    load_block(tile, 0);
+    // streams while the plan is scanned and the rows of z are staged (its
+    // second half once the scans' barrier is passed)
+    load_steps(tile, 0, 0, kFirstHalf);
     __builtin_amdgcn_sched_barrier(0);
     MF_STAMP(1);
 
@@ -378,13 +388,15 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
         ps.prefix[tid] = bn;
         ps.rprefix[tid] = bh;
       }
-      head_slot_store(f, 0u, slot0, src_row, src_norm, src_slack);
       if (tid == kThreads - 1 && rows == kPassRowsMax) {
         ps.prefix[rows] = bn + n;
         ps.rprefix[rows] = bh + has;
       }
       __syncthreads();
     }
+    __builtin_amdgcn_sched_barrier(0);
+    load_steps(tile, 0, kFirstHalf, kSteps);
+    __builtin_amdgcn_sched_barrier(0);
     MF_STAMP(2);
 
     // (3) batches of whole rows.  The first is scored block by block as the
@@ -459,7 +471,7 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
       __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (first) MF_STAMP(5);
-      if constexpr (first) load_block(tile, 1);
+      if constexpr (first) load_steps(tile, 1, 0, kFirstHalf);
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (first) MF_STAMP(16);
       // buckets: each candidate in its 16-token block's bucket
@@ -526,6 +538,11 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
         }
       }
       __syncthreads();  // buckets and staged rows visible
+      if constexpr (first) {
+        __builtin_amdgcn_sched_barrier(0);
+        load_steps(tile, 1, kFirstHalf, kSteps);
+        __builtin_amdgcn_sched_barrier(0);
+      }
       if constexpr (first) MF_STAMP(6);
 
       // (4) this wave's blocks in landing order: token norms (first batch),
@@ -714,6 +731,7 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
 
     // (6) the unrestricted rows: the head against each panel tile's hi rows
     // (panel tile 0 was staged by the last batch) and its records
+    head_slot_store(f, 0u, slot0, src_row, src_norm, src_slack);
     for (uint32_t pt = 0; pt < panels; ++pt) {
       if (pt > 0u) {
         stage_panel(pt);  // the previous tile's readers are done
