@@ -347,11 +347,15 @@ __device__ inline void range_walk(const TailNormArgs& a, const RangeRow& w, cons
   // in flight at the join)
   constexpr uint32_t kChunks = 8;
   constexpr uint32_t kStep = kChunks * kWave;
+  // positions past this wave's share load its last id (one address per
+  // instruction), not the next wave's ids
+  const uint32_t end = hi < c ? hi : c;
+  const uint32_t last = end > 0u ? end - 1u : 0u;
   auto load = [&](uint32_t base, uint32_t (&ids)[kChunks], uint32_t (&pre)[kChunks]) {
 #pragma unroll
     for (uint32_t u = 0; u < kChunks; ++u) {
       const uint32_t q = base + u * kWave + lane;
-      const uint32_t qi = q < c ? q : c - 1u;
+      const uint32_t qi = q < end ? q : last;
       ids[u] = a.tokens[b + qi];
       pre[u] = a.tokens[b + (qi > 0u ? qi - 1u : 0u)];
     }
