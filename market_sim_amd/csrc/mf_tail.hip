@@ -78,7 +78,7 @@ constexpr int kChooseThreads = 1024;
 __global__ __launch_bounds__(kChooseThreads) void dense_choose_kernel(TailNormArgs a) {
   // 32-bit keys (count << 13) | (8191 - row): descending order is longest
   // first, then by row (rows < 8192, counts < 2^19 here), all distinct
-  extern __shared__ uint32_t keys[];
+  extern __shared__ __align__(16) uint32_t keys[];
   constexpr uint32_t kChooseWaves = kChooseThreads / kWave;
   __shared__ uint32_t wave_part[kChooseWaves];
   __shared__ uint64_t wave_ids[kChooseWaves];
@@ -91,7 +91,16 @@ __global__ __launch_bounds__(kChooseThreads) void dense_choose_kernel(TailNormAr
   const uint32_t r0 = tid * per < a.rows ? tid * per : a.rows;
   const uint32_t r1 = r0 + per < a.rows ? r0 + per : a.rows;
   uint32_t local = 0u;
-  for (uint32_t r = r0; r < r1; ++r) local += a.dense_flag[r] != 0u ? 1u : 0u;
+  // (rows <= kChooseThreads, the common case: the thread's row's flag and
+  // count in one round trip, kept for the compaction)
+  const bool one = per == 1u && r0 < r1;
+  const uint32_t flag0 = one ? a.dense_flag[r0] : 0u;
+  const uint32_t count0 = one ? a.row_meta[r0].count : 0u;
+  if (one) {
+    local = flag0 != 0u ? 1u : 0u;
+  } else {
+    for (uint32_t r = r0; r < r1; ++r) local += a.dense_flag[r] != 0u ? 1u : 0u;
+  }
   uint32_t incl = local;
 #pragma unroll
   for (int d = 1; d < kWave; d <<= 1) {
@@ -107,19 +116,30 @@ __global__ __launch_bounds__(kChooseThreads) void dense_choose_kernel(TailNormAr
     nc += wave_part[w];
   }
   if (nc == 0u) return;
-  for (uint32_t r = r0; r < r1; ++r) {
-    const uint32_t count = a.row_meta[r].count;
-    if (a.dense_flag[r] != 0u) keys[at++] = (count << 13) | (8191u - r);
+  if (one) {
+    if (flag0 != 0u) keys[at] = (count0 << 13) | (8191u - r0);
+  } else {
+    for (uint32_t r = r0; r < r1; ++r) {
+      const uint32_t count = a.row_meta[r].count;
+      if (a.dense_flag[r] != 0u) keys[at++] = (count << 13) | (8191u - r);
+    }
   }
   uint32_t n2 = 1u;
   while (n2 < nc) n2 <<= 1;
   for (uint32_t i = nc + tid; i < n2; i += kChooseThreads) keys[i] = 0u;
   __syncthreads();
   if (nc <= static_cast<uint32_t>(kChooseThreads)) {
-    // rank of key tid: the keys above it (every lane reads the same key)
+    // rank of key tid: the keys above it (every lane reads the same four
+    // keys at a time, then the last nc % 4 one by one)
     const uint32_t mine = tid < nc ? keys[tid] : 0u;
     uint32_t rank = 0u;
-    for (uint32_t i = 0; i < nc; ++i) rank += keys[i] > mine ? 1u : 0u;
+    const uint4* k4 = reinterpret_cast<const uint4*>(keys);
+    for (uint32_t i = 0; i < nc / 4u; ++i) {
+      const uint4 v = k4[i];
+      rank += (v.x > mine ? 1u : 0u) + (v.y > mine ? 1u : 0u) + (v.z > mine ? 1u : 0u) +
+              (v.w > mine ? 1u : 0u);
+    }
+    for (uint32_t i = nc & ~3u; i < nc; ++i) rank += keys[i] > mine ? 1u : 0u;
     __syncthreads();
     if (tid < nc) keys[rank] = mine;
     __syncthreads();
