@@ -102,6 +102,19 @@ def test_full_comparator_tile_edges(vocab, rows):
     _same(_run(w, full=True), exp)
 
 
+def test_vocab_past_one_tile_per_compute_unit():
+    """A vocabulary of 313 token tiles at H = 576: the table pass gives each
+    workgroup a run of two tiles (256 compute units), so its second tile
+    reissues the plan, the halves of blocks 0 and 1 and the head's slots
+    after the first tile's barriers; unrestricted rows included."""
+    w = wl.config(3, seed=12, scale_vocab=60000, scale_rows=64)
+    assert w.unrestricted_rows.size > 0
+    t = _tail(w)
+    if _MODE["mode"] == "table_pass":
+        assert t.table_pass
+    _same(t.run(), _oracle(w, threads=16))
+
+
 def test_cfg3_full_size_mul_add_order():
     w = wl.config(3, seed=1)
     _same(_run(w, order=abi.ORDER_MUL_ADD_CHAIN),
