@@ -125,7 +125,7 @@ struct alignas(16) PassShared {
   uint32_t rprefix[kPassRowsMax + 1];   // rows with candidates before row r
   uint32_t lo[kPassRowsMax];            // list position of the row's first id in the tile
   uint32_t rec[kPassRowsMax];           // record index of (row, tile)
-  uint32_t slot_row[kPassRowsMax];      // staged slot -> row (batch)
+  uint32_t slot_off[kPassRowsMax];      // staged slot -> byte offset of its row of z (batch)
   float rf1[kPassRowsMax];              // coef * ||z|| + coef2 of the row
   float rf2[kPassRowsMax];              // its absolute error term
   uint32_t row_lower[kPassRowsMax];     // per row: max of g - b, order-preserving bits
@@ -182,54 +182,77 @@ __device__ __forceinline__ uint32_t last_within(const uint32_t* v, uint32_t rows
   return lo;
 }
 
-// Copies `n` FP16 rows of H halves into LDS slots (slot_bytes(H) each),
-// wave w taking the 1 KiB copies w, w + 4, ...: piece q of the area is 16
-// bytes of slot q / per at offset q % per; src(i) is slot i's row.  The pad
-// pieces and the lanes past the last piece read piece 0 of a staged row.
-template <uint32_t H, typename Src>
-__device__ __forceinline__ void stage_rows(unsigned char* area, uint32_t n, Src src) {
+// Copies the first n slots of a panel tile (slots of [hi | lo], kPanelPad
+// halves after each) into LDS slots of slot_bytes(H): the hi half with its
+// pad.  Wave w takes the 1 KiB copies w, w + 4, ...: piece q of the area is
+// piece q % per of slot q / per; each lane steps its slot and piece from one
+// copy of its wave to the next (no division per copy).  Lanes past the last
+// piece copy piece 0.
+template <uint32_t H>
+__device__ __forceinline__ void stage_panel_rows(unsigned char* area, uint32_t n,
+                                                 const uint16_t* base) {
   constexpr uint32_t per = slot_bytes(H) / 16u;
+  constexpr uint32_t kStride = kWaves * kWave;
   const uint32_t lane = threadIdx.x % kWave;
-  const uint32_t wave = threadIdx.x / kWave;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const uint32_t pieces = n * per;
+  const unsigned char* b = reinterpret_cast<const unsigned char*>(base);
+  uint32_t q = wave * kWave + lane;
+  uint32_t i = q / per;
+  uint32_t pp = q - i * per;
   for (uint32_t c = wave; c * kWave < pieces; c += kWaves) {
-    const uint32_t q = c * kWave + lane;
-    const uint32_t i = q < pieces ? q / per : 0u;
-    const uint32_t pp = q < pieces ? q % per : 0u;
-    burst_to_lds(src(i) + (pp < H / 8u ? pp : 0u) * 8u, area + c * kWave * 16u);
+    const uint32_t g = q < pieces ? __umul24(i, 2u * per) + pp : 0u;  // piece of the panel tile
+    burst_to_lds(b + g * 16u, area + c * kWave * 16u);
+    q += kStride;
+    i += kStride / per;
+    pp += kStride % per;
+    if (pp >= per) {
+      pp -= per;
+      ++i;
+    }
   }
 }
 
-// stage_rows for rows of z given by a slot -> row map in LDS, eight copies
-// per round: the eight map reads are issued together, then the eight
-// copies (a loop of single copies pays an LDS round trip per copy).
+// stage_rows for rows of z given by a slot -> byte offset map in LDS, eight
+// copies per round: the eight map reads are issued together, then the eight
+// copies (a loop of single copies pays an LDS round trip per copy).  Each
+// lane steps its slot and piece from one copy of its wave to the next (the
+// wave's copies are kWaves apart, kWaves kWave pieces), so a copy costs no
+// division and no 64-bit multiply.
 template <uint32_t H>
 __device__ __forceinline__ void stage_rows_batched(unsigned char* area, uint32_t n,
-                                                   const uint32_t* slot_row, const uint16_t* z) {
+                                                   const uint32_t* slot_off, const uint16_t* z) {
   constexpr uint32_t per = slot_bytes(H) / 16u;
   constexpr uint32_t kRound = 8;
+  constexpr uint32_t kStride = kWaves * kWave;
   const uint32_t lane = threadIdx.x % kWave;
-  const uint32_t wave = threadIdx.x / kWave;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const uint32_t pieces = n * per;
-  const uint32_t copies = (pieces + kWave - 1u) / kWave;  // over the workgroup
+  const uint32_t copies = (pieces + kWave - 1u) / kWave;
+  const unsigned char* zb = reinterpret_cast<const unsigned char*>(z);
+  uint32_t q = wave * kWave + lane;  // this lane's piece in the wave's next copy
+  uint32_t i = q / per;
+  uint32_t pp = q - i * per;
   for (uint32_t c0 = wave; c0 < copies; c0 += kWaves * kRound) {
-    uint32_t i[kRound];
-    uint32_t pp[kRound];
-    uint32_t rr[kRound];
+    uint32_t off[kRound];
+    uint32_t pq[kRound];
 #pragma unroll
     for (uint32_t u = 0; u < kRound; ++u) {
-      const uint32_t q = (c0 + u * kWaves) * kWave + lane;
-      i[u] = q < pieces ? q / per : 0u;
-      pp[u] = q < pieces ? q % per : 0u;
-      rr[u] = slot_row[i[u]];
+      const bool in = q < pieces;
+      off[u] = slot_off[in ? i : 0u];
+      pq[u] = in && pp < H / 8u ? pp : 0u;
+      q += kStride;
+      i += kStride / per;
+      pp += kStride % per;
+      if (pp >= per) {
+        pp -= per;
+        ++i;
+      }
     }
 #pragma unroll
     for (uint32_t u = 0; u < kRound; ++u) {
       const uint32_t c = c0 + u * kWaves;
-      if (c < copies) {
-        burst_to_lds(z + static_cast<uint64_t>(rr[u]) * H + (pp[u] < H / 8u ? pp[u] : 0u) * 8u,
-                     area + c * kWave * 16u);
-      }
+      if (c < copies) burst_to_lds(zb + off[u] + pq[u] * 16u, area + c * kWave * 16u);
     }
   }
 }
@@ -284,7 +307,7 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
   auto stage_panel = [&](uint32_t pt) {
     const uint16_t* base = f.panel + static_cast<uint64_t>(pt) * kTileHalves;
     const uint32_t n = f.m - pt * kPanelRows < kPanelRows ? f.m - pt * kPanelRows : kPanelRows;
-    stage_rows<H>(panel, n, [&](uint32_t j) { return base + j * kPanelSlotHalves; });
+    stage_panel_rows<H>(panel, n, base);
   };
   auto head_lds = [&](HeadAcc<kBlocks>& h) {
 #pragma unroll
@@ -426,7 +449,7 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
       if (tid >= r0 && tid < r1) {
         const uint32_t n = ps.count[tid];
         if (n > 0u) {
-          ps.slot_row[ps.rprefix[tid] - s0] = tid;
+          ps.slot_off[ps.rprefix[tid] - s0] = tid * (2u * H);
           // the row of each of its candidates (a row has at most one
           // tile's worth)
           const uint32_t base = ps.prefix[tid] - k0;
@@ -457,7 +480,7 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
         at[u] = nb > 0u ? ps.begin[row[u]] + (k0 + kk - ps.prefix[row[u]]) : 0u;
       }
       __builtin_amdgcn_sched_barrier(0);
-      stage_rows_batched<H>(stage, nz, ps.slot_row, p.z_hi);
+      stage_rows_batched<H>(stage, nz, ps.slot_off, p.z_hi);
       __builtin_amdgcn_sched_barrier(0);
       uint32_t tok[2];
 #pragma unroll
