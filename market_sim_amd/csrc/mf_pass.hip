@@ -30,8 +30,8 @@
 // loads is the schedule:
 //   1. the plan's per-row values, then the first half of the tile's first
 //      block of table rows (it streams while the plan is scanned);
-//   2. (plan landed) scans over the rows; the block's second half; each
-//      candidate's row, then the rows of z to stage (copies straight into
+//   2. (plan landed) scans over the rows; each candidate's row; the
+//      block's second half; the rows of z to stage (copies straight into
 //      LDS) and the candidate ids;
 //   3. (all landed) the second block's first half; buckets; its second
 //      half; block 0's token norms and candidates; the third block is
@@ -417,9 +417,6 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
       }
       __syncthreads();
     }
-    __builtin_amdgcn_sched_barrier(0);
-    load_steps(tile, 0, kFirstHalf, kSteps);
-    __builtin_amdgcn_sched_barrier(0);
     MF_STAMP(2);
 
     // (3) batches of whole rows.  The first is scored block by block as the
@@ -462,6 +459,13 @@ __global__ __launch_bounds__(kThreads) void pass_kernel(PassArgs p) {
         ps.row_flags[tid] = 0u;
       }
       __syncthreads();  // slot rows, candidate rows, cleared counters
+      if constexpr (first) {
+        // block 0's second half: its issue waits for the first half's loads
+        // to drain, which the batch set-up above no longer does
+        __builtin_amdgcn_sched_barrier(0);
+        load_steps(tile, 0, kFirstHalf, kSteps);
+        __builtin_amdgcn_sched_barrier(0);
+      }
       if constexpr (first) MF_STAMP(3);
       // the batch's rows of z straight into LDS (block 0 of the table rows
       // streams ahead of them), then its candidate ids (lanes past the
