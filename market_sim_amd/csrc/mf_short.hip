@@ -77,24 +77,45 @@ __device__ inline void stage_part(const TailNormArgs& n, const FinalizeArgs& f, 
   constexpr uint32_t kBatch = 24;
   const uint32_t per = H / 8u;
   const uint32_t total = cnt * per;
+  // piece q = q0 + u kWave of the staged rows is piece q % per of the
+  // part's candidate q / per: each lane steps (candidate, piece) by kWave
+  // pieces from one u to the next (one division per lane, not per piece)
+  const uint32_t step_c = kWave / per;
+  const uint32_t step_p = kWave % per;
+  uint32_t c0 = lane / per;  // the lane's first piece of a batch
+  uint32_t p0 = lane % per;
   for (uint32_t q0 = lane; q0 < total; q0 += kWave * kBatch) {
     uint4 v[kBatch];
+    uint32_t c = c0;
+    uint32_t pp = p0;
 #pragma unroll
     for (uint32_t u = 0; u < kBatch; ++u) {
       const uint32_t q = q0 + u * kWave;
-      const uint32_t j = part + parts * (q / per);
-      const uint32_t id = q < total ? sh.cand[j] : kInvalidToken;
-      v[u] = id < n.V ? reinterpret_cast<const uint4*>(f.emb + static_cast<uint64_t>(id) * H)[q % per]
+      const uint32_t id = q < total ? sh.cand[part + parts * c] : kInvalidToken;
+      v[u] = id < n.V ? reinterpret_cast<const uint4*>(f.emb + static_cast<uint64_t>(id) * H)[pp]
                       : uint4{0u, 0u, 0u, 0u};
-    }
-#pragma unroll
-    for (uint32_t u = 0; u < kBatch; ++u) {
-      const uint32_t q = q0 + u * kWave;
-      if (q < total) {
-        const uint32_t j = part + parts * (q / per);
-        reinterpret_cast<uint4*>(es + j * rs)[q % per] = v[u];
+      c += step_c;
+      pp += step_p;
+      if (pp >= per) {
+        pp -= per;
+        ++c;
       }
     }
+    c = c0;
+    pp = p0;
+#pragma unroll
+    for (uint32_t u = 0; u < kBatch; ++u) {
+      const uint32_t q = q0 + u * kWave;
+      if (q < total) reinterpret_cast<uint4*>(es + (part + parts * c) * rs)[pp] = v[u];
+      c += step_c;
+      pp += step_p;
+      if (pp >= per) {
+        pp -= per;
+        ++c;
+      }
+    }
+    c0 = c;
+    p0 = pp;
   }
 }
 
