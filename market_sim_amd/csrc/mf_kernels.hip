@@ -679,40 +679,6 @@ __global__ __launch_bounds__(kThreads) void restricted_greedy_kernel(
   }
 }
 
-// Upper bounds of the token norms ||e_t|| (FP32 sum of squares of the FP16
-// row, any order: within a relative H 2^-24; the factor covers it and the
-// square root).  Eight lanes per token row, 16 bytes per load; H % 8 == 0.
-__global__ __launch_bounds__(kThreads) void token_norm_kernel(const uint16_t* emb, uint32_t V,
-                                                             uint32_t H, float* out) {
-  const uint32_t sub = threadIdx.x % 8;
-  const uint64_t t = static_cast<uint64_t>(blockIdx.x) * (kThreads / 8) + threadIdx.x / 8;
-  float s = 0.0f;
-  if (t < V) {
-    const uint4* row = reinterpret_cast<const uint4*>(emb + t * H);
-    const uint32_t n = H / 8;
-    for (uint32_t base = sub; base < n; base += 8 * 4) {
-      uint4 v[4];
-#pragma unroll
-      for (uint32_t u = 0; u < 4; ++u) {
-        const uint32_t q = base + u * 8;
-        v[u] = q < n ? row[q] : uint4{0u, 0u, 0u, 0u};
-      }
-#pragma unroll
-      for (uint32_t u = 0; u < 4; ++u) {
-        const uint16_t* h = reinterpret_cast<const uint16_t*>(&v[u]);
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          const float e = half_to_float(h[k]);
-          s = __builtin_fmaf(e, e, s);
-        }
-      }
-    }
-  }
-#pragma unroll
-  for (int m = 4; m > 0; m >>= 1) s += __shfl_xor(s, m, 8);
-  if (t < V && sub == 0) out[t] = __fsqrt_rn(s) * (1.0f + 0x1p-7f);
-}
-
 __global__ __launch_bounds__(kThreads) void fill_zero_kernel(uint4* p, uint64_t n16) {
   for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n16;
        i += static_cast<uint64_t>(gridDim.x) * kThreads) {
@@ -831,14 +797,6 @@ hipError_t launch_restricted_greedy(const void* logits, bool half,
     hipLaunchKernelGGL((restricted_greedy_kernel<false>), dim3(rows), dim3(kThreads), 0,
                        stream, logits, allowed, counts, tokens, vocab, max_allowed);
   }
-  return hipGetLastError();
-}
-
-hipError_t launch_token_norms(const uint16_t* emb, uint32_t V, uint32_t H, float* out,
-                              hipStream_t stream) {
-  if (H % 8 != 0) return hipErrorInvalidValue;
-  const uint32_t blocks = (V + kThreads / 8 - 1) / (kThreads / 8);
-  hipLaunchKernelGGL(token_norm_kernel, dim3(blocks), dim3(kThreads), 0, stream, emb, V, H, out);
   return hipGetLastError();
 }
 

@@ -67,8 +67,6 @@ hipError_t launch_restricted_greedy(const void* logits, bool half,
                                     uint32_t rows, uint32_t vocab,
                                     uint32_t max_allowed, hipStream_t stream);
 
-hipError_t launch_token_norms(const uint16_t* emb, uint32_t V, uint32_t H, float* out,
-                              hipStream_t stream);
 hipError_t launch_fill_zero(void* address, uint64_t bytes, hipStream_t stream);
 hipError_t launch_read_floor(const void* address, uint64_t bytes, uint32_t* sink,
                              hipStream_t stream);
